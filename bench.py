@@ -1,0 +1,317 @@
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Workload (the headline): the five ternary linears of one BitNet-b1.58-2B-shaped decoder layer at M = 1 token
+(QKV 3840x2560, O 2560x2560, gate and up 6912x2560 with g128 scales, down 2560x6912 with g96 scales). One step =
+the four activation preps (WHT-128 + INT8) and the five int8-MFMA GEMVs of that layer, all inputs resident in
+HBM. Weights rotate over enough copies (> 2x the 256 MB Infinity Cache) that every step streams from HBM.
+
+value = algorithmic bytes of a step / step time (GB/s). The roofline object covers the dominant kernel, the
+ternary GEMV: its algorithmic bytes per launch / its average launch duration, timed with HIP events on the stream
+the kernels run on. cpu_baseline times the reference's own x86 path for the same layer (WHT + the FP32-activation
+grouped GEMV that its engine runs), compiled from its sources into oracle/_ref, on the host cores.
+
+Extra keys report the other workloads: the single 6912x2560 linear, token batches 8/64/512, the INT4 tied head,
+the INT8 layer, and a measured device-to-device copy ceiling.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "bitllm.c_amd"))
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the current (launch) stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def __call__(self, fn, reps):
+        t = self.torch
+        s = t.cuda.current_stream()
+        a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        t.cuda.synchronize()
+        a.record(s)
+        for i in range(reps):
+            fn(i)
+        b.record(s)
+        b.synchronize()
+        return a.elapsed_time(b) / reps * 1e-3  # seconds per call
+
+
+def copies_for(nbytes):
+    return max(3, -(-2 * MALL_BYTES // nbytes) + 1)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported (the path shards by output rows, "
+              f"see the design notes, but no multi-GPU run exists)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import bitllm_hip as bh
+    import synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    lib = bh.load()
+    bh.check(lib.eif_hip_init(0), "eif_hip_init")
+    dev = torch.device("cuda:0")
+    timer = Timer(torch)
+
+    # ---------------- headline: BitNet-2B layer, M = 1 ----------------
+    layer = synth.BITNET_2B_LAYER
+    layer_w_bytes = sum(synth.ternary_linear_bytes(N, K, g, 0) for _, N, K, g in layer)
+    ncopy = copies_for(layer_w_bytes)
+    base = {name: synth.ternary_weight((100, i), N, K, g) for i, (name, N, K, g) in enumerate(layer)}
+    copies = []
+    for c in range(ncopy):
+        copies.append({name: bh.QWeight(bh.W_TERNARY, N, K, g, *base[name]) for name, N, K, g in layer})
+    shapes = {name: (N, K, g) for name, N, K, g in layer}
+
+    M = 1
+    x_in = {K: torch.from_numpy(synth.activations((101, K), M, K)).to(dev) for K in (2560, 6912)}
+    kp = {K: (K + 255) // 256 * 256 for K in (2560, 6912)}
+    xq = {K: torch.zeros((M, kp[K]), dtype=torch.int8, device=dev) for K in (2560, 6912)}
+    xs = {K: torch.zeros(M, dtype=torch.float32, device=dev) for K in (2560, 6912)}
+    y = {name: torch.zeros((M, N), dtype=torch.float32, device=dev) for name, N, K, g in layer}
+    norm = bh.wht_norm(128)
+
+    def prep(K):
+        bh.prep_rows(x_in[K], xq[K], xs[K], 128, norm)
+
+    def layer_step(i):
+        w = copies[i % ncopy]
+        prep(2560)                                   # input norm -> QKV
+        w["qkv"].linear(xq[2560], xs[2560], y["qkv"], path=bh.PATH_GEMV)
+        prep(2560)                                   # attention output -> O
+        w["o"].linear(xq[2560], xs[2560], y["o"], path=bh.PATH_GEMV)
+        prep(2560)                                   # post-attention norm -> gate, up
+        w["gate"].linear(xq[2560], xs[2560], y["gate"], path=bh.PATH_GEMV)
+        w["up"].linear(xq[2560], xs[2560], y["up"], path=bh.PATH_GEMV)
+        prep(6912)                                   # SwiGLU output -> down
+        w["down"].linear(xq[6912], xs[6912], y["down"], path=bh.PATH_GEMV)
+
+    prep_bytes = 3 * (2560 * 4 + 2560 + 4) + (6912 * 4 + 6912 + 4)
+    gemv_bytes = sum(synth.ternary_linear_bytes(N, K, g, M) for _, N, K, g in layer)
+    step_bytes = prep_bytes + gemv_bytes
+
+    for i in range(args.warmup):
+        layer_step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sec = timer(layer_step, args.steps)
+    wall = time.perf_counter() - t0
+    value = step_bytes / sec / 1e9
+
+    # dominant kernel: ternary GEMV, per-linear launch duration over back-to-back launches (rotating weights)
+    prep(2560)
+    prep(6912)
+    reps = max(50, args.steps)
+    per_linear = {}
+    for name, (N, K, g) in shapes.items():
+        fn = lambda i, name=name, K=K: copies[i % ncopy][name].linear(xq[K], xs[K], y[name], path=bh.PATH_GEMV)
+        for i in range(10):
+            fn(i)
+        t = timer(fn, reps)
+        per_linear[name] = {"us": t * 1e6, "GBps": synth.ternary_linear_bytes(N, K, g, M) / t / 1e9}
+    gemv_time = sum(v["us"] for v in per_linear.values()) * 1e-6
+    gemv_gbs = gemv_bytes / gemv_time / 1e9
+    prep_t = timer(lambda i: prep(2560), reps)
+
+    out = {
+        "metric": "BitNet-2B-shape layer ternary hot path (WHT+INT8 prep + GEMV), M=1, HBM GB/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x ternary -> int32 acc, fp32 scale",
+        "data": "synthetic (seeded; random-init weights of the BitNet-b1.58-2B layer shapes)",
+        "config": {"workload": "bitnet2b_layer_linears_m1", "tokens": M, "hidden": 2560, "ffn": 6912,
+                   "qkv_rows": 3840, "groups": "g128 (qkv/o/gate/up), g96 (down)", "wht_block": 128,
+                   "weight_copies": ncopy, "step_bytes": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qlinear_kernel (ternary GEMV, the 5 layer linears)",
+                     "per_launch": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)}
+                                    for k, v in per_linear.items()}},
+        "prep_us": round(prep_t * 1e6, 3),
+        "wall_s_timed": round(wall, 3),
+    }
+
+    if not args.no_extra:
+        out["extra"] = extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in, norm)
+
+    for cs in copies:
+        for w in cs.values():
+            w.close()
+
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args, np, synth, step_bytes)
+        if out["cpu_baseline"].get("value"):
+            out["gpu_over_cpu"] = round(value / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out))
+
+
+def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in, norm):
+    ex = {}
+    reps = max(50, args.steps // 2)
+    ncopy = len(copies)
+    # single 6912x2560 g128 linear (the gate projection), M = 1
+    t = timer(lambda i: copies[i % ncopy]["gate"].linear(xq[2560], xs[2560], y["gate"], path=bh.PATH_GEMV), reps)
+    b = synth.ternary_linear_bytes(6912, 2560, 128, 1)
+    ex["ternary_6912x2560_g128_m1"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1)}
+
+    # token batches through the layer linears (GEMV for M = 8, MFMA GEMM for M >= 64)
+    for M in (8, 64, 512):
+        xm = {K: torch.from_numpy(synth.activations((102, K, M), M, K)).to(dev) for K in (2560, 6912)}
+        qm = {K: torch.zeros((M, (K + 255) // 256 * 256), dtype=torch.int8, device=dev) for K in (2560, 6912)}
+        sm = {K: torch.zeros(M, dtype=torch.float32, device=dev) for K in (2560, 6912)}
+        for K in (2560, 6912):
+            bh.prep_rows(xm[K], qm[K], sm[K], 128, norm)
+        ym = {name: torch.zeros((M, w.rows), dtype=torch.float32, device=dev) for name, w in copies[0].items()}
+
+        def lin(i):
+            w = copies[i % ncopy]
+            for name, q in w.items():
+                K = q.cols
+                q.linear(qm[K], sm[K], ym[name])
+        t = timer(lin, max(20, reps // 4))
+        nbytes = sum(synth.ternary_linear_bytes(q.rows, q.cols, q.group, M) for q in copies[0].values())
+        ops = sum(2 * q.rows * q.cols * M for q in copies[0].values())
+        ex[f"bitnet2b_layer_linears_m{M}"] = {"us": round(t * 1e6, 2), "GBps": round(nbytes / t / 1e9, 1),
+                                              "TOPS": round(ops / t / 1e12, 2),
+                                              "path": "gemm" if M >= bh.load().eif_hip_gemm_min_tokens() else "gemv"}
+        del xm, qm, sm, ym
+
+    # INT4 tied head 151936x1024 (M = 1 and 32) and INT4 FFN linears
+    N, K = synth.QWEN35_INT4_HEAD[1:]
+    hw, hs = synth.int4_weight((103,), N, K)
+    nb = synth.int_linear_bytes(N, K, 4, 1)
+    heads = [bh.QWeight(bh.W_INT4, N, K, 0, hw, hs) for _ in range(copies_for(nb))]
+    for M in (1, 32):
+        xh = torch.from_numpy(synth.activations((104, M), M, K)).to(dev)
+        qh = torch.zeros((M, heads[0].kpad), dtype=torch.int8, device=dev)
+        sh = torch.zeros(M, dtype=torch.float32, device=dev)
+        bh.prep_rows(xh, qh, sh, 0, 1.0)
+        yh = torch.zeros((M, N), dtype=torch.float32, device=dev)
+        t = timer(lambda i: heads[i % len(heads)].linear(qh, sh, yh), max(20, reps // 2))
+        b = synth.int_linear_bytes(N, K, 4, M)
+        ex[f"int4_head_151936x1024_m{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                                              "frac_hbm": round(b / t / 1e9 / HBM_PEAK_GBS, 4)}
+    for h in heads:
+        h.close()
+
+    # INT8 Qwen2.5-0.5B-like layer, M = 1 and 128
+    l8 = synth.QWEN25_05B_LAYER
+    base8 = {name: synth.int8_weight((105, i), N, K) for i, (name, N, K) in enumerate(l8)}
+    wb8 = sum(synth.int_linear_bytes(N, K, 8, 0) for _, N, K in l8)
+    c8 = [{name: bh.QWeight(bh.W_INT8, N, K, 0, *base8[name]) for name, N, K in l8} for _ in range(copies_for(wb8))]
+    for M in (1, 128):
+        xk = {K: torch.from_numpy(synth.activations((106, K, M), M, K)).to(dev) for K in (896, 4864)}
+        qk = {K: torch.zeros((M, (K + 63) // 64 * 64), dtype=torch.int8, device=dev) for K in (896, 4864)}
+        sk = {K: torch.zeros(M, dtype=torch.float32, device=dev) for K in (896, 4864)}
+        for K in (896, 4864):
+            bh.prep_rows(xk[K], qk[K], sk[K], 0, 1.0)
+        yk = {name: torch.zeros((M, N), dtype=torch.float32, device=dev) for name, N, K in l8}
+
+        def lin8(i):
+            for name, q in c8[i % len(c8)].items():
+                q.linear(qk[q.cols], sk[q.cols], yk[name])
+        t = timer(lin8, max(20, reps // 4))
+        b = sum(synth.int_linear_bytes(N, K, 8, M) for _, N, K in l8)
+        ex[f"int8_qwen05b_layer_m{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1)}
+    for cs in c8:
+        for q in cs.values():
+            q.close()
+
+    # measured copy ceiling: 1 GiB device-to-device copy (read + write bytes)
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    t = timer(lambda i: dst.copy_(src), 10)
+    ex["d2d_copy_GBps"] = round(2 * src.numel() * 4 / t / 1e9, 1)
+    del src, dst
+    return ex
+
+
+def cpu_baseline(args, np, synth, step_bytes):
+    """The reference's own x86 path for the same layer step, on the host cores, over a bounded sample."""
+    nthreads = min(16, os.cpu_count() or 1)
+    os.environ.setdefault("OMP_NUM_THREADS", str(nthreads))
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_WAIT_POLICY", "ACTIVE")
+    os.environ.setdefault("GOMP_SPINCOUNT", "100000")
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ctypes as C
+    import oracle_api
+    P = oracle_api.P
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+    port_so = os.path.join(ROOT, "oracle", "liboracle_port.so")
+    if os.path.exists(ref_so):
+        lib, kind = oracle_api.load_ref(ref_so), "reference"
+        rot = lambda x, n: lib.eif_hadamard_rotate_f32(P(x), None, n, 128)
+        gemv = lambda w, s, g, x, yv, N, K: lib.eif_matmul_bitnet_block_f32(P(w), P(s), g, P(x), None, P(yv), N, K)
+    elif os.path.exists(port_so):
+        lib, kind = oracle_api.load(port_so), "port"
+        nrm = lib.orc_wht_norm_fastmath(128)
+        rot = lambda x, n: lib.orc_hadamard_rotate(P(x), None, n, 128, C.c_float(nrm))
+        gemv = lambda w, s, g, x, yv, N, K: lib.orc_matmul_bitnet_block_f32(P(w), P(s), g, P(x), None, P(yv), N, K)
+    else:
+        return {"value": None, "unit": "GB/s", "cores": 0, "kind": "none", "sample": "no CPU library built"}
+    layer = synth.BITNET_2B_LAYER
+    ncp = 6  # ~120 MB of weights, past the host's last-level cache
+    ws = [{name: synth.ternary_weight((100, i), N, K, g) for i, (name, N, K, g) in enumerate(layer)}]
+    for c in range(1, ncp):
+        ws.append({k: (v[0].copy(), v[1].copy()) for k, v in ws[0].items()})
+    x0 = {K: synth.activations((101, K), 1, K)[0] for K in (2560, 6912)}
+    yv = {name: np.zeros(N, np.float32) for name, N, K, g in layer}
+
+    def step(i):
+        w = ws[i % ncp]
+        for name, N, K, g in layer:
+            if name in ("qkv", "o", "gate", "down"):
+                x = x0[K].copy()
+                rot(x, K)
+            gemv(w[name][0], w[name][1], g, x, yv[name], N, K)
+
+    step(0)
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    i = 1
+    while time.perf_counter() < t_end or len(times) < 5:
+        t0 = time.perf_counter()
+        step(i)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    med = float(np.median(times))
+    return {"value": round(step_bytes / med / 1e9, 2), "unit": "GB/s", "cores": nthreads, "kind": kind,
+            "ms_per_step": round(med * 1e3, 3),
+            "sample": f"{len(times)} layer steps (WHT-128 + FP32-activation grouped GEMV, the reference x86 path) "
+                      f"over {ncp} weight copies, median; OMP_NUM_THREADS={os.environ['OMP_NUM_THREADS']}"}
+
+
+if __name__ == "__main__":
+    main()

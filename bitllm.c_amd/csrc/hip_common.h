@@ -1,0 +1,70 @@
+// hip_common.h -- shared helpers of libbitllm_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/eif_hip.h"
+
+#define EIF_DEV __device__ __forceinline__
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Return-code plumbing for the C ABI: every HIP call is checked, a failure maps to EIF_HIP_E_DEVICE.
+#define EIF_HIP_TRY(expr)                                                                                      \
+    do {                                                                                                       \
+        hipError_t e__ = (expr);                                                                               \
+        if (e__ != hipSuccess) {                                                                               \
+            fprintf(stderr, "libbitllm_hip: %s failed: %s (%s:%d)\n", #expr, hipGetErrorString(e__), __FILE__, \
+                    __LINE__);                                                                                 \
+            return EIF_HIP_E_DEVICE;                                                                           \
+        }                                                                                                      \
+    } while (0)
+
+// Checks the launch that was just enqueued (configuration errors surface here, not at execution).
+#define EIF_HIP_LAUNCHED() EIF_HIP_TRY(hipGetLastError())
+
+static inline int eif_ceil_div(int a, int b) { return (a + b - 1) / b; }
+static inline int eif_round_up(int a, int b) { return eif_ceil_div(a, b) * b; }
+
+// Device-side wave64 reductions (xor butterflies; exact for max and for integers).
+EIF_DEV float eif_wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+EIF_DEV float eif_wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Internal launchers shared between translation units (defined in the .hip files).
+namespace eif {
+int launch_prep_rows(const float *x, int ldx, const float *signs, int M, int K, int wht_block, float norm,
+                     int8_t *xq, int ldq, float *xs, float *xrot, int ldr, hipStream_t st);
+int launch_rotate_rows(float *x, int ldx, const float *signs, int M, int K, int wht_block, float norm,
+                       hipStream_t st);
+int launch_quant_rows(const float *x, int ldx, int M, int K, int8_t *xq, int ldq, float *xs, hipStream_t st);
+
+int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *xq, int ldq, const float *xs,
+                   const float *bias, float *y, int ldy, int M, int path, hipStream_t st);
+
+int launch_tern_f32(const uint8_t *W, const float *scales, int mode, int block, const float *x, const float *bias,
+                    float *y, int rows, int cols, int il, hipStream_t st);
+int launch_dense_f32(const uint8_t *W, const float *scales, const float *x, const float *bias, float *y, int rows,
+                     int cols, hipStream_t st);
+int launch_int8_f32(const int8_t *W, const float *scales, const float *x, float *y, int rows, int cols,
+                    hipStream_t st);
+int launch_int4_f32(const uint8_t *W, const float *scales, const float *x, float *y, int rows, int cols,
+                    hipStream_t st);
+int launch_tern_int8_out(const uint8_t *W, const int8_t *x, const int32_t *bias, int8_t *y, float eff, int rows,
+                         int cols, hipStream_t st);
+int launch_gemm_f32_nt(const float *A, int lda, const float *W, int ldw, const float *bias, float *C, int ldc, int M,
+                       int N, int K, int act, int accumulate, hipStream_t st);
+int launch_softmax_rows(float *S, int rows, int cols, int ld, float scale, hipStream_t st);
+}  // namespace eif

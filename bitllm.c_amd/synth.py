@@ -1,0 +1,115 @@
+"""Seeded synthetic inputs of the benchmark workloads, in the reference's storage formats.
+
+Every tensor draws from its own numpy PCG64 stream keyed by (workload id, tensor id, copy), so the CPU baseline,
+the GPU runs and the parity tests see identical bytes on any machine.
+
+Formats (reference):
+  ternary  2-bit codes, column c in byte c>>2 at bits 2*(c&3); 01 = +1, 10 = -1   include/eif_quantize_bitnet.h:4-11
+  int8     row-major int8                                                     src/eif_tinyllm.c:1651-1721
+  int4     (cols+1)/2 bytes per row, even column in the high nibble, v = n-8   src/eif_qwen35_gguf.c:249-253
+Distributions: ternary codes uniform over {-1, 0, +1}; group scales |N(0,1)|*0.02; row scales |N(0,1)|*0.01;
+activations N(0,1) float32 with exactly floor(0.01*K) distinct entries per row multiplied by 20; int8 codes
+uniform in [-127, 127]; int4 codes uniform in [-8, 7].
+"""
+import numpy as np
+
+
+def rng(*key):
+    return np.random.Generator(np.random.PCG64(np.random.SeedSequence([0xB17, *[int(k) for k in key]])))
+
+
+def pack_ternary(v):
+    """int8 values in {-1,0,1}, shape [..., K] -> uint8 [..., (K+3)//4] in the reference 2-bit format."""
+    v = np.asarray(v)
+    K = v.shape[-1]
+    Kp = (K + 3) // 4 * 4
+    codes = np.zeros(v.shape[:-1] + (Kp,), np.uint8)
+    codes[..., :K] = np.where(v > 0, 1, np.where(v < 0, 2, 0))
+    c = codes.reshape(v.shape[:-1] + (Kp // 4, 4))
+    return (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).astype(np.uint8)
+
+
+def unpack_ternary(packed, K):
+    p = np.asarray(packed, np.uint8)
+    codes = np.stack([(p >> (2 * i)) & 3 for i in range(4)], axis=-1).reshape(p.shape[:-1] + (-1,))[..., :K]
+    return np.where(codes == 1, 1, np.where(codes == 2, -1, 0)).astype(np.int8)
+
+
+def pack_int4(v):
+    """int values in [-8,7], shape [..., K] -> uint8 [..., (K+1)//2], even column in the high nibble."""
+    v = np.asarray(v)
+    K = v.shape[-1]
+    Kp = (K + 1) // 2 * 2
+    n = np.full(v.shape[:-1] + (Kp,), 8, np.uint8)
+    n[..., :K] = (v + 8).astype(np.uint8)
+    return ((n[..., 0::2] << 4) | n[..., 1::2]).astype(np.uint8)
+
+
+def unpack_int4(packed, K):
+    p = np.asarray(packed, np.uint8).astype(np.int16)
+    v = np.stack([(p >> 4) - 8, (p & 15) - 8], axis=-1).reshape(p.shape[:-1] + (-1,))[..., :K]
+    return v.astype(np.int8)
+
+
+def ternary_weight(key, N, K, group):
+    """(packed [N,(K+3)//4] uint8, scales) with group scales [N, ceil(K/group)] or row scales [N]."""
+    r = rng(*key, 1)
+    codes = r.integers(-1, 2, size=(N, K), dtype=np.int8)
+    ns = N * ((K + group - 1) // group) if group > 0 else N
+    scales = (np.abs(rng(*key, 2).standard_normal(ns)) * 0.02).astype(np.float32)
+    return pack_ternary(codes), scales.reshape(N, -1) if group > 0 else scales
+
+
+def int8_weight(key, N, K):
+    w = rng(*key, 1).integers(-127, 128, size=(N, K), dtype=np.int8)
+    scales = (np.abs(rng(*key, 2).standard_normal(N)) * 0.01).astype(np.float32)
+    return w, scales
+
+
+def int4_weight(key, N, K):
+    v = rng(*key, 1).integers(-8, 8, size=(N, K), dtype=np.int8)
+    scales = (np.abs(rng(*key, 2).standard_normal(N)) * 0.01).astype(np.float32)
+    return pack_int4(v), scales
+
+
+def activations(key, M, K, outliers=True):
+    r = rng(*key, 3)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    if outliers:
+        n = int(0.01 * K)
+        for m in range(M):
+            idx = r.choice(K, size=n, replace=False)
+            x[m, idx] *= np.float32(20.0)
+    return x
+
+
+# Decoder layer of a BitNet-b1.58-2B-shaped model: hidden 2560, 20 query / 5 KV heads of dim 128, FFN 6912.
+BITNET_2B_LAYER = [
+    # name, rows (N), cols (K), group
+    ("qkv", 3840, 2560, 128),
+    ("o", 2560, 2560, 128),
+    ("gate", 6912, 2560, 128),
+    ("up", 6912, 2560, 128),
+    ("down", 2560, 6912, 96),
+]
+
+# Qwen2.5-0.5B-like layer: hidden 896, 14 query / 2 KV heads of dim 64, FFN 4864 (INT8 weights).
+QWEN25_05B_LAYER = [
+    ("q", 896, 896), ("k", 128, 896), ("v", 128, 896), ("o", 896, 896),
+    ("gate", 4864, 896), ("up", 4864, 896), ("down", 896, 4864),
+]
+
+# Qwen3.5-style INT4 layer linears and the tied vocab head.
+QWEN35_INT4_LAYER = [("gate", 3584, 1024), ("up", 3584, 1024), ("down", 1024, 3584)]
+QWEN35_INT4_HEAD = ("head", 151936, 1024)
+
+
+def ternary_linear_bytes(N, K, group, M):
+    """Algorithmic bytes of one int8-activation ternary linear: codes + fp32 scales + xq and its fp32 scale in
+    + fp32 y out."""
+    ns = N * ((K + group - 1) // group) if group > 0 else N
+    return N * ((K + 3) // 4) + 4 * ns + M * (K + 4) + 4 * M * N
+
+
+def int_linear_bytes(N, K, bits, M):
+    return N * ((K * bits + 7) // 8) + 4 * N + M * (K + 4) + 4 * M * N

@@ -1,0 +1,108 @@
+/*
+ * eif_hip.h -- device-pointer core of libbitllm_hip.so (gfx950 / MI355X).
+ *
+ * The host-pointer symbols of eif_quantize_bitnet.h, eif_gemm.h and eif_quant_linear.h wrap this layer. It has
+ * no counterpart in the reference: it is the seam for callers whose activations stay in HBM (the
+ * decode loop that replaces src/eif_tinyllm.c:371-857 and the qwen35 prefill that replaces
+ * src/eif_qwen35.c:1034-1065). All pointers are DEVICE pointers; `stream` is a hipStream_t (NULL = the null
+ * stream); every call is asynchronous on that stream and returns 0 or a negative EIF_HIP_E_* code.
+ *
+ * Integer contract (bit-exact with the CPU oracle):
+ *   prep:   v = x*signs (if signs), butterflies h = 1,2,..,block/2 (a+b, a-b), v *= norm; amax = max|v|;
+ *           amax < 1e-12 -> q = 0, xs = 1; else xs = amax*(1/127), q = trunc(v*(127/amax) +- 0.5) in [-128,127]
+ *           (src/eif_quantize_bitnet.c:1032-1060, :1646-1677).
+ *   linear: per (token m, row r, group g) acc = sum_{c in g} w[r,c]*xq[m,c] in int32 (exact);
+ *           grouped ternary:  y = xs[m] * sum_g s[r,g]*(float)acc_g (+ bias[r])   (FP32, rel. 1e-5)
+ *           row-scaled:       isum = sum_g acc_g; y = ((float)isum * xs[m]) * s[r] (+ bias[r]), the order the
+ *                             reference build evaluates src/eif_quantize_bitnet.c:1199-1200 in.
+ */
+#ifndef EIF_HIP_H
+#define EIF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    EIF_HIP_OK = 0,
+    EIF_HIP_E_ARG = -1,     /* invalid size, pointer or combination */
+    EIF_HIP_E_DEVICE = -2,  /* no usable gfx950 device / HIP runtime error */
+    EIF_HIP_E_NOMEM = -3,   /* device allocation failed */
+    EIF_HIP_E_LIMIT = -4    /* request beyond a documented maximum */
+};
+
+/* Weight formats of eif_hip_qweight_create. */
+enum {
+    EIF_HIP_W_TERNARY = 1, /* 2-bit codes, reference layout rows of (cols+3)/4 bytes */
+    EIF_HIP_W_INT8 = 2,    /* int8 [rows, cols] row-major */
+    EIF_HIP_W_INT4 = 3     /* 4-bit, reference layout rows of (cols+1)/2 bytes, even col = high nibble, v = n-8 */
+};
+
+/* Paths of eif_hip_qlinear_ex. */
+enum { EIF_HIP_PATH_AUTO = 0, EIF_HIP_PATH_GEMV = 1, EIF_HIP_PATH_GEMM = 2 };
+
+typedef struct eif_hip_qweight eif_hip_qweight;
+
+/* Select device `device` for this thread and check it is gfx950. */
+int eif_hip_init(int device);
+
+/* Human-readable text of a return code. */
+const char *eif_hip_strerror(int code);
+
+/* The per-element WHT scale the reference build uses for `block`: on x86 the value its -O3 -ffast-math code
+ * computes for 1.0f/sqrtf(block) (rsqrtss + one Newton step), elsewhere the correctly rounded value.
+ * ref: src/eif_quantize_bitnet.c:1554, CMakeLists.txt:19 */
+float eif_hip_wht_norm(int block);
+
+/* Correctly rounded 1/sqrt(block) in float. */
+float eif_hip_wht_norm_exact(int block);
+
+/* Activation prep for M rows of K floats (row stride ldx): optional sign flip + blockwise WHT (wht_block = 0:
+ * no rotation; else a power of two dividing K) + per-row absmax INT8. Writes xq [M, ldq] (ldq >= K, the bytes
+ * [K, ldq) are zeroed), xs [M], and, if xrot != NULL, the rotated FP32 rows [M, ldr]. xq/xs may be NULL to
+ * rotate only. K <= 12288 runs as one fused kernel; larger K needs xrot.                               */
+int eif_hip_prep_rows(const float *x, int ldx, const float *signs, int M, int K, int wht_block, float norm,
+                      int8_t *xq, int ldq, float *xs, float *xrot, int ldr, void *stream);
+
+/* Upload/repack a weight matrix into the GPU layout (kept in HBM until eif_hip_qweight_destroy).
+ *   codes, scales: host pointers (src_on_device = 0) or device pointers (src_on_device = 1);
+ *   EIF_HIP_W_TERNARY: group > 0 (multiple of 32) -> scales [rows, ceil(cols/group)];
+ *                      group == 0 -> row scales [rows] (NULL = 1);
+ *   EIF_HIP_W_INT8/INT4: group must be 0, row scales [rows] (NULL = 1).
+ * Synchronous (returns after the copy and repack completed).                                            */
+int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, int group, const void *codes,
+                           const float *scales, int src_on_device, void *stream);
+void eif_hip_qweight_destroy(eif_hip_qweight *w);
+
+/* Shape of a weight: rows, cols, padded cols (the minimum ldq for activations), group, and device bytes. */
+int eif_hip_qweight_info(const eif_hip_qweight *w, int *rows, int *cols, int *kpad, int *group, size_t *bytes);
+
+/* y[m, r] for m < M, r < rows (row stride ldy), activations xq [M, ldq] (ldq >= kpad, multiple of 16) with
+ * per-row scales xs [M]; bias [rows] or NULL. Auto path: GEMV for M < eif_hip_gemm_min_tokens(), else the
+ * int8-MFMA GEMM.                                                                                      */
+int eif_hip_qlinear(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, const float *bias,
+                    float *y, int ldy, int M, void *stream);
+int eif_hip_qlinear_ex(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, const float *bias,
+                       float *y, int ldy, int M, int path, void *stream);
+
+/* Exact int32 accumulators of the same kernels: grouped ternary -> acc [M, rows, ngroups]; row-scaled -> acc
+ * [M, rows]. For parity tests.                                                                          */
+int eif_hip_qlinear_acc(const eif_hip_qweight *w, const int8_t *xq, int ldq, int32_t *acc, int M, int path,
+                        void *stream);
+
+/* Drop the device copies the host-pointer ABI keeps for the weight buffer at host_ptr (NULL: all of them).
+ * Call it after rewriting a weight buffer in place or before freeing it.                                 */
+void eif_hip_forget_host_weights(const void *host_ptr);
+
+/* Token count from which the auto path uses the MFMA GEMM (default 16); returns the previous value.     */
+int eif_hip_set_gemm_min_tokens(int m);
+int eif_hip_gemm_min_tokens(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EIF_HIP_H */

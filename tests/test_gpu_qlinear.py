@@ -1,0 +1,171 @@
+"""INT8-activation linears (MFMA GEMV and GEMM paths) against the oracle.
+
+Integer accumulators are compared bit for bit; row-scaled outputs bit for bit (same epilogue order as the
+reference build); group-scaled FP32 outputs to 1e-5 relative to sum_g |s*acc_g|*xs + |bias| (the group partial
+sums are combined in a different order on the GPU).
+"""
+import numpy as np
+import pytest
+
+from conftest import P
+import synth
+
+pytestmark = pytest.mark.gpu
+
+GEMV, GEMM = 1, 2
+REL_TOL = 1e-5
+
+
+def dev_inputs(gpu, oracle, x, kpad):
+    import torch
+    M, K = x.shape
+    dev = torch.device("cuda:0")
+    xq = np.zeros((M, kpad), np.int8)
+    xs = np.zeros(M, np.float32)
+    assert oracle.orc_prep_rows(P(x), K, None, M, K, 0, 1.0, P(xq), kpad, P(xs), None, 0) == 0
+    return xq, xs, torch.from_numpy(xq).to(dev), torch.from_numpy(xs).to(dev)
+
+
+def run_linear(gpu, qw, xq_d, xs_d, M, path, bias=None):
+    import torch
+    y = torch.full((M, qw.rows), float("nan"), dtype=torch.float32, device="cuda:0")
+    b = torch.from_numpy(bias).to("cuda:0") if bias is not None else None
+    qw.linear(xq_d, xs_d, y, M=M, bias=b, path=path)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def run_acc(gpu, qw, xq_d, M, shape, path):
+    import torch
+    acc = torch.full(shape, -7, dtype=torch.int32, device="cuda:0")
+    qw.acc(xq_d, acc, M=M, path=path)
+    torch.cuda.synchronize()
+    return acc.cpu().numpy()
+
+
+TERN_GROUPED = [
+    # N, K, g, M, path
+    (6912, 2560, 128, 1, GEMV),     # the single BitNet linear
+    (2560, 6912, 96, 1, GEMV),      # down projection, g96
+    (3840, 2560, 128, 8, GEMV),
+    (130, 200, 32, 3, GEMV),        # ragged rows and columns
+    (70, 640, 64, 5, GEMV),
+    (64, 512, 256, 2, GEMV),
+    (70, 640, 64, 17, GEMM),
+    (6912, 2560, 128, 64, GEMM),
+    (2560, 6912, 96, 64, GEMM),
+    (300, 2560, 128, 200, GEMM),
+    (17, 96, 96, 1, GEMM),
+]
+
+
+@pytest.mark.parametrize("N,K,g,M,path", TERN_GROUPED)
+def test_ternary_grouped(gpu, oracle, N, K, g, M, path):
+    w, s = synth.ternary_weight((40, N, K, g), N, K, g)
+    x = synth.activations((41, M, K), M, K)
+    qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    ng = -(-K // g)
+    acc = run_acc(gpu, qw, xq_d, M, (M, N, ng), path)
+    oacc = np.zeros((M, N, ng), np.int32)
+    oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+    assert np.array_equal(acc, oacc)
+    bias = synth.rng(42, N).standard_normal(N).astype(np.float32) if M % 2 else None
+    y = run_linear(gpu, qw, xq_d, xs_d, M, path, bias)
+    oy = np.zeros((M, N), np.float32)
+    oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+    mag = np.einsum("mng,ng->mn", np.abs(oacc).astype(np.float64), s.astype(np.float64)) * xs[:, None]
+    if bias is not None:
+        mag = mag + np.abs(bias)[None, :]
+    err = np.abs(y.astype(np.float64) - oy) / (mag + 1e-30)
+    assert np.all(np.isfinite(y)) and err.max() <= REL_TOL, err.max()
+    qw.close()
+
+
+@pytest.mark.parametrize("N,K,M,path,with_bias", [
+    (6912, 2560, 1, GEMV, False), (2560, 6912, 1, GEMV, True), (100, 300, 7, GEMV, True),
+    (333, 1000, 70, GEMM, False), (64, 2560, 16, GEMM, True),
+])
+def test_ternary_rowscale_bit_exact(gpu, oracle, N, K, M, path, with_bias):
+    w, s = synth.ternary_weight((43, N, K), N, K, 0)
+    x = synth.activations((44, M, K), M, K)
+    qw = gpu.QWeight(gpu.W_TERNARY, N, K, 0, w, s)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    acc = run_acc(gpu, qw, xq_d, M, (M, N), path)
+    codes = synth.unpack_ternary(w, K)
+    assert np.array_equal(acc, xq[:, :K].astype(np.int64) @ codes.astype(np.int64).T)
+    bias = synth.rng(45, N).standard_normal(N).astype(np.float32) if with_bias else None
+    y = run_linear(gpu, qw, xq_d, xs_d, M, path, bias)
+    oy = np.zeros((M, N), np.float32)
+    oracle.orc_ternary_gemv_rowscale(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+    assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
+    qw.close()
+
+
+@pytest.mark.parametrize("fmt,N,K,M,path", [
+    ("int8", 4864, 896, 1, GEMV), ("int8", 896, 4864, 1, GEMV), ("int8", 128, 896, 3, GEMV),
+    ("int8", 4864, 896, 128, GEMM), ("int8", 77, 100, 20, GEMM),
+    ("int4", 3584, 1024, 1, GEMV), ("int4", 1024, 3584, 1, GEMV), ("int4", 3584, 1024, 32, GEMM),
+    ("int4", 50, 333, 4, GEMV), ("int4", 50, 333, 40, GEMM),
+])
+def test_int_rowscale_bit_exact(gpu, oracle, fmt, N, K, M, path):
+    if fmt == "int8":
+        w, s = synth.int8_weight((46, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+        vals = w
+    else:
+        w, s = synth.int4_weight((47, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+        vals = synth.unpack_int4(w, K)
+    x = synth.activations((48, M, K), M, K)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    acc = run_acc(gpu, qw, xq_d, M, (M, N), path)
+    assert np.array_equal(acc, xq[:, :K].astype(np.int64) @ vals.astype(np.int64).T)
+    y = run_linear(gpu, qw, xq_d, xs_d, M, path)
+    oy = np.zeros((M, N), np.float32)
+    fn = oracle.orc_int8_gemv_i8act if fmt == "int8" else oracle.orc_int4_gemv_i8act
+    fn(P(w), P(s), P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
+    assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
+    qw.close()
+
+
+def test_int4_tied_head_full_size(gpu, oracle):
+    # the 151936 x 1024 INT4 head at M = 1 (GEMV) and M = 32 (GEMM): int32 sums against an exact integer product
+    N, K = synth.QWEN35_INT4_HEAD[1:]
+    w, s = synth.int4_weight((49,), N, K)
+    qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+    vals = synth.unpack_int4(w, K).astype(np.float64)
+    for M, path in ((1, GEMV), (32, GEMM)):
+        x = synth.activations((50, M), M, K)
+        xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+        acc = run_acc(gpu, qw, xq_d, M, (M, N), path)
+        exact = xq[:, :K].astype(np.float64) @ vals.T          # integer-valued, |sums| < 2^53
+        assert np.array_equal(acc.astype(np.float64), exact)
+    qw.close()
+
+
+def test_bitnet_layer_prefill_512(gpu, oracle):
+    # every linear of the BitNet-2B-shaped layer at M = 512 through the MFMA GEMM, group sums exact
+    import torch
+    M = 512
+    for name, N, K, g in synth.BITNET_2B_LAYER:
+        w, s = synth.ternary_weight((51, N, K, g), N, K, g)
+        x = synth.activations((52, K), M, K)
+        qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+        xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+        y = run_linear(gpu, qw, xq_d, xs_d, M, GEMM)
+        codes = synth.unpack_ternary(w, K).astype(np.float64)
+        ng = K // g
+        want = np.zeros((M, N))
+        mag = np.zeros((M, N))
+        for gi in range(ng):
+            a = xq[:, gi * g:(gi + 1) * g].astype(np.float64) @ codes[:, gi * g:(gi + 1) * g].T   # exact ints
+            want += a * s[None, :, gi]
+            mag += np.abs(a) * s[None, :, gi]
+        want *= xs[:, None]
+        mag *= xs[:, None]
+        err = np.abs(y - want) / (mag + 1e-30)
+        assert err.max() <= REL_TOL, (name, err.max())
+        qw.close()
+        del xq_d, xs_d
+        torch.cuda.empty_cache()
