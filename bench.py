@@ -38,22 +38,40 @@ def parse():
 
 
 class Timer:
-    """HIP events on the current (launch) stream."""
+    """Seconds per call of fn(i), i = 0..n-1, launched back to back.
+
+    The n calls are captured once into a HIP graph and the graph is replayed; HIP events recorded on the stream
+    the graph runs on bracket the replays, so host-side enqueue cost is excluded and the figure is the device time
+    of the launches including the gaps between them. eager=True times plain launches from Python instead."""
 
     def __init__(self, torch):
         self.torch = torch
 
-    def __call__(self, fn, reps):
+    def __call__(self, fn, n, replays=5, eager=False):
         t = self.torch
         s = t.cuda.current_stream()
         a, b = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        if eager:
+            t.cuda.synchronize()
+            a.record(s)
+            for i in range(n):
+                fn(i)
+            b.record(s)
+            b.synchronize()
+            return a.elapsed_time(b) / n * 1e-3
+        g = t.cuda.CUDAGraph()
+        with t.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        g.replay()
         t.cuda.synchronize()
         a.record(s)
-        for i in range(reps):
-            fn(i)
+        for _ in range(replays):
+            g.replay()
         b.record(s)
         b.synchronize()
-        return a.elapsed_time(b) / reps * 1e-3  # seconds per call
+        del g
+        return a.elapsed_time(b) / (n * replays) * 1e-3
 
 
 def copies_for(nbytes):
@@ -78,13 +96,15 @@ def main():
     timer = Timer(torch)
 
     # ---------------- headline: BitNet-2B layer, M = 1 ----------------
-    layer = synth.BITNET_2B_LAYER
+    # gate and up share their input, so their rows are stacked into one 13824-row weight (one launch), as the
+    # reference's fused w1w3 entry point does (src/eif_quantize_bitnet.c:894-942).
+    base = {name: synth.ternary_weight((100, i), N, K, g) for i, (name, N, K, g) in enumerate(synth.BITNET_2B_LAYER)}
+    base["gateup"] = (np.concatenate([base["gate"][0], base["up"][0]]), np.concatenate([base["gate"][1], base["up"][1]]))
+    layer = [("qkv", 3840, 2560, 128), ("o", 2560, 2560, 128), ("gateup", 13824, 2560, 128), ("down", 2560, 6912, 96)]
     layer_w_bytes = sum(synth.ternary_linear_bytes(N, K, g, 0) for _, N, K, g in layer)
     ncopy = copies_for(layer_w_bytes)
-    base = {name: synth.ternary_weight((100, i), N, K, g) for i, (name, N, K, g) in enumerate(layer)}
-    copies = []
-    for c in range(ncopy):
-        copies.append({name: bh.QWeight(bh.W_TERNARY, N, K, g, *base[name]) for name, N, K, g in layer})
+    copies = [{name: bh.QWeight(bh.W_TERNARY, N, K, g, *base[name]) for name, N, K, g in layer}
+              for _ in range(ncopy)]
     shapes = {name: (N, K, g) for name, N, K, g in layer}
 
     M = 1
@@ -98,47 +118,50 @@ def main():
     def prep(K):
         bh.prep_rows(x_in[K], xq[K], xs[K], 128, norm)
 
-    def layer_step(i):
-        w = copies[i % ncopy]
-        prep(2560)                                   # input norm -> QKV
-        w["qkv"].linear(xq[2560], xs[2560], y["qkv"], path=bh.PATH_GEMV)
-        prep(2560)                                   # attention output -> O
-        w["o"].linear(xq[2560], xs[2560], y["o"], path=bh.PATH_GEMV)
-        prep(2560)                                   # post-attention norm -> gate, up
-        w["gate"].linear(xq[2560], xs[2560], y["gate"], path=bh.PATH_GEMV)
-        w["up"].linear(xq[2560], xs[2560], y["up"], path=bh.PATH_GEMV)
-        prep(6912)                                   # SwiGLU output -> down
-        w["down"].linear(xq[6912], xs[6912], y["down"], path=bh.PATH_GEMV)
+    def fused(i, name):
+        K = shapes[name][1]
+        copies[i % ncopy][name].linear_f32(x_in[K], y[name], 128, norm)
 
-    prep_bytes = 3 * (2560 * 4 + 2560 + 4) + (6912 * 4 + 6912 + 4)
-    gemv_bytes = sum(synth.ternary_linear_bytes(N, K, g, M) for _, N, K, g in layer)
-    step_bytes = prep_bytes + gemv_bytes
+    def layer_step(i):
+        # FP32 activations in: each launch rotates + quantizes its input row and runs the ternary GEMV
+        for name in ("qkv", "o", "gateup", "down"):
+            fused(i, name)
+
+    def layer_step_unfused(i):
+        w = copies[i % ncopy]
+        for name in ("qkv", "o", "gateup", "down"):
+            K = shapes[name][1]
+            prep(K)
+            w[name].linear(xq[K], xs[K], y[name], path=bh.PATH_GEMV)
+
+    def fused_bytes(N, K, g):
+        # codes + fp32 group scales + the fp32 activation row in + fp32 outputs
+        return N * (K // 4) + 4 * N * (-(-K // g)) + 4 * M * K + 4 * M * N
+
+    step_bytes = sum(fused_bytes(N, K, g) for _, N, K, g in layer)
 
     for i in range(args.warmup):
         layer_step(i)
     torch.cuda.synchronize()
+    eager_sec = timer(layer_step, min(args.steps, 100), eager=True)
     t0 = time.perf_counter()
-    sec = timer(layer_step, args.steps)
+    sec = timer(layer_step, args.steps, replays=1)
     wall = time.perf_counter() - t0
     value = step_bytes / sec / 1e9
+    unfused_sec = timer(layer_step_unfused, args.steps, replays=1)
 
-    # dominant kernel: ternary GEMV, per-linear launch duration over back-to-back launches (rotating weights)
-    prep(2560)
-    prep(6912)
+    # dominant kernel: the fused prep + ternary GEMV, per-linear launch duration over back-to-back launches
     reps = max(50, args.steps)
     per_linear = {}
     for name, (N, K, g) in shapes.items():
-        fn = lambda i, name=name, K=K: copies[i % ncopy][name].linear(xq[K], xs[K], y[name], path=bh.PATH_GEMV)
-        for i in range(10):
-            fn(i)
-        t = timer(fn, reps)
-        per_linear[name] = {"us": t * 1e6, "GBps": synth.ternary_linear_bytes(N, K, g, M) / t / 1e9}
+        t = timer(lambda i, name=name: fused(i, name), reps)
+        per_linear[name] = {"us": t * 1e6, "GBps": fused_bytes(N, K, g) / t / 1e9}
     gemv_time = sum(v["us"] for v in per_linear.values()) * 1e-6
-    gemv_gbs = gemv_bytes / gemv_time / 1e9
+    gemv_gbs = step_bytes / gemv_time / 1e9
     prep_t = timer(lambda i: prep(2560), reps)
 
     out = {
-        "metric": "BitNet-2B-shape layer ternary hot path (WHT+INT8 prep + GEMV), M=1, HBM GB/s",
+        "metric": "Ternary/INT4 GEMV HBM GB/s (% of peak); BitNet-2B-shape decode tok/s",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -151,14 +174,18 @@ def main():
         "dtype": "int8 x ternary -> int32 acc, fp32 scale",
         "data": "synthetic (seeded; random-init weights of the BitNet-b1.58-2B layer shapes)",
         "config": {"workload": "bitnet2b_layer_linears_m1", "tokens": M, "hidden": 2560, "ffn": 6912,
-                   "qkv_rows": 3840, "groups": "g128 (qkv/o/gate/up), g96 (down)", "wht_block": 128,
+                   "launches": "qkv 3840x2560, o 2560x2560, gate+up 13824x2560 (g128), down 2560x6912 (g96), "
+                               "each with its WHT-128 + INT8 prep fused",
                    "weight_copies": ncopy, "step_bytes": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qlinear_kernel (ternary GEMV, the 5 layer linears)",
+                     "kernel": "qgemv_kernel (prep fused, ternary int8-MFMA GEMV), the 4 launches of a layer",
                      "per_launch": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)}
                                     for k, v in per_linear.items()}},
         "prep_us": round(prep_t * 1e6, 3),
+        "step_us_unfused_prep_kernel": round(unfused_sec * 1e6, 2),
+        "step_us_eager_python_launch": round(eager_sec * 1e6, 2),
+        "timing": "HIP graph of the timed steps, replayed; HIP events on its stream",
         "wall_s_timed": round(wall, 3),
     }
 
@@ -180,10 +207,20 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
     ex = {}
     reps = max(50, args.steps // 2)
     ncopy = len(copies)
-    # single 6912x2560 g128 linear (the gate projection), M = 1
-    t = timer(lambda i: copies[i % ncopy]["gate"].linear(xq[2560], xs[2560], y["gate"], path=bh.PATH_GEMV), reps)
+    # the single 6912x2560 g128 linear, M = 1: from prepped int8 activations, and with the prep fused
+    gw, gs = synth.ternary_weight((100, 2), 6912, 2560, 128)
+    single = [bh.QWeight(bh.W_TERNARY, 6912, 2560, 128, gw, gs)
+              for _ in range(copies_for(synth.ternary_linear_bytes(6912, 2560, 128, 0)))]
+    ys = torch.zeros((1, 6912), dtype=torch.float32, device=dev)
+    bh.prep_rows(x_in[2560], xq[2560], xs[2560], 128, norm)
+    t = timer(lambda i: single[i % len(single)].linear(xq[2560], xs[2560], ys, path=bh.PATH_GEMV), reps)
     b = synth.ternary_linear_bytes(6912, 2560, 128, 1)
     ex["ternary_6912x2560_g128_m1"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1)}
+    t = timer(lambda i: single[i % len(single)].linear_f32(x_in[2560], ys, 128, norm), reps)
+    b = 6912 * 640 + 4 * 6912 * 20 + 4 * 2560 + 4 * 6912
+    ex["ternary_6912x2560_g128_m1_prep_fused"] = {"us": round(t * 1e6, 3), "GBps": round(b / t / 1e9, 1)}
+    for q in single:
+        q.close()
 
     # token batches through the layer linears (GEMV for M = 8, MFMA GEMM for M >= 64)
     for M in (8, 64, 512):

@@ -29,8 +29,11 @@ _SIGS = {
     "eif_hip_qlinear": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_ex": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "eif_hip_qlinear_acc": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),
+    "eif_hip_qlinear_f32": (_i, [_vp, _vp, _i, _vp, _i, _f, _vp, _vp, _i, _i, _vp]),
+    "eif_hip_qlinear_f32_acc": (_i, [_vp, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),
     "eif_hip_set_gemm_min_tokens": (_i, [_i]),
     "eif_hip_gemm_min_tokens": (_i, []),
+    "eif_hip_set_gemv_ksplit": (_i, [_i]),
     "eif_hip_forget_host_weights": (None, [_vp]),
     # host-pointer drop-in ABI
     "eif_unpack_ternary": (C.c_int8, [C.c_uint8, _i]),
@@ -145,3 +148,12 @@ class QWeight:
         M = xq.shape[0] if M is None else M
         check(load().eif_hip_qlinear_acc(self.h, ptr(xq), xq.stride(0), ptr(acc), M, path, stream_ptr(stream)),
               "eif_hip_qlinear_acc")
+
+    def linear_f32(self, x, y, block, norm, signs=None, bias=None, stream=None):
+        """prep(x) fused into the GEMV: x [M, K] FP32 on the device, M <= 8."""
+        check(load().eif_hip_qlinear_f32(self.h, ptr(x), x.stride(0), ptr(signs), block, norm, ptr(bias), ptr(y),
+                                         y.stride(0), x.shape[0], stream_ptr(stream)), "eif_hip_qlinear_f32")
+
+    def acc_f32(self, x, acc, block, norm, signs=None, stream=None):
+        check(load().eif_hip_qlinear_f32_acc(self.h, ptr(x), x.stride(0), ptr(signs), block, norm, ptr(acc),
+                                             x.shape[0], stream_ptr(stream)), "eif_hip_qlinear_f32_acc")

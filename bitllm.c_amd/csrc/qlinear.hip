@@ -278,6 +278,368 @@ __global__ __launch_bounds__(64 * RT * KSPLIT) void qlinear_kernel(QArgs a)
         }
 }
 
+// ---- small-batch GEMV (M <= kGemvMaxM): one 16-row tile per workgroup, ks = blockDim.x / 64 waves ----
+//
+// Wave kw owns steps kw, kw + ks, ... of the tile. Order of work, chosen so no load waits on another:
+//   1. the activation loads (the FP32 row slice of the fused prep, or the int8 row pieces to stage),
+//   2. every weight load of the wave's steps (codes and group scales, up to kMaxS steps in registers),
+//   3. the prep (sign flip + blockwise WHT + absmax INT8 -- the operations of prep.hip, bit-identical) or the
+//      copy, writing the int8 activations to LDS, while the weight loads are in flight,
+//   4. the MFMAs, reading activations from LDS, and a K-split reduction through LDS in wave order.
+// Memory-level parallelism comes from the number of waves (up to 16 per tile, one or two steps each) rather
+// than from long per-thread loops: for matrices of a few MB that is what keeps HBM busy.
+
+constexpr int kGemvMaxM = 8;
+constexpr int kMaxS = 8;
+constexpr int kMaxPieces = 4;
+
+struct PrepArgs {
+    const float *x;       // [M, ldx] FP32 rows to prep in the kernel, or NULL (xq/xs of QArgs are staged)
+    int ldx;
+    const float *signs;   // [K] or NULL
+    int K, block;         // block 0: no rotation
+    float norm;
+    int ldl;              // LDS row stride of the staged activations (bytes)
+};
+
+// v <- v of lane (l ^ LX): DPP only for LX <= 8 (quad_perm, row_half_mirror, row_mirror compositions).
+template <int LX>
+EIF_DEV float xlane(float v)
+{
+    int i = __float_as_int(v);
+    if constexpr (LX == 1) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);            // quad_perm [1,0,3,2]
+    } else if constexpr (LX == 2) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);            // quad_perm [2,3,0,1]
+    } else if constexpr (LX == 4) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);           // row_half_mirror: l ^ 7
+        i = __builtin_amdgcn_update_dpp(0, i, 0x1B, 0xF, 0xF, false);            // quad_perm [3,2,1,0]: ^ 3
+    } else if constexpr (LX == 8) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0x140, 0xF, 0xF, false);           // row_mirror: l ^ 15
+        i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);           // row_half_mirror: ^ 7
+    } else {
+        return __shfl_xor(v, LX, 64);
+    }
+    return __int_as_float(i);
+}
+
+template <int LX, int E>
+EIF_DEV void wht_cross(float (&v)[E], int t)
+{
+    const bool upper = (t & LX) != 0;
+    float o[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = xlane<LX>(v[e]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = upper ? o[e] - v[e] : v[e] + o[e];
+}
+
+// q = trunc(t +- 0.5) clamped, t = v*inv. copysign(0.5, t) + t equals the reference's branch for every t
+// (t = -0 gives -0.5 -> 0 where the branch gives 0.5 -> 0).
+EIF_DEV int quant1(float v, float inv)
+{
+    const float t = v * inv;
+    const float r = t + __builtin_copysignf(0.5f, t);
+    const int q = (int)r;
+    return min(max(q, -128), 127);
+}
+
+// max over the 64 lanes: DPP butterflies inside each 16-lane row, then the four row maxima via readlane.
+EIF_DEV float wave_max_dpp(float v)
+{
+    v = fmaxf(v, xlane<1>(v));
+    v = fmaxf(v, xlane<2>(v));
+    v = fmaxf(v, xlane<4>(v));
+    v = fmaxf(v, xlane<8>(v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Thread t holds columns [E*t, E*t + E) of token row m (zeros past K). The loads are unconditional (clamped to
+// the row) and nothing consumes them here, so the weight loads issued next are not held behind them; the sign
+// flip and the zeroing past K happen in prep_finish.
+template <int E>
+EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E])
+{
+    const int i0 = E * threadIdx.x;
+    const int ic = i0 < p.K ? i0 : 0;
+    const float *xr = p.x + (size_t)m * p.ldx + ic;
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(xr + 4 * q);
+        v[4 * q] = a4.x, v[4 * q + 1] = a4.y, v[4 * q + 2] = a4.z, v[4 * q + 3] = a4.w;
+    }
+    const float *sp = p.signs ? p.signs + ic : p.x + ic;   // any valid address when there are no signs
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q) {
+        const float4 s4 = *reinterpret_cast<const float4 *>(sp + 4 * q);
+        sg[4 * q] = s4.x, sg[4 * q + 1] = s4.y, sg[4 * q + 2] = s4.z, sg[4 * q + 3] = s4.w;
+    }
+}
+
+// Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
+template <int E>
+EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], const float (&sg)[E], int8_t *lds_x,
+                         float *xs_l, float *red)
+{
+    const int t = threadIdx.x, i0 = E * t, nw = blockDim.x >> 6;
+    const bool live = i0 < p.K, flip = p.block > 0 && p.signs;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = !live ? 0.0f : (flip ? v[e] * sg[e] : v[e]);
+#pragma unroll
+    for (int h = 1; h < E; h <<= 1) {
+        if (h >= p.block) break;
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if ((e & h) == 0) {
+                const float a = v[e], b = v[e + h];
+                v[e] = a + b;
+                v[e + h] = a - b;
+            }
+    }
+    if (p.block > E) wht_cross<1>(v, t);
+    if (p.block > 2 * E) wht_cross<2>(v, t);
+    if (p.block > 4 * E) wht_cross<4>(v, t);
+    if (p.block > 8 * E) wht_cross<8>(v, t);
+    if (p.block > 16 * E) wht_cross<16>(v, t);
+    if (p.block > 32 * E) wht_cross<32>(v, t);
+    float amax = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if (p.block > 0) v[e] = v[e] * p.norm;
+        amax = fmaxf(amax, fabsf(v[e]));
+    }
+    amax = wave_max_dpp(amax);
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+    for (int w = 1; w < nw; ++w) amax = fmaxf(amax, red[w]);
+    const bool zero = amax < 1e-12f;
+    const float inv = zero ? 0.0f : 127.0f / amax;
+    if (t == 0) xs_l[m] = zero ? 1.0f : amax * (1.0f / 127.0f);
+    if (i0 < kpad) {
+        uint32_t d[E / 4];
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            uint32_t u = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                u |= ((uint32_t)quant1(v[4 * q + b], inv) & 0xFFu) << (8 * b);
+            d[q] = u;
+        }
+        int8_t *o = lds_x + m * p.ldl + i0;
+        if constexpr (E % 16 == 0) {
+#pragma unroll
+            for (int q = 0; q < E / 16; ++q)
+                *reinterpret_cast<uint4 *>(o + 16 * q) = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+        } else {
+            *reinterpret_cast<uint2 *>(o) = make_uint2(d[0], d[1]);
+        }
+    }
+    __syncthreads();   // red[] is reused by the next row; lds_x complete
+}
+
+// E = 0: activations come prepped (xq/xs); E = 8/16: prep fused, E columns per thread.
+// SPW: steps per wave held in registers at once; the first SPW are loaded unconditionally (a wave with fewer
+// steps loads its last step again and skips the copies), later chunks only when a row has more steps.
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW>
+__global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
+{
+    using GE = Geo<FMT, UD>;
+    constexpr int NW = GE::SB / 4;
+    constexpr int EV = E > 0 ? E : 4;
+    constexpr int MS = SPW;
+    extern __shared__ __align__(16) int8_t smem[];
+    __shared__ float xs_l[kGemvMaxM];
+    __shared__ float red_max[16];
+    const int ks = blockDim.x >> 6;
+    // the wave index through readfirstlane: a scalar, so the per-wave step bounds below are scalar branches
+    const int lane = threadIdx.x & 63, kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, s = lane >> 4;
+    const int row = blockIdx.x * 16 + r16;
+    const bool row_ok = row < a.N;
+    const int kpad = a.nsteps * GE::SC;
+    const int nj = (a.nsteps - kw + ks - 1) / ks;
+    int8_t *lds_x = smem;
+    float *red = reinterpret_cast<float *>(smem + a.M * p.ldl);   // [ks-1][4][64] K-split partials
+
+    // 1. activation loads
+    float v[EV], sg[EV];
+    int4 pc0, pc1, pc2, pc3;   // up to kMaxPieces 16-byte pieces of the int8 rows per thread
+    const int pieces = kpad / 16;
+    auto piece_at = [&](int i) -> const int4 * {
+        const int idx = threadIdx.x + i * blockDim.x;
+        const int ic = idx < a.M * pieces ? idx : a.M * pieces - 1;
+        const int m = ic / pieces, c = ic - m * pieces;
+        return reinterpret_cast<const int4 *>(a.xq + (size_t)m * a.ldq + 16 * c);
+    };
+    auto piece_store = [&](int i, const int4 &val) {
+        const int idx = threadIdx.x + i * blockDim.x;
+        if (idx < a.M * pieces) {
+            const int m = idx / pieces, c = idx - m * pieces;
+            *reinterpret_cast<int4 *>(lds_x + m * p.ldl + 16 * c) = val;
+        }
+    };
+    float xs_v = 0.0f;
+    if constexpr (E > 0) {
+        prep_load<E>(p, 0, v, sg);
+    } else {
+        pc0 = *piece_at(0);
+        pc1 = *piece_at(1);
+        pc2 = *piece_at(2);
+        pc3 = *piece_at(3);
+        xs_v = a.xs[(int)threadIdx.x < a.M ? threadIdx.x : 0];
+    }
+
+    // Keep the activation loads ahead of the weight loads: loads complete in issue order, so staging the
+    // activations then waits for them alone.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. weight loads: unconditional, with the step clamped into the row (steps past nj are loaded from the
+    // last step and never used) and the scale index clamped into the scale array; no branch, no wait.
+    const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
+    const int row_c = row_ok ? row : a.N - 1;
+    uint32_t wv[MS][NW];
+    float sc[MS][2];
+    auto load_chunk = [&](int j0) {
+#pragma unroll
+        for (int j = 0; j < MS; ++j) {
+            if (j0 > 0 && j0 + j >= nj) break;   // later chunks: wave-uniform bound
+            const int stj = kw + (j0 + j) * ks;
+            const int st = stj < a.nsteps ? stj : a.nsteps - 1;
+            load_words<NW>(wp + (size_t)st * 4 * GE::SB, wv[j]);
+            if constexpr (GROUPED) {
+#pragma unroll
+                for (int grp = 0; grp < 2; ++grp) {
+                    const int gi = 2 * st + grp;
+                    sc[j][grp] = a.scales[(size_t)row_c * a.G + (gi < a.G ? gi : a.G - 1)];
+                }
+            }
+        }
+    };
+    load_chunk(0);
+
+    // 3. activations -> LDS
+    if constexpr (E > 0) {
+        prep_finish<E>(p, 0, kpad, v, sg, lds_x, xs_l, red_max);
+        for (int m = 1; m < a.M; ++m) {
+            prep_load<E>(p, m, v, sg);
+            prep_finish<E>(p, m, kpad, v, sg, lds_x, xs_l, red_max);
+        }
+    } else {
+        piece_store(0, pc0);
+        piece_store(1, pc1);
+        piece_store(2, pc2);
+        piece_store(3, pc3);
+        if ((int)threadIdx.x < a.M) xs_l[threadIdx.x] = xs_v;
+        __syncthreads();
+    }
+
+    // 4. MFMAs
+    const bool tok_ok = r16 < a.M;
+    const int8_t *xl = lds_x + (tok_ok ? r16 : 0) * p.ldl;
+    float F[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4i C = {0, 0, 0, 0};
+    for (int j0 = 0; j0 < nj; j0 += MS) {
+        if (j0 > 0) load_chunk(j0);
+#pragma unroll
+        for (int j = 0; j < MS; ++j) {
+            if (j0 + j >= nj) break;
+            const int st = kw + (j0 + j) * ks;
+            long bop[GE::NMF];
+            decode<FMT, UD>(wv[j], bop);
+            if constexpr (FMT == kTern) {
+#pragma unroll
+                for (int grp = 0; grp < 2; ++grp) {
+                    long aop[UD];
+                    if (tok_ok) {
+                        load_ops<UD, (UD % 2 == 0)>(xl + st * GE::SC + 32 * UD * grp + 8 * UD * s, aop);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < UD; ++i) aop[i] = 0;
+                    }
+                    v4i c = GROUPED ? v4i{0, 0, 0, 0} : C;
+#pragma unroll
+                    for (int i = 0; i < UD; ++i) c = mfma(aop[i], bop[grp * UD + i], c);
+                    if constexpr (GROUPED) {
+                        const int gi = 2 * st + grp;
+                        const float scv = gi < a.G ? sc[j][grp] : 0.0f;
+#pragma unroll
+                        for (int vv = 0; vv < 4; ++vv) {
+                            const int g_acc = c[vv] >> GE::SHIFT;
+                            if constexpr (ACC) {
+                                const int tok = 4 * s + vv;
+                                if (row_ok && tok < a.M && gi < a.G)
+                                    a.acc[((size_t)tok * a.N + row) * a.G + gi] = g_acc;
+                            } else {
+                                F[vv] = fmaf((float)g_acc, scv, F[vv]);
+                            }
+                        }
+                    } else {
+                        C = c;
+                    }
+                }
+            } else {
+                long aop[GE::NMF];
+                if (tok_ok) {
+                    load_ops<GE::NMF, true>(xl + st * GE::SC + (GE::SC / 4) * s, aop);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < GE::NMF; ++i) aop[i] = 0;
+                }
+#pragma unroll
+                for (int i = 0; i < GE::NMF; ++i) C = mfma(aop[i], bop[i], C);
+            }
+        }
+    }
+    if constexpr (GROUPED && ACC) return;
+
+    // 5. K-split reduction (waves kw > 0 -> wave 0, added in wave order) and epilogue
+    if (ks > 1) {
+        if (kw > 0) {
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv)
+                red[((kw - 1) * 4 + vv) * 64 + lane] = GROUPED ? F[vv] : __int_as_float(C[vv]);
+        }
+        __syncthreads();
+        if (kw > 0) return;
+        for (int k = 0; k < ks - 1; ++k)
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const float r = red[(k * 4 + vv) * 64 + lane];
+                if constexpr (GROUPED)
+                    F[vv] += r;
+                else
+                    C[vv] += __float_as_int(r);
+            }
+    }
+    if (!row_ok) return;
+    const float rs = (!GROUPED && a.scales) ? a.scales[row] : 1.0f;
+    const float bb = a.bias ? a.bias[row] : 0.0f;
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+        const int tok = 4 * s + vv;
+        if (tok >= a.M) continue;
+        float out;
+        if constexpr (GROUPED) {
+            out = F[vv] * xs_l[tok];
+        } else {
+            const int isum = C[vv] >> GE::SHIFT;
+            if constexpr (ACC) {
+                a.acc[(size_t)tok * a.N + row] = isum;
+                continue;
+            }
+            out = ((float)isum * xs_l[tok]) * rs;
+        }
+        if (a.bias) out = out + bb;
+        a.y[(size_t)tok * a.ldy + row] = out;
+    }
+}
+
+
 // ---- repack kernels: reference formats -> GPU layouts (one thread per destination dword) ----
 
 EIF_DEV int tern_code(const uint8_t *src, int sld, int rows, int cols, int r, int c)
@@ -354,6 +716,7 @@ struct eif_hip_qweight {
 namespace {
 
 int g_gemm_min_tokens = 16;
+int g_gemv_ksplit = 0;   // 0 = pick_ksplit()
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
 
@@ -374,11 +737,72 @@ int pick_ksplit(int row_tiles, int nsteps)
     return k;
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC>
-int launch_shape(const QArgs &a, int rows_pad, int path, hipStream_t st)
+// Waves per tile of the small-batch GEMV (measured on MI355X with graph-chained launches): two steps per wave
+// for the 1-9 MB matrices of a layer, four for long rows (>= 24 steps), eight when the tiles alone fill the
+// chip (vocabulary heads), at most 16 waves.
+int pick_ks_gemv(int row_tiles, int nsteps)
 {
+    const int spw = row_tiles >= 4096 ? 8 : (nsteps >= 24 ? 4 : 2);
+    int ks = eif_ceil_div(nsteps, spw);
+    return ks > 16 ? 16 : (ks < 1 ? 1 : ks);
+}
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW>
+int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
+{
+    const size_t lds = (size_t)a.M * p.ldl + (size_t)(ks - 1) * 4 * 64 * sizeof(float);
+    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW><<<rows_pad / 16, 64 * ks, lds, st>>>(a, p);
+    EIF_HIP_LAUNCHED();
+    return EIF_HIP_OK;
+}
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int E>
+int launch_gemv_e(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
+{
+    const int steps = eif_ceil_div(a.nsteps, ks);
+    constexpr int SMAX = Geo<FMT, UD>::SB >= 32 ? 4 : 8;   // 8-dword steps: half the registers per chunk
+    if constexpr (ACC) {
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX>(a, p, rows_pad, ks, st);
+    } else {
+        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1>(a, p, rows_pad, ks, st);
+        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2>(a, p, rows_pad, ks, st);
+        if (steps <= 4 || SMAX == 4) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4>(a, p, rows_pad, ks, st);
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX>(a, p, rows_pad, ks, st);
+    }
+}
+
+// Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses qlinear_kernel).
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_gemv(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
+{
+    const int kpad = a.nsteps * Geo<FMT, UD>::SC;
+    p.ldl = kpad + 16;
+    int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(rows_pad / 16, a.nsteps);
+    if (p.x) {
+        // E columns per thread: the whole padded row covered, and a WHT block within one wave
+        for (;; ++ks) {
+            if (ks > 16) return EIF_HIP_E_LIMIT;
+            for (int e = 8; e <= 16; e *= 2)
+                if (64 * ks * e >= kpad && 64 * e >= p.block) {
+                    if (e == 8) return launch_gemv_e<FMT, UD, GROUPED, ACC, 8>(a, p, rows_pad, ks, st);
+                    return launch_gemv_e<FMT, UD, GROUPED, ACC, 16>(a, p, rows_pad, ks, st);
+                }
+        }
+    }
+    while (ks < 16 && a.M * (kpad / 16) > kMaxPieces * 64 * ks) ++ks;
+    if (a.M * (kpad / 16) > kMaxPieces * 64 * ks) return 1;
+    return launch_gemv_e<FMT, UD, GROUPED, ACC, 0>(a, p, rows_pad, ks, st);
+}
+
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_shape(const QArgs &a, const PrepArgs &p, int rows_pad, int path, hipStream_t st)
+{
+    if (p.x || (path == EIF_HIP_PATH_GEMV && a.M <= kGemvMaxM)) {
+        const int rc = launch_gemv<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
+        if (rc != 1) return rc;
+    }
     if (path == EIF_HIP_PATH_GEMM) return launch_one<FMT, UD, GROUPED, ACC, 4, 4, 1, false>(a, rows_pad, st);
-    const int ks = pick_ksplit(rows_pad / 16, a.nsteps);
+    const int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ksplit(rows_pad / 16, a.nsteps);
     if constexpr (ACC) {
         return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 4, false>(a, rows_pad, st);
     } else {
@@ -400,20 +824,39 @@ int launch_shape(const QArgs &a, int rows_pad, int path, hipStream_t st)
 }
 
 template <bool ACC>
-int dispatch(const eif_hip_qweight *w, const QArgs &a, int path, hipStream_t st)
+int dispatch(const eif_hip_qweight *w, const QArgs &a, const PrepArgs &p, int path, hipStream_t st)
 {
     const bool grouped = w->fmt == kTern && w->group > 0;
-    if (w->fmt == kI8) return launch_shape<kI8, 0, false, ACC>(a, w->rows_pad, path, st);
-    if (w->fmt == kI4) return launch_shape<kI4, 0, false, ACC>(a, w->rows_pad, path, st);
-    if (!grouped) return launch_shape<kTern, 4, false, ACC>(a, w->rows_pad, path, st);
+    if (w->fmt == kI8) return launch_shape<kI8, 0, false, ACC>(a, p, w->rows_pad, path, st);
+    if (w->fmt == kI4) return launch_shape<kI4, 0, false, ACC>(a, p, w->rows_pad, path, st);
+    if (!grouped) return launch_shape<kTern, 4, false, ACC>(a, p, w->rows_pad, path, st);
     switch (w->ud) {
-    case 1: return launch_shape<kTern, 1, true, ACC>(a, w->rows_pad, path, st);
-    case 2: return launch_shape<kTern, 2, true, ACC>(a, w->rows_pad, path, st);
-    case 3: return launch_shape<kTern, 3, true, ACC>(a, w->rows_pad, path, st);
-    case 4: return launch_shape<kTern, 4, true, ACC>(a, w->rows_pad, path, st);
-    case 8: return launch_shape<kTern, 8, true, ACC>(a, w->rows_pad, path, st);
+    case 1: return launch_shape<kTern, 1, true, ACC>(a, p, w->rows_pad, path, st);
+    case 2: return launch_shape<kTern, 2, true, ACC>(a, p, w->rows_pad, path, st);
+    case 3: return launch_shape<kTern, 3, true, ACC>(a, p, w->rows_pad, path, st);
+    case 4: return launch_shape<kTern, 4, true, ACC>(a, p, w->rows_pad, path, st);
+    case 8: return launch_shape<kTern, 8, true, ACC>(a, p, w->rows_pad, path, st);
     default: return EIF_HIP_E_ARG;
     }
+}
+
+// Fused-prep arguments: x [M, ldx] FP32 with K == cols, K % 32 == 0, 16-byte aligned rows and signs.
+int make_prep(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int block, float norm, int M,
+              PrepArgs *p)
+{
+    *p = PrepArgs{};
+    if (!w || !x || M < 1 || M > kGemvMaxM) return M > kGemvMaxM ? EIF_HIP_E_LIMIT : EIF_HIP_E_ARG;
+    const int K = w->cols;
+    if (K % 32 != 0 || ldx < K || ldx % 4 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)signs & 15))
+        return EIF_HIP_E_ARG;
+    if (block < 0 || block > 1024 || (block > 0 && ((block & (block - 1)) || K % block != 0))) return EIF_HIP_E_ARG;
+    p->x = x;
+    p->ldx = ldx;
+    p->signs = signs;
+    p->K = K;
+    p->block = block;
+    p->norm = norm;
+    return EIF_HIP_OK;
 }
 
 int check_linear_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
@@ -463,10 +906,37 @@ int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *
     a.bias = bias;
     a.y = y;
     a.ldy = ldy;
-    return dispatch<false>(w, a, resolve_path(path, M), st);
+    return dispatch<false>(w, a, PrepArgs{}, resolve_path(path, M), st);
 }
 
 }  // namespace eif
+
+extern "C" int eif_hip_qlinear_f32(const eif_hip_qweight *w, const float *x, int ldx, const float *signs,
+                                   int wht_block, float norm, const float *bias, float *y, int ldy, int M,
+                                   void *stream)
+{
+    PrepArgs p;
+    int rc = make_prep(w, x, ldx, signs, wht_block, norm, M, &p);
+    if (rc) return rc;
+    if (!y || ldy < w->rows) return EIF_HIP_E_ARG;
+    QArgs a = make_args(w, nullptr, 0, M);
+    a.bias = bias;
+    a.y = y;
+    a.ldy = ldy;
+    return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
+}
+
+extern "C" int eif_hip_qlinear_f32_acc(const eif_hip_qweight *w, const float *x, int ldx, const float *signs,
+                                       int wht_block, float norm, int32_t *acc, int M, void *stream)
+{
+    PrepArgs p;
+    int rc = make_prep(w, x, ldx, signs, wht_block, norm, M, &p);
+    if (rc) return rc;
+    if (!acc) return EIF_HIP_E_ARG;
+    QArgs a = make_args(w, nullptr, 0, M);
+    a.acc = acc;
+    return dispatch<true>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
+}
 
 extern "C" {
 
@@ -478,6 +948,13 @@ int eif_hip_set_gemm_min_tokens(int m)
 }
 
 int eif_hip_gemm_min_tokens(void) { return g_gemm_min_tokens; }
+
+int eif_hip_set_gemv_ksplit(int k)
+{
+    int old = g_gemv_ksplit;
+    if (k >= 0 && k <= 16) g_gemv_ksplit = k;
+    return old;
+}
 
 int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, int group, const void *codes,
                            const float *scales, int src_on_device, void *stream)
@@ -610,7 +1087,7 @@ int eif_hip_qlinear_acc(const eif_hip_qweight *w, const int8_t *xq, int ldq, int
     if (!acc) return EIF_HIP_E_ARG;
     QArgs a = make_args(w, xq, ldq, M);
     a.acc = acc;
-    return dispatch<true>(w, a, resolve_path(path, M), (hipStream_t)stream);
+    return dispatch<true>(w, a, PrepArgs{}, resolve_path(path, M), (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -93,6 +93,15 @@ int eif_hip_qlinear_ex(const eif_hip_qweight *w, const int8_t *xq, int ldq, cons
 int eif_hip_qlinear_acc(const eif_hip_qweight *w, const int8_t *xq, int ldq, int32_t *acc, int M, int path,
                         void *stream);
 
+/* Prep fused into the GEMV: y = linear(prep(x)) for M <= 8 FP32 rows x [M, ldx] of K = cols (K % 32 == 0,
+ * rows and signs 16-byte aligned, ldx % 4 == 0, K <= 16384), with the prep contract above (signs, wht_block <= 1024,
+ * norm). One launch; the result equals eif_hip_prep_rows followed by eif_hip_qlinear bit for bit. M > 8
+ * returns EIF_HIP_E_LIMIT (use the two calls).                                                         */
+int eif_hip_qlinear_f32(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int wht_block,
+                        float norm, const float *bias, float *y, int ldy, int M, void *stream);
+int eif_hip_qlinear_f32_acc(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int wht_block,
+                            float norm, int32_t *acc, int M, void *stream);
+
 /* Drop the device copies the host-pointer ABI keeps for the weight buffer at host_ptr (NULL: all of them).
  * Call it after rewriting a weight buffer in place or before freeing it.                                 */
 void eif_hip_forget_host_weights(const void *host_ptr);
@@ -100,6 +109,10 @@ void eif_hip_forget_host_weights(const void *host_ptr);
 /* Token count from which the auto path uses the MFMA GEMM (default 16); returns the previous value.     */
 int eif_hip_set_gemm_min_tokens(int m);
 int eif_hip_gemm_min_tokens(void);
+
+/* Waves that split one 16-row tile's columns in the GEMV (1, 2, 4 or 8; 0 = chosen from the shape, the
+ * default); returns the previous setting. A tuning knob: results do not depend on it.                   */
+int eif_hip_set_gemv_ksplit(int k);
 
 #ifdef __cplusplus
 }

@@ -44,6 +44,10 @@ def run_case(gpu, oracle, x, block, signs=None, with_rot=False, ldq=None):
     (2, 4864, 0, False),
     (1, 12288, 4096, True),     # largest row of the fused kernel
     (512, 2560, 128, False),    # prefill batch
+    (3, 2560, 512, True),       # largest block of the register path
+    (2, 2560, 1, True),         # block 1: signs and norm only
+    (2, 996, 4, True),          # K % 8 != 0: LDS path with a small block
+    (4, 11264, 256, False),     # six chunks of the register path
 ])
 def test_prep_matches_oracle(gpu, oracle, M, K, block, signed):
     x = synth.activations((31, M, K), M, K)

@@ -169,3 +169,68 @@ def test_bitnet_layer_prefill_512(gpu, oracle):
         qw.close()
         del xq_d, xs_d
         torch.cuda.empty_cache()
+
+
+FUSED = [
+    # fmt, N, K, group, M, wht block, signed
+    ("tern", 6912, 2560, 128, 1, 128, False),   # the single BitNet linear, prep fused
+    ("tern", 2560, 6912, 96, 1, 128, True),     # down projection
+    ("tern", 3840, 2560, 128, 4, 128, True),
+    ("tern", 100, 640, 64, 8, 64, False),
+    ("tern", 64, 2560, 0, 3, 128, False),       # row scales
+    ("tern", 256, 4096, 128, 2, 1024, True),    # largest WHT block of the fused prep
+    ("tern", 96, 16384, 128, 1, 128, False),    # longest row of the fused prep
+    ("int8", 4864, 896, 0, 1, 0, False),
+    ("int4", 3584, 1024, 0, 2, 0, False),
+]
+
+
+@pytest.mark.parametrize("fmt,N,K,g,M,block,signed", FUSED)
+def test_fused_prep_linear(gpu, oracle, fmt, N, K, g, M, block, signed):
+    """prep fused into the GEMV launch == prep kernel + GEMV, bit for bit; int32 sums == oracle."""
+    import ctypes as C
+    import torch
+    dev = torch.device("cuda:0")
+    if fmt == "tern":
+        w, s = synth.ternary_weight((53, N, K, g), N, K, g)
+        qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+    elif fmt == "int8":
+        w, s = synth.int8_weight((54, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+    else:
+        w, s = synth.int4_weight((55, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+    x = synth.activations((56, M, K), M, K)
+    signs = np.where(synth.rng(57, K).uniform(size=K) > 0.5, 1.0, -1.0).astype(np.float32) if signed else None
+    norm = gpu.wht_norm(block) if block else 1.0
+    xd = torch.from_numpy(x).to(dev)
+    sd = torch.from_numpy(signs).to(dev) if signed else None
+    # two-call path
+    xq_d = torch.zeros((M, qw.kpad), dtype=torch.int8, device=dev)
+    xs_d = torch.zeros(M, dtype=torch.float32, device=dev)
+    gpu.prep_rows(xd, xq_d, xs_d, block, norm, signs=sd)
+    y2 = run_linear(gpu, qw, xq_d, xs_d, M, GEMV)
+    # fused path
+    y1 = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    qw.linear_f32(xd, y1, block, norm, signs=sd)
+    ng = -(-K // g) if (fmt == "tern" and g > 0) else 0
+    acc = torch.full((M, N, ng) if ng else (M, N), -7, dtype=torch.int32, device=dev)
+    qw.acc_f32(xd, acc, block, norm, signs=sd)
+    torch.cuda.synchronize()
+    y1 = y1.cpu().numpy()
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    # oracle: prep + exact integer sums
+    xq = np.zeros((M, qw.kpad), np.int8)
+    xs = np.zeros(M, np.float32)
+    assert oracle.orc_prep_rows(P(x), K, P(signs), M, K, block, C.c_float(norm), P(xq), qw.kpad, P(xs), None, 0) == 0
+    if fmt == "tern" and ng:
+        oacc = np.zeros((M, N, ng), np.int32)
+        oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+    elif fmt == "tern":
+        oacc = xq[:, :K].astype(np.int64) @ synth.unpack_ternary(w, K).astype(np.int64).T
+    elif fmt == "int8":
+        oacc = xq[:, :K].astype(np.int64) @ w.astype(np.int64).T
+    else:
+        oacc = xq[:, :K].astype(np.int64) @ synth.unpack_int4(w, K).astype(np.int64).T
+    assert np.array_equal(acc.cpu().numpy(), oacc)
+    qw.close()
