@@ -34,7 +34,20 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (known bytes for counter calibration)")
     return ap.parse_args()
+
+
+def measured_traffic():
+    """HBM bytes of one layer step from the committed counter runs of this workload (None if absent)."""
+    path = os.path.join(ROOT, "profiles", "qgemv_bitnet2b_layer_m1_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        return sum(v["read"] + v["write"] for v in rec["per_launch_bytes"].values())
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 class Timer:
@@ -178,7 +191,10 @@ def main():
                                "each with its WHT-128 + INT8 prep fused",
                    "weight_copies": ncopy, "step_bytes": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_unit": "HBM bytes read + written by the 4 launches of one layer step "
+                                     "(FETCH_SIZE x2, WRITE_SIZE x1, calibrated on a device copy)",
+                     "algorithmic_bytes": step_bytes,
                      "kernel": "qgemv_kernel (prep fused, ternary int8-MFMA GEMV), the 4 launches of a layer",
                      "per_launch": {k: {"us": round(v["us"], 3), "GBps": round(v["GBps"], 1)}
                                     for k, v in per_linear.items()}},
@@ -191,6 +207,13 @@ def main():
 
     if not args.no_extra:
         out["extra"] = extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in, norm)
+    if args.calib_copy_mib > 0:
+        src = torch.ones(args.calib_copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        out["calib_copy_bytes"] = src.numel() * 4
+        del src, dst
 
     for cs in copies:
         for w in cs.values():
