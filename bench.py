@@ -308,6 +308,26 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
         for q in cs.values():
             q.close()
 
+    # the drop-in host API (host x in, host y out over PCIe; weights resident after the first call), M = 1
+    import numpy as np
+    lib = bh.load()
+    N, K, g = 6912, 2560, 128
+    hw, hsc = synth.ternary_weight((107,), N, K, g)
+    hx = synth.activations((108,), 1, K)[0]
+    hy = np.zeros(N, np.float32)
+    call = lambda: lib.eif_matmul_bitnet_block_f32(hw.ctypes.data, hsc.ctypes.data, g, hx.ctypes.data, None,
+                                                   hy.ctypes.data, N, K)
+    call()
+    n = 200
+    t0 = time.perf_counter()
+    for _ in range(n):
+        call()
+    t = (time.perf_counter() - t0) / n
+    b = N * (K // 4) + 4 * N * (K // g) + 4 * K + 4 * N
+    ex["host_api_block_f32_6912x2560_g128_m1"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                                                  "note": "synchronous call incl. PCIe copies of x and y"}
+    lib.eif_hip_forget_host_weights(None)
+
     # measured copy ceiling: 1 GiB device-to-device copy (read + write bytes)
     src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
     dst = torch.empty_like(src)
