@@ -241,7 +241,7 @@ void eif_hip_forget_host_weights(const void *host_ptr)
     std::lock_guard<std::mutex> lock(g_wmu);
     for (auto it = g_wcache.begin(); it != g_wcache.end();) {
         if (host_ptr == nullptr || it->first.p == host_ptr) {
-            if (it->second.raw) hipFree(it->second.raw);
+            if (it->second.raw) (void)hipFree(it->second.raw);
             if (it->second.q) eif_hip_qweight_destroy(it->second.q);
             it = g_wcache.erase(it);
         } else {

@@ -278,20 +278,25 @@ __global__ __launch_bounds__(64 * RT * KSPLIT) void qlinear_kernel(QArgs a)
         }
 }
 
-// ---- small-batch GEMV (M <= kGemvMaxM): one 16-row tile per workgroup, ks = blockDim.x / 64 waves ----
+// ---- small-batch GEMV (M <= kGemvMaxM): RT 16-row tiles per workgroup, ks waves per tile ----
 //
-// Wave kw owns steps kw, kw + ks, ... of the tile. Order of work, chosen so no load waits on another:
-//   1. the activation loads (the FP32 row slice of the fused prep, or the int8 row pieces to stage),
-//   2. every weight load of the wave's steps (codes and group scales, up to kMaxS steps in registers),
+// Each wave owns some steps of one tile. Order of work, chosen so no load waits on another:
+//   1. the activation loads (the FP32 row slice of the fused prep, or the int8 row pieces to stage) and the
+//      workgroup's group scales (one contiguous block of the scale array),
+//   2. every weight load of the wave's steps (up to SPW steps in registers),
 //   3. the prep (sign flip + blockwise WHT + absmax INT8 -- the operations of prep.hip, bit-identical) or the
 //      copy, writing the int8 activations to LDS, while the weight loads are in flight,
-//   4. the MFMAs, reading activations from LDS, and a K-split reduction through LDS in wave order.
-// Memory-level parallelism comes from the number of waves (up to 16 per tile, one or two steps each) rather
-// than from long per-thread loops: for matrices of a few MB that is what keeps HBM busy.
+//   4. the MFMAs, reading activations from LDS,
+//   5. grouped: every exact per-group int32 sum goes to LDS and one thread per (token, row) combines them with
+//      the scales in group order; row-scaled: the int32 partial sums of the K-split are added through LDS.
+// Memory-level parallelism comes from the number of waves (up to 16 per workgroup, one to four steps each)
+// rather than from long per-thread loops: for matrices of a few MB that is what keeps HBM busy. Every
+// instruction of a wave is on its critical path (one or two waves per SIMD), so the prep is written for a
+// short per-thread chain: few columns per thread, the WHT block fixed at compile time, DPP butterflies.
 
 constexpr int kGemvMaxM = 8;
-constexpr int kMaxS = 8;
 constexpr int kMaxPieces = 4;
+constexpr int kMaxScLoads = 8;
 
 struct PrepArgs {
     const float *x;       // [M, ldx] FP32 rows to prep in the kernel, or NULL (xq/xs of QArgs are staged)
@@ -323,15 +328,18 @@ EIF_DEV float xlane(float v)
     return __int_as_float(i);
 }
 
+// One WHT butterfly stage across threads t and t ^ LX: the lower thread keeps a + b, the upper one a - b (a the
+// lower thread's value, b the upper one's). Written as partner + (upper ? -v : v): the same single rounding as
+// the reference's a + b and a - b, in one negate-select and one DPP-sourced add per element.
 template <int LX, int E>
 EIF_DEV void wht_cross(float (&v)[E], int t)
 {
     const bool upper = (t & LX) != 0;
-    float o[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) o[e] = xlane<LX>(v[e]);
-#pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = upper ? o[e] - v[e] : v[e] + o[e];
+    for (int e = 0; e < E; ++e) {
+        const float own = upper ? -v[e] : v[e];
+        v[e] = xlane<LX>(v[e]) + own;
+    }
 }
 
 // q = trunc(t +- 0.5) clamped, t = v*inv. copysign(0.5, t) + t equals the reference's branch for every t
@@ -372,26 +380,32 @@ EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E])
         const float4 a4 = *reinterpret_cast<const float4 *>(xr + 4 * q);
         v[4 * q] = a4.x, v[4 * q + 1] = a4.y, v[4 * q + 2] = a4.z, v[4 * q + 3] = a4.w;
     }
-    const float *sp = p.signs ? p.signs + ic : p.x + ic;   // any valid address when there are no signs
+    if (p.signs) {   // uniform: a scalar branch
 #pragma unroll
-    for (int q = 0; q < E / 4; ++q) {
-        const float4 s4 = *reinterpret_cast<const float4 *>(sp + 4 * q);
-        sg[4 * q] = s4.x, sg[4 * q + 1] = s4.y, sg[4 * q + 2] = s4.z, sg[4 * q + 3] = s4.w;
+        for (int q = 0; q < E / 4; ++q) {
+            const float4 s4 = *reinterpret_cast<const float4 *>(p.signs + ic + 4 * q);
+            sg[4 * q] = s4.x, sg[4 * q + 1] = s4.y, sg[4 * q + 2] = s4.z, sg[4 * q + 3] = s4.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) sg[e] = 1.0f;
     }
 }
 
 // Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
-template <int E>
+// LB = log2 of the WHT block when it is fixed at compile time (0: no rotation), -1: block read from p.block.
+template <int E, int LB>
 EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], const float (&sg)[E], int8_t *lds_x,
                          float *xs_l, float *red)
 {
     const int t = threadIdx.x, i0 = E * t, nw = blockDim.x >> 6;
-    const bool live = i0 < p.K, flip = p.block > 0 && p.signs;
+    const int block = LB >= 0 ? (LB > 0 ? 1 << LB : 0) : p.block;
+    const bool live = i0 < p.K, flip = block > 0 && p.signs;
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = !live ? 0.0f : (flip ? v[e] * sg[e] : v[e]);
 #pragma unroll
     for (int h = 1; h < E; h <<= 1) {
-        if (h >= p.block) break;
+        if (h >= block) break;
 #pragma unroll
         for (int e = 0; e < E; ++e)
             if ((e & h) == 0) {
@@ -400,23 +414,23 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
                 v[e + h] = a - b;
             }
     }
-    if (p.block > E) wht_cross<1>(v, t);
-    if (p.block > 2 * E) wht_cross<2>(v, t);
-    if (p.block > 4 * E) wht_cross<4>(v, t);
-    if (p.block > 8 * E) wht_cross<8>(v, t);
-    if (p.block > 16 * E) wht_cross<16>(v, t);
-    if (p.block > 32 * E) wht_cross<32>(v, t);
+    if (block > E) wht_cross<1>(v, t);
+    if (block > 2 * E) wht_cross<2>(v, t);
+    if (block > 4 * E) wht_cross<4>(v, t);
+    if (block > 8 * E) wht_cross<8>(v, t);
+    if (block > 16 * E) wht_cross<16>(v, t);
+    if (block > 32 * E) wht_cross<32>(v, t);
     float amax = 0.0f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        if (p.block > 0) v[e] = v[e] * p.norm;
+        if (block > 0) v[e] = v[e] * p.norm;
         amax = fmaxf(amax, fabsf(v[e]));
     }
     amax = wave_max_dpp(amax);
     if ((t & 63) == 0) red[t >> 6] = amax;
     __syncthreads();
-    amax = red[0];
-    for (int w = 1; w < nw; ++w) amax = fmaxf(amax, red[w]);
+    // the per-wave maxima, one per lane, reduced again across the wave
+    amax = wave_max_dpp(red[(t & 63) < nw ? (t & 63) : 0]);
     const bool zero = amax < 1e-12f;
     const float inv = zero ? 0.0f : 127.0f / amax;
     if (t == 0) xs_l[m] = zero ? 1.0f : amax * (1.0f / 127.0f);
@@ -435,36 +449,48 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
 #pragma unroll
             for (int q = 0; q < E / 16; ++q)
                 *reinterpret_cast<uint4 *>(o + 16 * q) = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
-        } else {
+        } else if constexpr (E == 8) {
             *reinterpret_cast<uint2 *>(o) = make_uint2(d[0], d[1]);
+        } else {
+            *reinterpret_cast<uint32_t *>(o) = d[0];
         }
     }
     __syncthreads();   // red[] is reused by the next row; lds_x complete
 }
 
-// E = 0: activations come prepped (xq/xs); E = 8/16: prep fused, E columns per thread.
-// SPW: steps per wave held in registers at once; the first SPW are loaded unconditionally (a wave with fewer
-// steps loads its last step again and skips the copies), later chunks only when a row has more steps.
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW>
+// E = 0: activations come prepped (xq/xs); E = 4/8/16: prep fused, E columns per thread, LB as in prep_finish.
+// RT row tiles of 16 rows per workgroup; wave w works on tile w % RT and on steps w / RT, w / RT + ks, ... of
+// it (ks = waves / RT). SPW: steps per wave held in registers at once; the first SPW are loaded unconditionally
+// (a wave with fewer steps loads its last step again and skips the copies), later chunks only when a row has
+// more steps.
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT>
 __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 {
     using GE = Geo<FMT, UD>;
     constexpr int NW = GE::SB / 4;
     constexpr int EV = E > 0 ? E : 4;
     constexpr int MS = SPW;
+    constexpr int TR = 16 * RT;   // rows per workgroup
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float xs_l[kGemvMaxM];
     __shared__ float red_max[16];
-    const int ks = blockDim.x >> 6;
+    const int ks = (blockDim.x >> 6) / RT;
     // the wave index through readfirstlane: a scalar, so the per-wave step bounds below are scalar branches
-    const int lane = threadIdx.x & 63, kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rt = wv % RT, kw = wv / RT;
     const int r16 = lane & 15, s = lane >> 4;
-    const int row = blockIdx.x * 16 + r16;
+    const int row0 = blockIdx.x * TR;
+    const int row = row0 + 16 * rt + r16;
     const bool row_ok = row < a.N;
     const int kpad = a.nsteps * GE::SC;
     const int nj = (a.nsteps - kw + ks - 1) / ks;
     int8_t *lds_x = smem;
-    float *red = reinterpret_cast<float *>(smem + a.M * p.ldl);   // [ks-1][4][64] K-split partials
+    // after the staged activations: grouped -> int32 group sums [M][TR][gld] and scales [TR][G];
+    // row-scaled -> int32 K-split partials [ks-1][RT][4][64]
+    const int gld = (a.G + 3) & ~3;
+    int32_t *red = reinterpret_cast<int32_t *>(smem + a.M * p.ldl);
+    int32_t *acc_l = red;
+    float *sc_l = reinterpret_cast<float *>(acc_l + a.M * TR * gld);
 
     // 1. activation loads
     float v[EV], sg[EV];
@@ -494,40 +520,44 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         xs_v = a.xs[(int)threadIdx.x < a.M ? threadIdx.x : 0];
     }
 
-    // Keep the activation loads ahead of the weight loads: loads complete in issue order, so staging the
-    // activations then waits for them alone.
+    // the workgroup's group scales, rows row0 .. row0 + TR - 1: one contiguous block of the [N, G] array,
+    // loaded flat (kMaxScLoads per thread at most, clamped to the array) and staged in LDS after the prep
+    float scv[kMaxScLoads];
+    const int nsc = TR * a.G, last_sc = a.N * a.G - 1;
+    if constexpr (GROUPED && !ACC) {
+#pragma unroll
+        for (int i = 0; i < kMaxScLoads; ++i) {
+            if (i > 0 && i * (int)blockDim.x >= nsc) break;   // uniform bound
+            const int idx = row0 * a.G + (int)threadIdx.x + i * (int)blockDim.x;
+            scv[i] = a.scales[idx < last_sc ? idx : last_sc];
+        }
+    }
+
+    // Keep the activation and scale loads ahead of the weight loads: loads complete in issue order, so staging
+    // them waits for them alone.
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. weight loads: unconditional, with the step clamped into the row (steps past nj are loaded from the
-    // last step and never used) and the scale index clamped into the scale array; no branch, no wait.
+    // last step and never used); no branch, no wait.
     const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
-    const int row_c = row_ok ? row : a.N - 1;
-    uint32_t wv[MS][NW];
-    float sc[MS][2];
+    uint32_t wq[MS][NW];
     auto load_chunk = [&](int j0) {
 #pragma unroll
         for (int j = 0; j < MS; ++j) {
             if (j0 > 0 && j0 + j >= nj) break;   // later chunks: wave-uniform bound
             const int stj = kw + (j0 + j) * ks;
             const int st = stj < a.nsteps ? stj : a.nsteps - 1;
-            load_words<NW>(wp + (size_t)st * 4 * GE::SB, wv[j]);
-            if constexpr (GROUPED) {
-#pragma unroll
-                for (int grp = 0; grp < 2; ++grp) {
-                    const int gi = 2 * st + grp;
-                    sc[j][grp] = a.scales[(size_t)row_c * a.G + (gi < a.G ? gi : a.G - 1)];
-                }
-            }
+            load_words<NW>(wp + (size_t)st * 4 * GE::SB, wq[j]);
         }
     };
     load_chunk(0);
 
     // 3. activations -> LDS
     if constexpr (E > 0) {
-        prep_finish<E>(p, 0, kpad, v, sg, lds_x, xs_l, red_max);
+        prep_finish<E, LB>(p, 0, kpad, v, sg, lds_x, xs_l, red_max);
         for (int m = 1; m < a.M; ++m) {
             prep_load<E>(p, m, v, sg);
-            prep_finish<E>(p, m, kpad, v, sg, lds_x, xs_l, red_max);
+            prep_finish<E, LB>(p, m, kpad, v, sg, lds_x, xs_l, red_max);
         }
     } else {
         piece_store(0, pc0);
@@ -537,11 +567,18 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         if ((int)threadIdx.x < a.M) xs_l[threadIdx.x] = xs_v;
         __syncthreads();
     }
+    if constexpr (GROUPED && !ACC) {
+#pragma unroll
+        for (int i = 0; i < kMaxScLoads; ++i) {
+            if (i > 0 && i * (int)blockDim.x >= nsc) break;
+            const int idx = (int)threadIdx.x + i * (int)blockDim.x;
+            if (idx < nsc) sc_l[idx] = scv[i];
+        }
+    }
 
     // 4. MFMAs
     const bool tok_ok = r16 < a.M;
     const int8_t *xl = lds_x + (tok_ok ? r16 : 0) * p.ldl;
-    float F[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     v4i C = {0, 0, 0, 0};
     for (int j0 = 0; j0 < nj; j0 += MS) {
         if (j0 > 0) load_chunk(j0);
@@ -550,7 +587,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
             if (j0 + j >= nj) break;
             const int st = kw + (j0 + j) * ks;
             long bop[GE::NMF];
-            decode<FMT, UD>(wv[j], bop);
+            decode<FMT, UD>(wq[j], bop);
             if constexpr (FMT == kTern) {
 #pragma unroll
                 for (int grp = 0; grp < 2; ++grp) {
@@ -566,16 +603,16 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
                     for (int i = 0; i < UD; ++i) c = mfma(aop[i], bop[grp * UD + i], c);
                     if constexpr (GROUPED) {
                         const int gi = 2 * st + grp;
-                        const float scv = gi < a.G ? sc[j][grp] : 0.0f;
+                        if (gi < a.G) {
 #pragma unroll
-                        for (int vv = 0; vv < 4; ++vv) {
-                            const int g_acc = c[vv] >> GE::SHIFT;
-                            if constexpr (ACC) {
+                            for (int vv = 0; vv < 4; ++vv) {
                                 const int tok = 4 * s + vv;
-                                if (row_ok && tok < a.M && gi < a.G)
-                                    a.acc[((size_t)tok * a.N + row) * a.G + gi] = g_acc;
-                            } else {
-                                F[vv] = fmaf((float)g_acc, scv, F[vv]);
+                                if (tok < a.M && (!ACC || row_ok)) {
+                                    if constexpr (ACC)
+                                        a.acc[((size_t)tok * a.N + row) * a.G + gi] = c[vv] >> GE::SHIFT;
+                                    else
+                                        acc_l[(tok * TR + 16 * rt + r16) * gld + gi] = c[vv] >> GE::SHIFT;
+                                }
                             }
                         }
                     } else {
@@ -597,45 +634,59 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     }
     if constexpr (GROUPED && ACC) return;
 
-    // 5. K-split reduction (waves kw > 0 -> wave 0, added in wave order) and epilogue
-    if (ks > 1) {
-        if (kw > 0) {
-#pragma unroll
-            for (int vv = 0; vv < 4; ++vv)
-                red[((kw - 1) * 4 + vv) * 64 + lane] = GROUPED ? F[vv] : __int_as_float(C[vv]);
-        }
+    if constexpr (GROUPED) {
+        // 5. group combine, in group order for every (token, row): t = fmaf((float)acc_g, s[r,g], t); the
+        // result does not depend on how the steps were split over waves.
         __syncthreads();
-        if (kw > 0) return;
-        for (int k = 0; k < ks - 1; ++k)
-#pragma unroll
-            for (int vv = 0; vv < 4; ++vv) {
-                const float r = red[(k * 4 + vv) * 64 + lane];
-                if constexpr (GROUPED)
-                    F[vv] += r;
-                else
-                    C[vv] += __float_as_int(r);
+        for (int c = threadIdx.x; c < TR * a.M; c += blockDim.x) {
+            const int tok = c / TR, r = c % TR, orow = row0 + r;
+            if (orow >= a.N) continue;
+            const int32_t *ap = acc_l + (tok * TR + r) * gld;
+            const float *sp = sc_l + r * a.G;
+            float t = 0.0f;
+            int g = 0;
+            for (; g + 4 <= a.G; g += 4) {
+                const int4 a4 = *reinterpret_cast<const int4 *>(ap + g);
+                t = fmaf((float)a4.x, sp[g], t);
+                t = fmaf((float)a4.y, sp[g + 1], t);
+                t = fmaf((float)a4.z, sp[g + 2], t);
+                t = fmaf((float)a4.w, sp[g + 3], t);
             }
-    }
-    if (!row_ok) return;
-    const float rs = (!GROUPED && a.scales) ? a.scales[row] : 1.0f;
-    const float bb = a.bias ? a.bias[row] : 0.0f;
+            for (; g < a.G; ++g) t = fmaf((float)ap[g], sp[g], t);
+            float out = t * xs_l[tok];
+            if (a.bias) out = out + a.bias[orow];
+            a.y[(size_t)tok * a.ldy + orow] = out;
+        }
+        return;
+    } else {
+        // 5. K-split reduction of the exact int32 sums (waves with kw > 0 -> the kw == 0 wave of the tile)
+        if (ks > 1) {
+            if (kw > 0) {
 #pragma unroll
-    for (int vv = 0; vv < 4; ++vv) {
-        const int tok = 4 * s + vv;
-        if (tok >= a.M) continue;
-        float out;
-        if constexpr (GROUPED) {
-            out = F[vv] * xs_l[tok];
-        } else {
+                for (int vv = 0; vv < 4; ++vv) red[(((kw - 1) * RT + rt) * 4 + vv) * 64 + lane] = C[vv];
+            }
+            __syncthreads();
+            if (kw > 0) return;
+            for (int k = 0; k < ks - 1; ++k)
+#pragma unroll
+                for (int vv = 0; vv < 4; ++vv) C[vv] += red[((k * RT + rt) * 4 + vv) * 64 + lane];
+        }
+        if (!row_ok) return;
+        const float rs = a.scales ? a.scales[row] : 1.0f;
+        const float bb = a.bias ? a.bias[row] : 0.0f;
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv) {
+            const int tok = 4 * s + vv;
+            if (tok >= a.M) continue;
             const int isum = C[vv] >> GE::SHIFT;
             if constexpr (ACC) {
                 a.acc[(size_t)tok * a.N + row] = isum;
                 continue;
             }
-            out = ((float)isum * xs_l[tok]) * rs;
+            float out = ((float)isum * xs_l[tok]) * rs;
+            if (a.bias) out = out + bb;
+            a.y[(size_t)tok * a.ldy + row] = out;
         }
-        if (a.bias) out = out + bb;
-        a.y[(size_t)tok * a.ldy + row] = out;
     }
 }
 
@@ -716,7 +767,8 @@ struct eif_hip_qweight {
 namespace {
 
 int g_gemm_min_tokens = 16;
-int g_gemv_ksplit = 0;   // 0 = pick_ksplit()
+int g_gemv_ksplit = 0;   // waves per row tile of the GEMV, 0 = pick_ks_gemv()
+int g_gemv_rt = 0;       // row tiles per workgroup of the GEMV, 0 = chosen from the shape
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
 
@@ -747,51 +799,124 @@ int pick_ks_gemv(int row_tiles, int nsteps)
     return ks > 16 ? 16 : (ks < 1 ? 1 : ks);
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW>
+// Dynamic LDS of qgemv_kernel: the staged int8 rows, then the group sums and scales (grouped) or the K-split
+// partials (row-scaled).
+size_t gemv_lds_bytes(bool grouped, const QArgs &a, int ldl, int rt, int ks)
+{
+    const size_t tr = 16 * (size_t)rt, gld = (size_t)((a.G + 3) & ~3);
+    const size_t tail = grouped ? ((size_t)a.M * tr * gld + tr * (size_t)a.G) * 4 : (size_t)(ks - 1) * rt * 4 * 64 * 4;
+    return (size_t)a.M * ldl + tail;
+}
+// LDS a workgroup may allocate on the current device (160 KiB on gfx950), read once per process.
+size_t gemv_max_lds()
+{
+    static const size_t bytes = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            return (size_t)65536;
+        return (size_t)v;
+    }();
+    return bytes - 256;   // the kernel's static LDS (xs_l, red_max)
+}
+
+// Launch shapes compiled for every step count and tile count: the BitNet group layouts (g96, g128), INT4 and
+// INT8. The other ternary layouts get one shape (one tile per workgroup, SMAX steps per wave, block at run time).
+template <int FMT, int UD, bool GROUPED>
+constexpr bool gemv_tuned() { return FMT != kTern || (GROUPED && (UD == 3 || UD == 4)); }
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT>
 int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
-    const size_t lds = (size_t)a.M * p.ldl + (size_t)(ks - 1) * 4 * 64 * sizeof(float);
-    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW><<<rows_pad / 16, 64 * ks, lds, st>>>(a, p);
+    const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
+    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT><<<rows_pad / (16 * RT), 64 * RT * ks, lds, st>>>(a, p);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
 int launch_gemv_e(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
-    const int steps = eif_ceil_div(a.nsteps, ks);
     constexpr int SMAX = Geo<FMT, UD>::SB >= 32 ? 4 : 8;   // 8-dword steps: half the registers per chunk
-    if constexpr (ACC) {
-        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX>(a, p, rows_pad, ks, st);
+    const int steps = eif_ceil_div(a.nsteps, ks);
+    if constexpr (ACC || !gemv_tuned<FMT, UD, GROUPED>()) {
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT>(a, p, rows_pad, ks, st);
     } else {
-        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1>(a, p, rows_pad, ks, st);
-        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2>(a, p, rows_pad, ks, st);
-        if (steps <= 4 || SMAX == 4) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4>(a, p, rows_pad, ks, st);
-        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX>(a, p, rows_pad, ks, st);
+        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1, LB, RT>(a, p, rows_pad, ks, st);
+        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2, LB, RT>(a, p, rows_pad, ks, st);
+        if (steps <= 4 || SMAX == 4) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4, LB, RT>(a, p, rows_pad, ks, st);
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT>(a, p, rows_pad, ks, st);
     }
 }
 
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB>
+int launch_gemv_rt(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int ks, hipStream_t st)
+{
+    if constexpr (gemv_tuned<FMT, UD, GROUPED>())
+        if (rt == 4) return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 4>(a, p, rows_pad, ks, st);
+    return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 1>(a, p, rows_pad, ks, st);
+}
+
+// Fused prep: E columns per thread. The WHT-128 of the BitNet configurations is compiled with the block
+// fixed; other blocks read it at run time.
+template <int FMT, int UD, bool GROUPED, bool ACC, int E>
+int launch_gemv_fused(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int ks, hipStream_t st)
+{
+    if constexpr (E <= 8 && gemv_tuned<FMT, UD, GROUPED>())
+        if (p.block == 128) return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 7>(a, p, rows_pad, rt, ks, st);
+    return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, -1>(a, p, rows_pad, rt, ks, st);
+}
+
 // Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses qlinear_kernel).
+// Shape: four row tiles per workgroup for matrices of 768 tiles or more (fewer workgroups repeat the
+// activation prep and staging), ks waves per tile from pick_ks_gemv, raised until the threads cover the row
+// (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, hipStream_t st)
+{
+    const int kpad = a.nsteps * Geo<FMT, UD>::SC;
+    const int maxks = 16 / rt;
+    int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(rows_pad / 16, a.nsteps);
+    if (ks > maxks) ks = maxks;
+    auto scales_fit = [&](int k) { return !GROUPED || ACC || a.G <= kMaxScLoads * 4 * k; };
+    auto lds_fit = [&](int k) { return gemv_lds_bytes(GROUPED, a, p.ldl, rt, k) <= gemv_max_lds(); };
+    if (p.x) {
+        // E columns per thread: the fewest that let at most 16 waves cover the padded row (short per-thread
+        // chains), and a WHT block within one wave.
+        for (int e = 4; e <= 16; e *= 2) {
+            if (64 * e < p.block) continue;
+            int k = ks;
+            while (k < maxks && (64 * rt * k * e < kpad || !scales_fit(k))) ++k;
+            if (64 * rt * k * e < kpad || !scales_fit(k)) continue;
+            if (!lds_fit(k)) return EIF_HIP_E_LIMIT;
+            if (e == 4) return launch_gemv_fused<FMT, UD, GROUPED, ACC, 4>(a, p, rows_pad, rt, k, st);
+            if (e == 8) return launch_gemv_fused<FMT, UD, GROUPED, ACC, 8>(a, p, rows_pad, rt, k, st);
+            return launch_gemv_fused<FMT, UD, GROUPED, ACC, 16>(a, p, rows_pad, rt, k, st);
+        }
+        return EIF_HIP_E_LIMIT;
+    }
+    while (ks < maxks && (a.M * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks))) ++ks;
+    if (a.M * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks) || !lds_fit(ks)) return 1;
+    return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0>(a, p, rows_pad, rt, ks, st);
+}
+
+// Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses qlinear_kernel).
+// Shape: four row tiles per workgroup for matrices of 768 tiles or more (fewer workgroups repeat the
+// activation prep and staging), else one; ks waves per tile from pick_ks_gemv, raised until the threads cover
+// the row (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
+// A shape that does not fit with four tiles is launched with one.
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemv(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
 {
-    const int kpad = a.nsteps * Geo<FMT, UD>::SC;
-    p.ldl = kpad + 16;
-    int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(rows_pad / 16, a.nsteps);
-    if (p.x) {
-        // E columns per thread: the whole padded row covered, and a WHT block within one wave
-        for (;; ++ks) {
-            if (ks > 16) return EIF_HIP_E_LIMIT;
-            for (int e = 8; e <= 16; e *= 2)
-                if (64 * ks * e >= kpad && 64 * e >= p.block) {
-                    if (e == 8) return launch_gemv_e<FMT, UD, GROUPED, ACC, 8>(a, p, rows_pad, ks, st);
-                    return launch_gemv_e<FMT, UD, GROUPED, ACC, 16>(a, p, rows_pad, ks, st);
-                }
-        }
+    p.ldl = a.nsteps * Geo<FMT, UD>::SC + 16;
+    int rt = 1;
+    if constexpr (gemv_tuned<FMT, UD, GROUPED>())
+        rt = g_gemv_rt > 0 ? g_gemv_rt : (rows_pad / 16 >= 768 ? 4 : 1);
+    if (rt > 1) {
+        const int rc = launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, rt, st);
+        if (rc == EIF_HIP_OK || rc == EIF_HIP_E_DEVICE) return rc;
     }
-    while (ks < 16 && a.M * (kpad / 16) > kMaxPieces * 64 * ks) ++ks;
-    if (a.M * (kpad / 16) > kMaxPieces * 64 * ks) return 1;
-    return launch_gemv_e<FMT, UD, GROUPED, ACC, 0>(a, p, rows_pad, ks, st);
+    return launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, 1, st);
 }
 
 template <int FMT, int UD, bool GROUPED, bool ACC>
@@ -802,7 +927,8 @@ int launch_shape(const QArgs &a, const PrepArgs &p, int rows_pad, int path, hipS
         if (rc != 1) return rc;
     }
     if (path == EIF_HIP_PATH_GEMM) return launch_one<FMT, UD, GROUPED, ACC, 4, 4, 1, false>(a, rows_pad, st);
-    const int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ksplit(rows_pad / 16, a.nsteps);
+    // grouped: one wave per tile walks all steps, so a row's groups combine in group order
+    const int ks = GROUPED ? 1 : (g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ksplit(rows_pad / 16, a.nsteps));
     if constexpr (ACC) {
         return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 4, false>(a, rows_pad, st);
     } else {
@@ -956,6 +1082,13 @@ int eif_hip_set_gemv_ksplit(int k)
     return old;
 }
 
+int eif_hip_set_gemv_row_tiles(int rt)
+{
+    int old = g_gemv_rt;
+    if (rt == 0 || rt == 1 || rt == 4) g_gemv_rt = rt;
+    return old;
+}
+
 int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, int group, const void *codes,
                            const float *scales, int src_on_device, void *stream)
 {
@@ -996,7 +1129,7 @@ int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, i
     if (!src_on_device) {
         if (hipMalloc(&src_dev, src_bytes) != hipSuccess) return EIF_HIP_E_NOMEM;
         if (hipMemcpyAsync(src_dev, codes, src_bytes, hipMemcpyHostToDevice, st) != hipSuccess) {
-            hipFree(src_dev);
+            (void)hipFree(src_dev);
             return EIF_HIP_E_DEVICE;
         }
     }
@@ -1029,17 +1162,17 @@ int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, i
         }
         if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) rc = EIF_HIP_E_DEVICE;
     }
-    if (src_dev) hipFree(src_dev);
+    if (src_dev) (void)hipFree(src_dev);
     if (rc != EIF_HIP_OK) {
-        if (q.w) hipFree(q.w);
-        if (q.scales) hipFree(q.scales);
+        if (q.w) (void)hipFree(q.w);
+        if (q.scales) (void)hipFree(q.scales);
         return rc;
     }
     q.bytes = wbytes + (scales ? sizeof(float) * sc_count : 0);
     eif_hip_qweight *h = new (std::nothrow) eif_hip_qweight(q);
     if (!h) {
-        hipFree(q.w);
-        if (q.scales) hipFree(q.scales);
+        (void)hipFree(q.w);
+        if (q.scales) (void)hipFree(q.scales);
         return EIF_HIP_E_NOMEM;
     }
     *out = h;
@@ -1049,8 +1182,8 @@ int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, i
 void eif_hip_qweight_destroy(eif_hip_qweight *w)
 {
     if (!w) return;
-    if (w->w) hipFree(w->w);
-    if (w->scales) hipFree(w->scales);
+    if (w->w) (void)hipFree(w->w);
+    if (w->scales) (void)hipFree(w->scales);
     delete w;
 }
 

@@ -110,9 +110,13 @@ void eif_hip_forget_host_weights(const void *host_ptr);
 int eif_hip_set_gemm_min_tokens(int m);
 int eif_hip_gemm_min_tokens(void);
 
-/* Waves that split one 16-row tile's columns in the GEMV (1, 2, 4 or 8; 0 = chosen from the shape, the
- * default); returns the previous setting. A tuning knob: results do not depend on it.                   */
+/* Waves that split one 16-row tile's columns in the GEMV (1..16; 0 = chosen from the shape, the default);
+ * returns the previous setting. A tuning knob: results do not depend on it.                              */
 int eif_hip_set_gemv_ksplit(int k);
+
+/* 16-row tiles per workgroup of the GEMV (1 or 4; 0 = chosen from the shape, the default); returns the
+ * previous setting. A tuning knob: results do not depend on it.                                          */
+int eif_hip_set_gemv_row_tiles(int rt);
 
 #ifdef __cplusplus
 }

@@ -1,8 +1,8 @@
 """INT8-activation linears (MFMA GEMV and GEMM paths) against the oracle.
 
 Integer accumulators are compared bit for bit; row-scaled outputs bit for bit (same epilogue order as the
-reference build); group-scaled FP32 outputs to 1e-5 relative to sum_g |s*acc_g|*xs + |bias| (the group partial
-sums are combined in a different order on the GPU).
+reference build); group-scaled FP32 outputs to 1e-5 relative to sum_g |s*acc_g|*xs + |bias| and, since the
+kernels combine a row's groups in group order as the oracle does, bit for bit.
 """
 import numpy as np
 import pytest
@@ -79,7 +79,49 @@ def test_ternary_grouped(gpu, oracle, N, K, g, M, path):
         mag = mag + np.abs(bias)[None, :]
     err = np.abs(y.astype(np.float64) - oy) / (mag + 1e-30)
     assert np.all(np.isfinite(y)) and err.max() <= REL_TOL, err.max()
+    # the small-batch GEMV and the GEMM both combine the groups of a row in group order, as the oracle does
+    assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
     qw.close()
+
+
+@pytest.mark.parametrize("N,K,g", [(3072, 2560, 128), (1024, 6912, 96), (200, 2560, 128)])
+def test_gemv_shape_knobs(gpu, oracle, N, K, g):
+    """Row tiles per workgroup and waves per tile change the launch, never the result (y, acc, fused y)."""
+    import torch
+    dev = torch.device("cuda:0")
+    lib = gpu.load()
+    w, s = synth.ternary_weight((58, N, K, g), N, K, g)
+    qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+    ng = -(-K // g)
+    norm = gpu.wht_norm(128)
+    ref = None
+    try:
+        for M in (1, 5):
+            x = synth.activations((59, M, K), M, K)
+            xd = torch.from_numpy(x).to(dev)
+            xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+            oy = np.zeros((M, N), np.float32)
+            oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
+            oacc = np.zeros((M, N, ng), np.int32)
+            oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+            ref = None
+            for rt, ks in [(0, 0), (1, 0), (4, 0), (1, 2), (4, 2), (1, 16), (4, 4), (1, 1)]:
+                lib.eif_hip_set_gemv_row_tiles(rt)
+                lib.eif_hip_set_gemv_ksplit(ks)
+                y = run_linear(gpu, qw, xq_d, xs_d, M, GEMV)
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (M, rt, ks)
+                acc = run_acc(gpu, qw, xq_d, M, (M, N, ng), GEMV)
+                assert np.array_equal(acc, oacc), (M, rt, ks)
+                yf = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+                qw.linear_f32(xd, yf, 128, norm)
+                yf = yf.cpu().numpy()
+                if ref is None:
+                    ref = yf
+                assert np.array_equal(yf.view(np.uint32), ref.view(np.uint32)), (M, rt, ks)
+    finally:
+        lib.eif_hip_set_gemv_row_tiles(0)
+        lib.eif_hip_set_gemv_ksplit(0)
+        qw.close()
 
 
 @pytest.mark.parametrize("N,K,M,path,with_bias", [
