@@ -27,8 +27,11 @@
 //                     wave, partial F of the K-split waves added in wave order; y = F * xs[m] (+ bias).
 //   row-scaled:       isum = exact int32 over all K (K-split partials added as integers);
 //                     y = ((float)isum * xs[m]) * s[r] (+ bias).
+#include <algorithm>
 #include <mutex>
 #include <new>
+#include <type_traits>
+#include <unordered_map>
 
 #include "hip_common.h"
 
@@ -115,6 +118,33 @@ EIF_DEV void decode(const uint32_t (&w)[Geo<FMT, UD>::SB / 4], long (&b)[Geo<FMT
 
 EIF_DEV v4i mfma(long a, long b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0); }
 
+// Two 8-byte operands of the same lane concatenated into one 16-byte operand of v_mfma_i32_16x16x64_i8: A and
+// B are concatenated alike, so the product is the sum of the two 16x16x32 products (the gfx950 double-rate
+// form; a pair never spans two groups because it is formed inside one group's operands).
+EIF_DEV v4i mfma64(long a0, long a1, long b0, long b1, v4i c)
+{
+    const v4i a = {(int)a0, (int)(a0 >> 32), (int)a1, (int)(a1 >> 32)};
+    const v4i b = {(int)b0, (int)(b0 >> 32), (int)b1, (int)(b1 >> 32)};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// c += sum_i a[i] * b[OFF + i] over the N operands of a: an even count in pairs on the 64-deep form, an odd
+// count on the 32-deep form throughout (an accumulation chain never mixes the two forms: a 64-deep result fed
+// straight into a dependent 32-deep MFMA gave wrong sums on gfx950). Array references with a compile-time
+// offset keep both operand arrays in registers.
+template <int OFF, int N, int NB>
+EIF_DEV v4i mfma_ops(const long (&a)[N], const long (&b)[NB], v4i c)
+{
+    if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2) c = mfma64(a[i], a[i + 1], b[OFF + i], b[OFF + i + 1], c);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) c = mfma(a[i], b[OFF + i], c);
+    }
+    return c;
+}
+
 // Kernel parameters.
 struct QArgs {
     const uint8_t *W;      // GPU layout, rows padded to kRowPad
@@ -129,32 +159,71 @@ struct QArgs {
     int ldy;
     int32_t *acc;          // parity output or NULL
     int M, N, nsteps;
+    float *part;           // GEMM split along K: partial sums [split][M][N]
 };
 
-// RT row tiles x TT token tiles per workgroup, KSPLIT waves share a row tile and split its steps.
-// V1: only token 0 is live (M == 1), so only accumulator register 0 is converted.
-template <int FMT, int UD, bool GROUPED, bool ACC, int RT, int TT, int KSPLIT, bool V1>
-__global__ __launch_bounds__(64 * RT * KSPLIT) void qlinear_kernel(QArgs a)
+// ---- tiled GEMM (token batches above the small-batch GEMV) ----
+//
+// Workgroup: 4 waves, 64 rows x 16*TT tokens; wave w owns rows 16w..16w+15 for all TT token tiles and walks
+// every step of K in order. Per step the workgroup stages the activation block [16*TT tokens x SC columns] in
+// LDS (double-buffered, two steps of loads in flight), each wave loads its own weight codes and scales two
+// steps ahead, decodes them once and reuses them for the TT token tiles. Grouped ternary: each group's exact
+// int32 sum is combined at once, in group order, into FP32 accumulators (the same sequence as the oracle);
+// row-scaled: one int32 sum over K.
+constexpr int kGemmThreads = 256;
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
+__global__ __launch_bounds__(kGemmThreads) void qgemm_kernel(QArgs a)
 {
     using GE = Geo<FMT, UD>;
-    constexpr int NV = V1 ? 1 : 4;
     constexpr int NW = GE::SB / 4;
+    constexpr int TM = 16 * TT;                    // tokens per workgroup
+    constexpr int PR = GE::SC / 16;                // 16-byte pieces per token per step
+    constexpr int PPT = (TM * PR + kGemmThreads - 1) / kGemmThreads;
+    constexpr int LDA = GE::SC + 16;               // LDS row stride of the staged block
+    __shared__ __align__(16) int8_t xa[2][TM * LDA];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int kw = wave % KSPLIT, rw = wave / KSPLIT;
     const int r16 = lane & 15, s = lane >> 4;
-    const int row = (blockIdx.x * RT + rw) * 16 + r16;
-    const int m0 = blockIdx.y * (16 * TT);
+    const int row = blockIdx.x * 64 + wave * 16 + r16;   // < rows_pad
     const bool row_ok = row < a.N;
+    const int row_c = row_ok ? row : a.N - 1;
+    const int m0 = blockIdx.y * TM;
+    // split along K (gridDim.z > 1): this workgroup's steps [s0, s0 + ns)
+    const int s0 = (int)(blockIdx.z * a.nsteps / gridDim.z);
+    const int ns = (int)((blockIdx.z + 1) * a.nsteps / gridDim.z) - s0;
 
+    v4i ra[2][PPT];   // a clang vector type: an array of HIP's int4 structs would live in scratch
+    uint32_t wb[2][NW];
+    float sc[2][2];
     const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
-    const int8_t *xp[TT];
-    bool tok_ok[TT];
+    auto load_step = [&](int st, v4i (&r)[PPT], uint32_t (&w)[NW], float (&c)[2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt) {
-        const int tok = m0 + 16 * tt + r16;
-        tok_ok[tt] = tok < a.M;
-        xp[tt] = a.xq + (size_t)(tok_ok[tt] ? tok : 0) * a.ldq;
-    }
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * kGemmThreads;
+            const int t = pc / PR, q = pc - t * PR;
+            const int tok = m0 + (t < TM ? t : TM - 1);
+            r[i] = *reinterpret_cast<const v4i *>(a.xq + (size_t)(tok < a.M ? tok : a.M - 1) * a.ldq +
+                                                    (size_t)st * GE::SC + 16 * q);
+        }
+        load_words<NW>(wp + (size_t)st * 4 * GE::SB, w);
+        if constexpr (GROUPED) {
+#pragma unroll
+            for (int grp = 0; grp < 2; ++grp) {
+                const int gi = 2 * st + grp;
+                c[grp] = a.scales[(size_t)row_c * a.G + (gi < a.G ? gi : a.G - 1)];
+            }
+        }
+    };
+    auto store_step = [&](int b, const v4i (&r)[PPT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * kGemmThreads;
+            if (PPT * kGemmThreads == TM * PR || pc < TM * PR) {
+                const int t = pc / PR, q = pc - t * PR;
+                *reinterpret_cast<v4i *>(&xa[b][t * LDA + 16 * q]) = r[i];
+            }
+        }
+    };
 
     float F[TT][4];
     v4i C[TT];
@@ -165,92 +234,77 @@ __global__ __launch_bounds__(64 * RT * KSPLIT) void qlinear_kernel(QArgs a)
         for (int v = 0; v < 4; ++v) F[tt][v] = 0.0f;
     }
 
-#pragma unroll 2
-    for (int st = kw; st < a.nsteps; st += KSPLIT) {
-        uint32_t wv[NW];
-        load_words<NW>(wp + (size_t)st * 4 * GE::SB, wv);
+    auto compute = [&](int b, int st, const uint32_t (&w)[NW], const float (&c)[2]) __attribute__((always_inline)) {
         long bop[GE::NMF];
-        decode<FMT, UD>(wv, bop);
-        if constexpr (FMT == kTern) {
+        decode<FMT, UD>(w, bop);
 #pragma unroll
-            for (int grp = 0; grp < 2; ++grp) {
-                const int gi = 2 * st + grp;
-                float sc = 0.0f;
-                if constexpr (GROUPED) {
-                    if (row_ok && gi < a.G) sc = a.scales[(size_t)row * a.G + gi];
-                }
-                const int col = st * GE::SC + 32 * UD * grp + 8 * UD * s;
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt) {
+        for (int tt = 0; tt < TT; ++tt) {
+            const int8_t *xl = &xa[b][(16 * tt + r16) * LDA];
+            if constexpr (FMT == kTern) {
+                auto group = [&](auto grp_c) __attribute__((always_inline)) {
+                    constexpr int grp = decltype(grp_c)::value;
                     long aop[UD];
-                    if (tok_ok[tt]) {
-                        load_ops<UD, (UD % 2 == 0)>(xp[tt] + col, aop);
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < UD; ++i) aop[i] = 0;
-                    }
-                    v4i c = GROUPED ? v4i{0, 0, 0, 0} : C[tt];
-#pragma unroll
-                    for (int i = 0; i < UD; ++i) c = mfma(aop[i], bop[grp * UD + i], c);
+                    load_ops<UD, (UD % 2 == 0)>(xl + 32 * UD * grp + 8 * UD * s, aop);
+                    v4i cc = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C[tt]);
                     if constexpr (GROUPED) {
+                        const int gi = 2 * st + grp;
+                        if (gi < a.G) {
 #pragma unroll
-                        for (int v = 0; v < NV; ++v) {
-                            const int g_acc = c[v] >> GE::SHIFT;
-                            if constexpr (ACC) {
-                                const int tok = m0 + 16 * tt + 4 * s + v;
-                                if (row_ok && tok < a.M && gi < a.G)
-                                    a.acc[((size_t)tok * a.N + row) * a.G + gi] = g_acc;
-                            } else {
-                                F[tt][v] = fmaf((float)g_acc, sc, F[tt][v]);
+                            for (int v = 0; v < 4; ++v) {
+                                const int g_acc = cc[v] >> GE::SHIFT;
+                                if constexpr (ACC) {
+                                    const int tok = m0 + 16 * tt + 4 * s + v;
+                                    if (row_ok && tok < a.M) a.acc[((size_t)tok * a.N + row) * a.G + gi] = g_acc;
+                                } else {
+                                    F[tt][v] = fmaf((float)g_acc, c[grp], F[tt][v]);
+                                }
                             }
                         }
                     } else {
-                        C[tt] = c;
+                        C[tt] = cc;
                     }
-                }
-            }
-        } else {
-            const int col = st * GE::SC + (GE::SC / 4) * s;
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
+                };
+                group(std::integral_constant<int, 0>{});
+                group(std::integral_constant<int, 1>{});
+            } else {
                 long aop[GE::NMF];
-                if (tok_ok[tt]) {
-                    load_ops<GE::NMF, true>(xp[tt] + col, aop);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < GE::NMF; ++i) aop[i] = 0;
-                }
-#pragma unroll
-                for (int i = 0; i < GE::NMF; ++i) C[tt] = mfma(aop[i], bop[i], C[tt]);
+                load_ops<GE::NMF, true>(xl + (GE::SC / 4) * s, aop);
+                C[tt] = mfma_ops<0>(aop, bop, C[tt]);
             }
         }
-    }
+    };
 
+    load_step(s0, ra[0], wb[0], sc[0]);
+    if (ns > 1) load_step(s0 + 1, ra[1], wb[1], sc[1]);
+    store_step(0, ra[0]);
+    __syncthreads();
+    for (int j = 0; j < ns; j += 2) {
+        compute(0, s0 + j, wb[0], sc[0]);
+        if (j + 2 < ns) load_step(s0 + j + 2, ra[0], wb[0], sc[0]);
+        if (j + 1 < ns) store_step(1, ra[1]);
+        __syncthreads();
+        if (j + 1 >= ns) break;
+        compute(1, s0 + j + 1, wb[1], sc[1]);
+        if (j + 3 < ns) load_step(s0 + j + 3, ra[1], wb[1], sc[1]);
+        if (j + 2 < ns) store_step(0, ra[0]);
+        __syncthreads();
+    }
     if constexpr (GROUPED && ACC) return;
 
-    // K-split reduction through LDS (waves kw > 0 hand their partials to wave kw == 0 of the same row tile).
-    if constexpr (KSPLIT > 1) {
-        __shared__ float red[RT][KSPLIT - 1][TT][NV][64];
-        if (kw > 0) {
+    if (gridDim.z > 1) {
+        // Split along K: the partial sums of this split (FP32 group combines, or the exact int32 sums) go to
+        // part[split][token][row]; qgemm_reduce_kernel adds them in split order and applies the epilogue.
+        if (!row_ok) return;
+        float *pz = a.part + (size_t)blockIdx.z * a.M * a.N;
 #pragma unroll
-            for (int tt = 0; tt < TT; ++tt)
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-                for (int v = 0; v < NV; ++v)
-                    red[rw][kw - 1][tt][v][lane] = GROUPED ? F[tt][v] : __int_as_float(C[tt][v]);
-        }
-        __syncthreads();
-        if (kw > 0) return;
-#pragma unroll
-        for (int k = 0; k < KSPLIT - 1; ++k)
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-                for (int v = 0; v < NV; ++v) {
-                    if constexpr (GROUPED)
-                        F[tt][v] += red[rw][k][tt][v][lane];
-                    else
-                        C[tt][v] += __float_as_int(red[rw][k][tt][v][lane]);
-                }
+            for (int v = 0; v < 4; ++v) {
+                const int tok = m0 + 16 * tt + 4 * s + v;
+                if (tok < a.M)
+                    pz[(size_t)tok * a.N + row] = GROUPED ? F[tt][v] : __int_as_float(C[tt][v] >> GE::SHIFT);
+            }
+        return;
     }
 
     if (!row_ok) return;
@@ -259,7 +313,7 @@ __global__ __launch_bounds__(64 * RT * KSPLIT) void qlinear_kernel(QArgs a)
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
+        for (int v = 0; v < 4; ++v) {
             const int tok = m0 + 16 * tt + 4 * s + v;
             if (tok >= a.M) continue;
             float out;
@@ -276,6 +330,27 @@ __global__ __launch_bounds__(64 * RT * KSPLIT) void qlinear_kernel(QArgs a)
             if (a.bias) out = out + bb;
             a.y[(size_t)tok * a.ldy + row] = out;
         }
+}
+
+// Sum of the splits of a split GEMM, in split order, and the epilogue: one thread per (token, row).
+template <bool GROUPED>
+__global__ __launch_bounds__(256) void qgemm_reduce_kernel(QArgs a, int ks)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, mn = (size_t)a.M * a.N;
+    if (i >= mn) return;
+    const int tok = (int)(i / a.N), row = (int)(i % a.N);
+    float out;
+    if constexpr (GROUPED) {
+        float t = a.part[i];
+        for (int z = 1; z < ks; ++z) t += a.part[z * mn + i];
+        out = t * a.xs[tok];
+    } else {
+        int isum = __float_as_int(a.part[i]);
+        for (int z = 1; z < ks; ++z) isum += __float_as_int(a.part[z * mn + i]);
+        out = ((float)isum * a.xs[tok]) * (a.scales ? a.scales[row] : 1.0f);
+    }
+    if (a.bias) out = out + a.bias[row];
+    a.y[(size_t)tok * a.ldy + row] = out;
 }
 
 // ---- small-batch GEMV (M <= kGemvMaxM): RT 16-row tiles per workgroup, ks waves per tile ----
@@ -772,21 +847,78 @@ int g_gemv_rt = 0;       // row tiles per workgroup of the GEMV, 0 = chosen from
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int RT, int TT, int KSPLIT, bool V1>
-int launch_one(const QArgs &a, int rows_pad, hipStream_t st)
+// Per-stream workspace of the GEMM's split along K (launches on one stream run in order, so one buffer per
+// stream suffices), grown outside graph capture. Buffers are never freed before the process ends, also when
+// replaced by larger ones: a graph captured on the stream keeps using the buffers it was captured with.
+std::mutex g_ws_mu;
+std::unordered_map<hipStream_t, std::pair<float *, size_t>> g_ws;
+
+float *split_ws(hipStream_t st, size_t bytes)
 {
-    dim3 grid(rows_pad / (16 * RT), eif_ceil_div(a.M, 16 * TT));
-    qlinear_kernel<FMT, UD, GROUPED, ACC, RT, TT, KSPLIT, V1><<<grid, 64 * RT * KSPLIT, 0, st>>>(a);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto &w = g_ws[st];
+    if (w.second < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+        float *p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+        w = {p, bytes};   // the old buffer stays allocated
+    }
+    return w.first;
+}
+
+int device_cus()
+{
+    static const int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+            return 256;
+        return v;
+    }();
+    return n;
+}
+
+int g_gemm_split = 0;   // splits along K of the GEMM, 0 = chosen from the shape
+
+// Splits along K: enough workgroups for two per CU when the tiles alone are fewer than one per CU, at least
+// three steps per split, at most 16; 1 for the parity outputs and when no workspace can be had (first use of
+// a stream inside a graph capture).
+template <bool ACC>
+int pick_split(QArgs &a, int tiles, hipStream_t st)
+{
+    if (ACC) return 1;
+    int ks = g_gemm_split;
+    if (ks == 0) ks = tiles < device_cus() ? eif_ceil_div(2 * device_cus(), tiles) : 1;
+    ks = std::min(ks, std::min(16, std::max(1, a.nsteps / 3)));
+    if (ks <= 1) return 1;
+    a.part = split_ws(st, (size_t)ks * a.M * a.N * sizeof(float));
+    return a.part ? ks : 1;
+}
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
+int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
+{
+    const int tm = eif_ceil_div(a.M, 16 * TT), tiles = rows_pad / 64 * tm;
+    const int ks = pick_split<ACC>(a, tiles, st);
+    dim3 grid(rows_pad / 64, tm, ks);
+    qgemm_kernel<FMT, UD, GROUPED, ACC, TT><<<grid, kGemmThreads, 0, st>>>(a);
     EIF_HIP_LAUNCHED();
+    if (ks > 1) {
+        const size_t mn = (size_t)a.M * a.N;
+        qgemm_reduce_kernel<GROUPED><<<(unsigned)((mn + 255) / 256), 256, 0, st>>>(a, ks);
+        EIF_HIP_LAUNCHED();
+    }
     return EIF_HIP_OK;
 }
 
-// K-split factor for the GEMV: enough waves to cover the chip, never more than the steps of a row.
-int pick_ksplit(int row_tiles, int nsteps)
+// Token tile of the GEMM: 16, 32 or 64 tokens, the smallest that holds the batch (larger batches: 64).
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_gemm(const QArgs &a, int rows_pad, hipStream_t st)
 {
-    int k = 1;
-    while (k < 8 && row_tiles * k < 2048 && 2 * k <= nsteps) k *= 2;
-    return k;
+    if (a.M <= 16) return launch_gemm_t<FMT, UD, GROUPED, ACC, 1>(a, rows_pad, st);
+    if (a.M <= 32) return launch_gemm_t<FMT, UD, GROUPED, ACC, 2>(a, rows_pad, st);
+    return launch_gemm_t<FMT, UD, GROUPED, ACC, 4>(a, rows_pad, st);
 }
 
 // Waves per tile of the small-batch GEMV (measured on MI355X with graph-chained launches): two steps per wave
@@ -867,7 +999,7 @@ int launch_gemv_fused(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, i
     return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, -1>(a, p, rows_pad, rt, ks, st);
 }
 
-// Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses qlinear_kernel).
+// Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses the GEMM).
 // Shape: four row tiles per workgroup for matrices of 768 tiles or more (fewer workgroups repeat the
 // activation prep and staging), ks waves per tile from pick_ks_gemv, raised until the threads cover the row
 // (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
@@ -900,7 +1032,7 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0>(a, p, rows_pad, rt, ks, st);
 }
 
-// Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses qlinear_kernel).
+// Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses the GEMM).
 // Shape: four row tiles per workgroup for matrices of 768 tiles or more (fewer workgroups repeat the
 // activation prep and staging), else one; ks waves per tile from pick_ks_gemv, raised until the threads cover
 // the row (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
@@ -926,27 +1058,7 @@ int launch_shape(const QArgs &a, const PrepArgs &p, int rows_pad, int path, hipS
         const int rc = launch_gemv<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
         if (rc != 1) return rc;
     }
-    if (path == EIF_HIP_PATH_GEMM) return launch_one<FMT, UD, GROUPED, ACC, 4, 4, 1, false>(a, rows_pad, st);
-    // grouped: one wave per tile walks all steps, so a row's groups combine in group order
-    const int ks = GROUPED ? 1 : (g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ksplit(rows_pad / 16, a.nsteps));
-    if constexpr (ACC) {
-        return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 4, false>(a, rows_pad, st);
-    } else {
-        if (a.M == 1) {
-            switch (ks) {
-            case 1: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 1, true>(a, rows_pad, st);
-            case 2: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 2, true>(a, rows_pad, st);
-            case 4: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 4, true>(a, rows_pad, st);
-            default: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 8, true>(a, rows_pad, st);
-            }
-        }
-        switch (ks) {
-        case 1: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 1, false>(a, rows_pad, st);
-        case 2: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 2, false>(a, rows_pad, st);
-        case 4: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 4, false>(a, rows_pad, st);
-        default: return launch_one<FMT, UD, GROUPED, ACC, 1, 1, 8, false>(a, rows_pad, st);
-        }
-    }
+    return launch_gemm<FMT, UD, GROUPED, ACC>(a, rows_pad, st);
 }
 
 template <bool ACC>
@@ -1079,6 +1191,13 @@ int eif_hip_set_gemv_ksplit(int k)
 {
     int old = g_gemv_ksplit;
     if (k >= 0 && k <= 16) g_gemv_ksplit = k;
+    return old;
+}
+
+int eif_hip_set_gemm_split(int k)
+{
+    int old = g_gemm_split;
+    if (k >= 0 && k <= 16) g_gemm_split = k;
     return old;
 }
 

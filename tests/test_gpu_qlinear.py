@@ -79,7 +79,13 @@ def test_ternary_grouped(gpu, oracle, N, K, g, M, path):
         mag = mag + np.abs(bias)[None, :]
     err = np.abs(y.astype(np.float64) - oy) / (mag + 1e-30)
     assert np.all(np.isfinite(y)) and err.max() <= REL_TOL, err.max()
-    # the small-batch GEMV and the GEMM both combine the groups of a row in group order, as the oracle does
+    # the small-batch GEMV and the unsplit GEMM combine the groups of a row in group order, as the oracle does
+    lib = gpu.load()
+    old = lib.eif_hip_set_gemm_split(1)
+    try:
+        y = run_linear(gpu, qw, xq_d, xs_d, M, path, bias)
+    finally:
+        lib.eif_hip_set_gemm_split(old)
     assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
     qw.close()
 
@@ -121,6 +127,75 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
     finally:
         lib.eif_hip_set_gemv_row_tiles(0)
         lib.eif_hip_set_gemv_ksplit(0)
+        qw.close()
+
+
+@pytest.mark.parametrize("fmt,N,K,g,M", [("tern", 2560, 6912, 96, 64), ("tern", 640, 2560, 128, 40),
+                                          ("int8", 896, 4864, 0, 128), ("int4", 512, 1024, 0, 32)])
+def test_gemm_split(gpu, oracle, fmt, N, K, g, M):
+    """GEMM split along K: integer sums exact and row-scaled outputs bit-exact at every split; grouped FP32
+    within tolerance of the oracle, bit-exact unsplit, and the same bits on a repeated launch and on graph
+    replays (the arrival counters reset themselves)."""
+    import torch
+    lib = gpu.load()
+    if fmt == "tern":
+        w, s = synth.ternary_weight((60, N, K, g), N, K, g)
+        qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+    elif fmt == "int8":
+        w, s = synth.int8_weight((61, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+    else:
+        w, s = synth.int4_weight((62, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+    x = synth.activations((63, M, K), M, K)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    bias = synth.rng(64, N).standard_normal(N).astype(np.float32)
+    oy = np.zeros((M, N), np.float32)
+    if fmt == "tern":
+        ng = -(-K // g)
+        oacc = np.zeros((M, N, ng), np.int32)
+        oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+        oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+        mag = np.einsum("mng,ng->mn", np.abs(oacc).astype(np.float64), s.astype(np.float64)) * xs[:, None]
+        mag = mag + np.abs(bias)[None, :]
+    else:
+        wi = w.astype(np.int64) if fmt == "int8" else synth.unpack_int4(w, K).astype(np.int64)
+        oacc = (xq[:, :K].astype(np.int64) @ wi.T).astype(np.int32)
+        fn = oracle.orc_int8_gemv_i8act if fmt == "int8" else oracle.orc_int4_gemv_i8act
+        fn(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+    try:
+        for ks in (1, 2, 5, 16):
+            lib.eif_hip_set_gemm_split(ks)
+            acc = run_acc(gpu, qw, xq_d, M, oacc.shape, GEMM)
+            assert np.array_equal(acc, oacc), ks
+            y = run_linear(gpu, qw, xq_d, xs_d, M, GEMM, bias)
+            y2 = run_linear(gpu, qw, xq_d, xs_d, M, GEMM, bias)
+            assert np.array_equal(y.view(np.uint32), y2.view(np.uint32)), ks
+            if fmt != "tern" or ks == 1:
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), ks
+            else:
+                err = np.abs(y.astype(np.float64) - oy) / (mag + 1e-30)
+                assert err.max() <= REL_TOL, (ks, err.max())
+        # graph replays of a split launch
+        lib.eif_hip_set_gemm_split(5)
+        yd = torch.zeros((M, N), dtype=torch.float32, device="cuda:0")
+        bd = torch.from_numpy(bias).to("cuda:0")
+        cs = torch.cuda.Stream()
+        with torch.cuda.stream(cs):
+            qw.linear(xq_d, xs_d, yd, M=M, bias=bd, path=GEMM)
+        cs.synchronize()
+        ref = yd.cpu().numpy()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cs):
+            qw.linear(xq_d, xs_d, yd, M=M, bias=bd, path=GEMM)
+        for _ in range(4):
+            yd.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(yd.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+        del graph
+    finally:
+        lib.eif_hip_set_gemm_split(0)
         qw.close()
 
 
