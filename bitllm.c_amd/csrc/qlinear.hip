@@ -651,9 +651,11 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         }
     }
 
-    // 4. MFMAs
+    // 4. MFMAs. A lane's accumulator holds tokens 4s .. 4s+3 (ntok of them live) of row r16.
     const bool tok_ok = r16 < a.M;
     const int8_t *xl = lds_x + (tok_ok ? r16 : 0) * p.ldl;
+    const int ntok = min(4, a.M - 4 * s);
+    int32_t *accp = acc_l + ((4 * s) * TR + 16 * rt + r16) * gld;
     v4i C = {0, 0, 0, 0};
     for (int j0 = 0; j0 < nj; j0 += MS) {
         if (j0 > 0) load_chunk(j0);
@@ -664,8 +666,8 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
             long bop[GE::NMF];
             decode<FMT, UD>(wq[j], bop);
             if constexpr (FMT == kTern) {
-#pragma unroll
-                for (int grp = 0; grp < 2; ++grp) {
+                auto group = [&](auto grp_c) __attribute__((always_inline)) {
+                    constexpr int grp = decltype(grp_c)::value;
                     long aop[UD];
                     if (tok_ok) {
                         load_ops<UD, (UD % 2 == 0)>(xl + st * GE::SC + 32 * UD * grp + 8 * UD * s, aop);
@@ -673,27 +675,29 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 #pragma unroll
                         for (int i = 0; i < UD; ++i) aop[i] = 0;
                     }
-                    v4i c = GROUPED ? v4i{0, 0, 0, 0} : C;
-#pragma unroll
-                    for (int i = 0; i < UD; ++i) c = mfma(aop[i], bop[grp * UD + i], c);
+                    const v4i c = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C);
                     if constexpr (GROUPED) {
                         const int gi = 2 * st + grp;
-                        if (gi < a.G) {
+                        if (gi < a.G && ntok > 0) {
+                            if constexpr (ACC) {
+                                if (row_ok) {
 #pragma unroll
-                            for (int vv = 0; vv < 4; ++vv) {
-                                const int tok = 4 * s + vv;
-                                if (tok < a.M && (!ACC || row_ok)) {
-                                    if constexpr (ACC)
-                                        a.acc[((size_t)tok * a.N + row) * a.G + gi] = c[vv] >> GE::SHIFT;
-                                    else
-                                        acc_l[(tok * TR + 16 * rt + r16) * gld + gi] = c[vv] >> GE::SHIFT;
+                                    for (int vv = 0; vv < 4; ++vv)
+                                        if (vv < ntok) a.acc[((size_t)(4 * s + vv) * a.N + row) * a.G + gi] = c[vv] >> GE::SHIFT;
                                 }
+                            } else {
+                                accp[gi] = c[0] >> GE::SHIFT;
+#pragma unroll
+                                for (int vv = 1; vv < 4; ++vv)
+                                    if (vv < ntok) accp[vv * TR * gld + gi] = c[vv] >> GE::SHIFT;
                             }
                         }
                     } else {
                         C = c;
                     }
-                }
+                };
+                group(std::integral_constant<int, 0>{});
+                group(std::integral_constant<int, 1>{});
             } else {
                 long aop[GE::NMF];
                 if (tok_ok) {
@@ -702,8 +706,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 #pragma unroll
                     for (int i = 0; i < GE::NMF; ++i) aop[i] = 0;
                 }
-#pragma unroll
-                for (int i = 0; i < GE::NMF; ++i) C = mfma(aop[i], bop[i], C);
+                C = mfma_ops<0>(aop, bop, C);
             }
         }
     }
