@@ -380,6 +380,10 @@ struct PrepArgs {
     int K, block;         // block 0: no rotation
     float norm;
     int ldl;              // LDS row stride of the staged activations (bytes)
+    int pre;              // EIF_HIP_PRE_*: what the rows are before the rotation (see eif_hip.h)
+    const float *x2;      // EIF_HIP_PRE_SWIGLU_RMS: the up-projection rows [M, ldx] (x holds the gate)
+    const float *nw;      // RMSNorm weight [K], NULL = 1
+    float eps;            // RMSNorm epsilon
 };
 
 // v <- v of lane (l ^ LX): DPP only for LX <= 8 (quad_perm, row_half_mirror, row_mirror compositions).
@@ -441,43 +445,91 @@ EIF_DEV float wave_max_dpp(float v)
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
-// Thread t holds columns [E*t, E*t + E) of token row m (zeros past K). The loads are unconditional (clamped to
-// the row) and nothing consumes them here, so the weight loads issued next are not held behind them; the sign
-// flip and the zeroing past K happen in prep_finish.
+// sum over the 64 lanes: DPP butterflies inside each 16-lane row, then the four row sums via readlane
+EIF_DEV float wave_sum_dpp(float v)
+{
+    v = v + xlane<1>(v);
+    v = v + xlane<2>(v);
+    v = v + xlane<4>(v);
+    v = v + xlane<8>(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return ((a + b) + c) + d;
+}
+
 template <int E>
-EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E])
+EIF_DEV void load4(const float *p, float (&v)[E])
+{
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(p + 4 * q);
+        v[4 * q] = a4.x, v[4 * q + 1] = a4.y, v[4 * q + 2] = a4.z, v[4 * q + 3] = a4.w;
+    }
+}
+
+// Thread t holds columns [E*t, E*t + E) of token row m (zeros past K). The loads are unconditional (clamped to
+// the row) or under uniform branches, and nothing consumes them here, so the weight loads issued next are not
+// held behind them; the pre-op, the sign flip and the zeroing past K happen in prep_finish.
+//   v: x; sg: signs; v2: x2 (SwiGLU); nw: the RMSNorm weight.
+template <int E>
+EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E], float (&v2)[E], float (&nw)[E])
 {
     const int i0 = E * threadIdx.x;
     const int ic = i0 < p.K ? i0 : 0;
-    const float *xr = p.x + (size_t)m * p.ldx + ic;
-#pragma unroll
-    for (int q = 0; q < E / 4; ++q) {
-        const float4 a4 = *reinterpret_cast<const float4 *>(xr + 4 * q);
-        v[4 * q] = a4.x, v[4 * q + 1] = a4.y, v[4 * q + 2] = a4.z, v[4 * q + 3] = a4.w;
-    }
+    load4<E>(p.x + (size_t)m * p.ldx + ic, v);
     if (p.signs) {   // uniform: a scalar branch
-#pragma unroll
-        for (int q = 0; q < E / 4; ++q) {
-            const float4 s4 = *reinterpret_cast<const float4 *>(p.signs + ic + 4 * q);
-            sg[4 * q] = s4.x, sg[4 * q + 1] = s4.y, sg[4 * q + 2] = s4.z, sg[4 * q + 3] = s4.w;
-        }
+        load4<E>(p.signs + ic, sg);
     } else {
 #pragma unroll
         for (int e = 0; e < E; ++e) sg[e] = 1.0f;
+    }
+    if (p.pre == EIF_HIP_PRE_SWIGLU_RMS) load4<E>(p.x2 + (size_t)m * p.ldx + ic, v2);
+    if (p.pre != EIF_HIP_PRE_NONE) {
+        if (p.nw) {
+            load4<E>(p.nw + ic, nw);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) nw[e] = 1.0f;
+        }
     }
 }
 
 // Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
 // LB = log2 of the WHT block when it is fixed at compile time (0: no rotation), -1: block read from p.block.
 template <int E, int LB>
-EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], const float (&sg)[E], int8_t *lds_x,
-                         float *xs_l, float *red)
+EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], const float (&sg)[E],
+                         const float (&v2)[E], const float (&nwv)[E], int8_t *lds_x, float *xs_l, float *red,
+                         float *red_ss)
 {
     const int t = threadIdx.x, i0 = E * t, nw = blockDim.x >> 6;
     const int block = LB >= 0 ? (LB > 0 ? 1 << LB : 0) : p.block;
     const bool live = i0 < p.K, flip = block > 0 && p.signs;
 #pragma unroll
-    for (int e = 0; e < E; ++e) v[e] = !live ? 0.0f : (flip ? v[e] * sg[e] : v[e]);
+    for (int e = 0; e < E; ++e) v[e] = live ? v[e] : 0.0f;
+    if (p.pre != EIF_HIP_PRE_NONE) {   // uniform
+        if (p.pre == EIF_HIP_PRE_SWIGLU_RMS) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[e] = (v[e] / (1.0f + expf(-v[e]))) * (live ? v2[e] : 0.0f);
+        }
+        // RMSNorm over the K columns: (v * (1 / sqrtf(sum(v^2) / K + eps))) * weight
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss = fmaf(v[e], v[e], ss);
+        ss = wave_sum_dpp(ss);
+        if ((t & 63) == 0) red_ss[t >> 6] = ss;
+        __syncthreads();
+        ss = 0.0f;
+        for (int w = 0; w < nw; ++w) ss += red_ss[w];
+        const float inv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = (v[e] * inv) * nwv[e];
+    }
+    if (flip) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = v[e] * sg[e];
+    }
 #pragma unroll
     for (int h = 1; h < E; h <<= 1) {
         if (h >= block) break;
@@ -548,7 +600,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     constexpr int TR = 16 * RT;   // rows per workgroup
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float xs_l[kGemvMaxM];
-    __shared__ float red_max[16];
+    __shared__ float red_max[16], red_ss[16];
     const int ks = (blockDim.x >> 6) / RT;
     // the wave index through readfirstlane: a scalar, so the per-wave step bounds below are scalar branches
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -568,7 +620,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     float *sc_l = reinterpret_cast<float *>(acc_l + a.M * TR * gld);
 
     // 1. activation loads
-    float v[EV], sg[EV];
+    float v[EV], sg[EV], v2[EV], nwv[EV];
     int4 pc0, pc1, pc2, pc3;   // up to kMaxPieces 16-byte pieces of the int8 rows per thread
     const int pieces = kpad / 16;
     auto piece_at = [&](int i) -> const int4 * {
@@ -586,7 +638,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     };
     float xs_v = 0.0f;
     if constexpr (E > 0) {
-        prep_load<E>(p, 0, v, sg);
+        prep_load<E>(p, 0, v, sg, v2, nwv);
     } else {
         pc0 = *piece_at(0);
         pc1 = *piece_at(1);
@@ -629,10 +681,10 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 
     // 3. activations -> LDS
     if constexpr (E > 0) {
-        prep_finish<E, LB>(p, 0, kpad, v, sg, lds_x, xs_l, red_max);
+        prep_finish<E, LB>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
         for (int m = 1; m < a.M; ++m) {
-            prep_load<E>(p, m, v, sg);
-            prep_finish<E, LB>(p, m, kpad, v, sg, lds_x, xs_l, red_max);
+            prep_load<E>(p, m, v, sg, v2, nwv);
+            prep_finish<E, LB>(p, m, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
         }
     } else {
         piece_store(0, pc0);
@@ -1097,6 +1149,23 @@ int make_prep(const eif_hip_qweight *w, const float *x, int ldx, const float *si
     p->K = K;
     p->block = block;
     p->norm = norm;
+    p->pre = EIF_HIP_PRE_NONE;
+    return EIF_HIP_OK;
+}
+
+int make_prep_spec(const eif_hip_qweight *w, const eif_hip_prep_spec *sp, int M, PrepArgs *p)
+{
+    if (!sp) return EIF_HIP_E_ARG;
+    int rc = make_prep(w, sp->x, sp->ldx, sp->signs, sp->wht_block, sp->wht_norm, M, p);
+    if (rc) return rc;
+    if (sp->pre != EIF_HIP_PRE_NONE && sp->pre != EIF_HIP_PRE_RMS && sp->pre != EIF_HIP_PRE_SWIGLU_RMS)
+        return EIF_HIP_E_ARG;
+    if (sp->pre == EIF_HIP_PRE_SWIGLU_RMS && (!sp->x2 || ((uintptr_t)sp->x2 & 15))) return EIF_HIP_E_ARG;
+    if (((uintptr_t)sp->norm_w & 15) || !(sp->eps >= 0.0f)) return EIF_HIP_E_ARG;
+    p->pre = sp->pre;
+    p->x2 = sp->x2;
+    p->nw = sp->norm_w;
+    p->eps = sp->eps;
     return EIF_HIP_OK;
 }
 
@@ -1165,6 +1234,32 @@ extern "C" int eif_hip_qlinear_f32(const eif_hip_qweight *w, const float *x, int
     a.y = y;
     a.ldy = ldy;
     return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
+}
+
+extern "C" int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias,
+                                    float *y, int ldy, int M, void *stream)
+{
+    PrepArgs p;
+    int rc = make_prep_spec(w, spec, M, &p);
+    if (rc) return rc;
+    if (!y || ldy < w->rows) return EIF_HIP_E_ARG;
+    QArgs a = make_args(w, nullptr, 0, M);
+    a.bias = bias;
+    a.y = y;
+    a.ldy = ldy;
+    return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
+}
+
+extern "C" int eif_hip_qlinear_prep_acc(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, int32_t *acc, int M,
+                                        void *stream)
+{
+    PrepArgs p;
+    int rc = make_prep_spec(w, spec, M, &p);
+    if (rc) return rc;
+    if (!acc) return EIF_HIP_E_ARG;
+    QArgs a = make_args(w, nullptr, 0, M);
+    a.acc = acc;
+    return dispatch<true>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
 }
 
 extern "C" int eif_hip_qlinear_f32_acc(const eif_hip_qweight *w, const float *x, int ldx, const float *signs,

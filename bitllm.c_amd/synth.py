@@ -113,3 +113,53 @@ def ternary_linear_bytes(N, K, group, M):
 
 def int_linear_bytes(N, K, bits, M):
     return N * ((K * bits + 7) // 8) + 4 * N + M * (K + 4) + 4 * M * N
+
+
+def bitnet_config(dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len, group_in, group_down,
+                  wht_dim, wht_q, wht_hidden, rope_theta=500000.0, rms_eps=None, sub_eps=1e-5):
+    """A BitNet-b1.58 decoder configuration (the reference's tinyllm BitNet model, src/eif_tinyllm.c:371-857).
+
+    group_in: ternary group of every matrix whose input is dim or q_dim wide; group_down: of the down projection.
+    rms_eps defaults to the reference's choice (1e-6 for vocabularies above 120000, else 1e-5)."""
+    def norm(b):
+        return float(np.float32(1.0) / np.sqrt(np.float32(b))) if b else 1.0
+    return dict(dim=dim, hidden=hidden, n_layers=n_layers, n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=head_dim,
+                vocab=vocab, seq_len=seq_len, rope_theta=rope_theta,
+                rms_eps=(1e-6 if vocab > 120000 else 1e-5) if rms_eps is None else rms_eps, sub_eps=sub_eps,
+                wht_dim=wht_dim, wht_q=wht_q, wht_hidden=wht_hidden, wht_norm_dim=norm(wht_dim),
+                wht_norm_q=norm(wht_q), wht_norm_hidden=norm(wht_hidden),
+                g_q=group_in, g_o=group_in, g_13=group_in, g_2=group_down)
+
+
+# The BitNet-b1.58-2B-shaped decode model: 30 layers of the layer shapes above, WHT-128, g128 (g96 down),
+# INT8 vocabulary head 128256 x 2560, context 2048.
+BITNET_2B_DECODE = dict(dim=2560, hidden=6912, n_layers=30, n_heads=20, n_kv_heads=5, head_dim=128, vocab=128256,
+                        seq_len=2048, group_in=128, group_down=96, wht_dim=128, wht_q=128, wht_hidden=128)
+
+
+def bitnet_model(key, cfg):
+    """Random-init weights of a BitNet decoder in the reference's formats, per-layer arrays concatenated over layers:
+    INT8 embedding with per-token scales, 2-bit ternary matrices with grouped FP32 scales, RMSNorm weights, +-1
+    rotation signs, INT8 head with per-row scales."""
+    d, h, L = cfg["dim"], cfg["hidden"], cfg["n_layers"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    V = cfg["vocab"]
+    w = {}
+    r = rng(*key, 10)
+    w["emb"] = r.integers(-127, 128, size=(V, d), dtype=np.int8)
+    w["emb_scale"] = (np.abs(rng(*key, 11).standard_normal(V)) * 0.01 + 0.01).astype(np.float32)
+    shapes = {"q": (qd, d, cfg["g_q"]), "k": (kvd, d, cfg["g_q"]), "v": (kvd, d, cfg["g_q"]), "o": (d, qd, cfg["g_o"]),
+              "1": (h, d, cfg["g_13"]), "3": (h, d, cfg["g_13"]), "2": (d, h, cfg["g_2"])}
+    for i, (name, (N, K, g)) in enumerate(shapes.items()):
+        codes = rng(*key, 20 + i).integers(-1, 2, size=(L * N, K), dtype=np.int8)
+        w["w" + name] = pack_ternary(codes)
+        ng = -(-K // g)
+        w["g" + name] = (np.abs(rng(*key, 30 + i).standard_normal((L * N, ng))) * 0.02 + 0.005).astype(np.float32)
+    for i, (name, n) in enumerate((("rms_att", d), ("rms_ffn", d), ("rms_sub_att", qd), ("rms_sub_ffn", h))):
+        w[name] = (1.0 + 0.1 * rng(*key, 40 + i).standard_normal(L * n)).astype(np.float32)
+    w["rms_final"] = (1.0 + 0.1 * rng(*key, 45).standard_normal(d)).astype(np.float32)
+    for i, (name, n) in enumerate((("signs_dim", d), ("signs_q", qd), ("signs_hidden", h))):
+        w[name] = np.where(rng(*key, 50 + i).uniform(size=n) < 0.5, -1.0, 1.0).astype(np.float32)
+    w["wcls"] = rng(*key, 60).integers(-127, 128, size=(V, d), dtype=np.int8)
+    w["wcls_scale"] = (np.abs(rng(*key, 61).standard_normal(V)) * 0.01 + 0.002).astype(np.float32)
+    return w

@@ -102,6 +102,35 @@ int eif_hip_qlinear_f32(const eif_hip_qweight *w, const float *x, int ldx, const
 int eif_hip_qlinear_f32_acc(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int wht_block,
                             float norm, int32_t *acc, int M, void *stream);
 
+/* What the fused prep does before the rotation (eif_hip_qlinear_prep):
+ *   EIF_HIP_PRE_NONE        the rows as given;
+ *   EIF_HIP_PRE_RMS         RMSNorm: (x * (1 / sqrtf(sum(x^2) / K + eps))) * norm_w, the decoder's pre-norm
+ *                           (src/eif_tinyllm.c:196-330, weight NULL = 1);
+ *   EIF_HIP_PRE_SWIGLU_RMS  h = (x / (1 + expf(-x))) * x2 (SiLU gate times up, src/eif_tinyllm.c:740-780), then
+ *                           RMSNorm of h (the BitNet sub-norm before the down projection).            */
+#define EIF_HIP_PRE_NONE 0
+#define EIF_HIP_PRE_RMS 1
+#define EIF_HIP_PRE_SWIGLU_RMS 2
+
+typedef struct eif_hip_prep_spec {
+    const float *x;       /* [M, ldx] FP32 rows (device), 16-byte aligned */
+    int ldx;              /* row stride in floats, a multiple of 4, >= K */
+    const float *x2;      /* EIF_HIP_PRE_SWIGLU_RMS: up-projection rows [M, ldx]; else ignored */
+    const float *norm_w;  /* RMSNorm weight [K] or NULL (= 1) */
+    float eps;            /* RMSNorm epsilon */
+    int pre;              /* EIF_HIP_PRE_* */
+    const float *signs;   /* [K] or NULL */
+    int wht_block;        /* 0: no rotation; else a power of two <= 1024 dividing K */
+    float wht_norm;       /* the WHT scale, e.g. eif_hip_wht_norm(wht_block) */
+} eif_hip_prep_spec;
+
+/* eif_hip_qlinear_f32 with a pre-op: y = linear(prep(pre(x))) (+ bias) for M <= 8 rows, one launch. The
+ * bias may be the residual stream itself (y == bias: each output reads its own bias element first).     */
+int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias, float *y,
+                         int ldy, int M, void *stream);
+int eif_hip_qlinear_prep_acc(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, int32_t *acc, int M,
+                             void *stream);
+
 /* Drop the device copies the host-pointer ABI keeps for the weight buffer at host_ptr (NULL: all of them).
  * Call it after rewriting a weight buffer in place or before freeing it.                                 */
 void eif_hip_forget_host_weights(const void *host_ptr);

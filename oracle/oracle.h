@@ -40,6 +40,31 @@ void orc_int4_gemv_f32(float *out, const uint8_t *w, const float *sc, const floa
 void orc_gemm_f32_nt_ld(const float *A, int lda, const float *W, int ldw, const float *bias, float *C, int ldc, int M, int N, int K, int act, int accumulate);
 void orc_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale);
 int orc_num_threads(void);
+
+/* One BitNet-b1.58 decoder step (decode_oracle.c). */
+float orc_round_f16(float v);
+#define ORC_LIN_INT8 0
+#define ORC_LIN_F32 1
+typedef struct orc_bitnet_cfg {
+    int dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len;
+    float rope_theta, rms_eps, sub_eps;
+    int wht_dim, wht_q, wht_hidden;            /* WHT blocks of the inputs of wq/wk/wv/w1/w3, wo, w2 (0: none) */
+    float wht_norm_dim, wht_norm_q, wht_norm_hidden;
+    int g_q, g_o, g_13, g_2;                   /* ternary groups of wq/wk/wv, wo, w1/w3, w2 */
+} orc_bitnet_cfg;
+typedef struct orc_bitnet_weights {            /* reference formats, per-layer arrays concatenated over layers */
+    const int8_t *emb;                         /* [vocab, dim] */
+    const float *emb_scale;                    /* [vocab] or NULL */
+    const uint8_t *wq, *wk, *wv, *wo, *w1, *w3, *w2;
+    const float *gq, *gk, *gv, *go, *g1, *g3, *g2;
+    const float *rms_att, *rms_ffn, *rms_sub_att, *rms_sub_ffn, *rms_final;
+    const float *signs_dim, *signs_q, *signs_hidden;
+    const int8_t *wcls;                        /* [vocab, dim] */
+    const float *wcls_scale;                   /* [vocab] */
+} orc_bitnet_weights;
+/* kcache / vcache: [n_layers, seq_len, kv_dim] floats. Returns 0, or -1 on bad arguments. */
+int orc_bitnet_forward(const orc_bitnet_cfg *c, const orc_bitnet_weights *w, float *kcache, float *vcache, int token,
+                       int pos, int mode, float *logits);
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,8 @@ ORACLE_SIGS = {
     "orc_gemm_f32_nt_ld": (None, [_vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i]),
     "orc_softmax_rows_f32": (None, [_vp, _i, _i, _i, _f]),
     "orc_num_threads": (_i, []),
+    "orc_round_f16": (_f, [_f]),
+    "orc_bitnet_forward": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }
 
 # The reference's own symbols (same signatures as the product's drop-in ABI) plus the two wrapped statics.
@@ -81,5 +83,44 @@ def load_ref(path):
     return _bind(path, REF_SIGS)
 
 
+def load_ref_tinyllm(path):
+    """The reference's tinyllm decode wrapper (_ref/libref.so or _ref/libref_scalar.so)."""
+    return _bind(path, REF_TINYLLM_SIGS)
+
+
 def P(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+ORC_LIN_INT8, ORC_LIN_F32 = 0, 1
+
+
+class OrcBitnetCfg(C.Structure):
+    _fields_ = [(n, _i) for n in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "seq_len")] + \
+               [(n, _f) for n in ("rope_theta", "rms_eps", "sub_eps")] + \
+               [(n, _i) for n in ("wht_dim", "wht_q", "wht_hidden")] + \
+               [(n, _f) for n in ("wht_norm_dim", "wht_norm_q", "wht_norm_hidden")] + \
+               [(n, _i) for n in ("g_q", "g_o", "g_13", "g_2")]
+
+
+BITNET_WEIGHT_FIELDS = ("emb", "emb_scale", "wq", "wk", "wv", "wo", "w1", "w3", "w2", "gq", "gk", "gv", "go", "g1", "g3",
+                        "g2", "rms_att", "rms_ffn", "rms_sub_att", "rms_sub_ffn", "rms_final", "signs_dim", "signs_q",
+                        "signs_hidden", "wcls", "wcls_scale")
+
+
+class OrcBitnetWeights(C.Structure):
+    _fields_ = [(n, _vp) for n in BITNET_WEIGHT_FIELDS]
+
+
+def bitnet_structs(cfg, w):
+    """ctypes (config, weights) for a model from synth.bitnet_model; the numpy arrays must outlive them."""
+    c = OrcBitnetCfg(**{k: cfg[k] for k, _ in OrcBitnetCfg._fields_})
+    ws = OrcBitnetWeights(**{k: (w[k].ctypes.data if w.get(k) is not None else None) for k in BITNET_WEIGHT_FIELDS})
+    return c, ws
+
+
+REF_TINYLLM_SIGS = {
+    "ref_bitnet_create": (_vp, [_vp, _vp, _i]),
+    "ref_bitnet_forward": (C.POINTER(_f), [_vp, _i, _i]),
+    "ref_bitnet_destroy": (None, [_vp]),
+}

@@ -1,0 +1,74 @@
+/*
+ * ref_tinyllm_wrap.c -- TEST INFRASTRUCTURE. Builds the reference's own BitNet tinyllm model (include/eif_tinyllm.h,
+ * the in-memory construction of tests/test_seq_bounds.c:11-26) from the oracle's weight arrays and runs its decode
+ * (tinyllm_forward, src/eif_tinyllm.c:1502-1506). Compiled together with the reference sources into oracle/_ref/.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "eif_tinyllm.h"
+#include "oracle.h"
+
+typedef struct {
+    tinyllm_t llm;
+    void *pool;
+    float *ones;
+} ref_bitnet;
+
+/* bitnet_group: the reference's one group bound for all matrices (eif_bitnet_group_size per input width). */
+void *ref_bitnet_create(const orc_bitnet_cfg *c, const orc_bitnet_weights *w, int bitnet_group)
+{
+    ref_bitnet *r = (ref_bitnet *)calloc(1, sizeof(ref_bitnet));
+    if (!r) return NULL;
+    tinyllm_config_t cfg;
+    memset(&cfg, 0, sizeof(cfg));
+    cfg.dim = c->dim;
+    cfg.hidden_dim = c->hidden;
+    cfg.n_layers = c->n_layers;
+    cfg.n_heads = c->n_heads;
+    cfg.n_kv_heads = c->n_kv_heads;
+    cfg.vocab_size = c->vocab;
+    cfg.seq_len = c->seq_len;
+    cfg.qtype = TINYLLM_QTYPE_BITNET_158;
+    cfg.head_dim = c->head_dim;
+    cfg.rope_theta = c->rope_theta;
+    cfg.bitnet_group = bitnet_group;
+    cfg.bitnet_hadamard = 1;
+    const size_t sz = tinyllm_memory_size(&cfg);
+    r->pool = malloc(sz);
+    const int big = c->dim * 4 + c->hidden * 3 + c->n_heads * c->head_dim * 4;
+    r->ones = (float *)malloc(sizeof(float) * (size_t)big * c->n_layers);
+    if (!r->pool || !r->ones || tinyllm_init(&r->llm, &cfg, r->pool, sz) != 0) {
+        free(r->pool), free(r->ones), free(r);
+        return NULL;
+    }
+    for (int i = 0; i < big * c->n_layers; i++) r->ones[i] = 1.0f;
+    tinyllm_weights_t *tw = &r->llm.weights;
+    tw->token_embedding = (void *)w->emb;
+    tw->token_embedding_scale = (float *)w->emb_scale;
+    tw->rms_att_weight = (float *)w->rms_att;
+    tw->rms_ffn_weight = (float *)w->rms_ffn;
+    tw->rms_sub_att_weight = (float *)w->rms_sub_att;
+    tw->rms_sub_ffn_weight = (float *)w->rms_sub_ffn;
+    tw->rms_final_weight = (float *)w->rms_final;
+    tw->wq = (void *)w->wq, tw->wk = (void *)w->wk, tw->wv = (void *)w->wv, tw->wo = (void *)w->wo;
+    tw->w1 = (void *)w->w1, tw->w2 = (void *)w->w2, tw->w3 = (void *)w->w3;
+    tw->attn_scale = r->ones;   /* row scales: unused with grouped scales */
+    tw->ffn_scale = r->ones;
+    tw->bitnet_gscale[TL_BN_WQ] = w->gq, tw->bitnet_gscale[TL_BN_WK] = w->gk, tw->bitnet_gscale[TL_BN_WV] = w->gv;
+    tw->bitnet_gscale[TL_BN_WO] = w->go, tw->bitnet_gscale[TL_BN_W1] = w->g1, tw->bitnet_gscale[TL_BN_W3] = w->g3;
+    tw->bitnet_gscale[TL_BN_W2] = w->g2;
+    tw->had_signs_dim = w->signs_dim, tw->had_signs_q = w->signs_q, tw->had_signs_hidden = w->signs_hidden;
+    tw->wcls = (void *)w->wcls;
+    tw->wcls_scale = (float *)w->wcls_scale;
+    return r;
+}
+
+float *ref_bitnet_forward(void *h, int token, int pos) { return tinyllm_forward(&((ref_bitnet *)h)->llm, token, pos); }
+
+void ref_bitnet_destroy(void *h)
+{
+    ref_bitnet *r = (ref_bitnet *)h;
+    if (!r) return;
+    free(r->pool), free(r->ones), free(r);
+}

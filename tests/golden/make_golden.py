@@ -144,5 +144,46 @@ def main():
     print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path)} bytes")
 
 
+# the decode fixture: a tiny BitNet model regenerated from its seed by synth.bitnet_model (weights are not stored)
+DECODE_KEY = (7,)
+DECODE_CFG = dict(dim=128, hidden=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=32, vocab=300, seq_len=32,
+                  group_in=32, group_down=32, wht_dim=128, wht_q=128, wht_hidden=256)
+DECODE_STEPS = 16
+
+
+def decode_config():
+    c = dict(DECODE_CFG)
+    return synth.bitnet_config(c.pop("dim"), c.pop("hidden"), c.pop("n_layers"), c.pop("n_heads"), c.pop("n_kv_heads"),
+                               c.pop("head_dim"), c.pop("vocab"), c.pop("seq_len"), c.pop("group_in"),
+                               c.pop("group_down"), c.pop("wht_dim"), c.pop("wht_q"), c.pop("wht_hidden"))
+
+
+def decode_main():
+    """Writes tests/golden/decode_vectors.npz: greedy decode of the reference's own tinyllm BitNet model
+    (oracle/ref_tinyllm_wrap.c) built from synth.bitnet_model(DECODE_KEY, ...), by the scalar build
+    (_ref/libref_scalar.so) and by the reference-flag build (_ref/libref.so)."""
+    import ctypes as C
+    cfg = decode_config()
+    w = synth.bitnet_model(DECODE_KEY, cfg)
+    c, ws = oracle_api.bitnet_structs(cfg, w)
+    out = {}
+    for tag, lib in (("scalar", "libref_scalar.so"), ("x86", "libref.so")):
+        ref = oracle_api.load_ref_tinyllm(os.path.join(ROOT, "oracle", "_ref", lib))
+        h = ref.ref_bitnet_create(C.byref(c), C.byref(ws), cfg["g_q"])
+        tokens, logits = [5], []
+        for pos in range(DECODE_STEPS):
+            lp = ref.ref_bitnet_forward(h, tokens[-1], pos)
+            lo = np.ctypeslib.as_array(lp, shape=(cfg["vocab"],)).copy()
+            logits.append(lo)
+            tokens.append(int(np.argmax(lo)))
+        ref.ref_bitnet_destroy(h)
+        out[tag + "_tokens"] = np.array(tokens, np.int32)
+        out[tag + "_logits"] = np.stack(logits)
+    path = os.path.join(ROOT, "tests", "golden", "decode_vectors.npz")
+    np.savez_compressed(path, **out)
+    print(f"wrote {path}: {len(out)} arrays, {os.path.getsize(path)} bytes")
+
+
 if __name__ == "__main__":
     main()
+    decode_main()
