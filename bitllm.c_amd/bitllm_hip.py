@@ -15,8 +15,50 @@ PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
 
+PRE_NONE, PRE_RMS, PRE_SWIGLU_RMS = 0, 1, 2
+
+
+class PrepSpec(C.Structure):
+    """eif_hip_prep_spec (include/eif_hip.h)."""
+    _fields_ = [("x", _vp), ("ldx", _i), ("x2", _vp), ("norm_w", _vp), ("eps", _f), ("pre", _i), ("signs", _vp),
+                ("wht_block", _i), ("wht_norm", _f)]
+
+
+class BitnetConfig(C.Structure):
+    """eif_hip_bitnet_config (include/eif_hip_decode.h)."""
+    _fields_ = [(n, _i) for n in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "seq_len")] + \
+               [(n, _f) for n in ("rope_theta", "rms_eps", "sub_eps")] + \
+               [(n, _i) for n in ("wht_dim", "wht_q", "wht_hidden")] + \
+               [(n, _f) for n in ("wht_norm_dim", "wht_norm_q", "wht_norm_hidden")] + \
+               [(n, _i) for n in ("g_q", "g_o", "g_13", "g_2")]
+
+
+class BitnetLayer(C.Structure):
+    _fields_ = [(n, _vp) for n in ("wq", "wk", "wv", "wo", "w1", "w3", "w2", "gq", "gk", "gv", "go", "g1", "g3", "g2",
+                                    "rms_att", "rms_ffn", "rms_sub_att", "rms_sub_ffn")]
+
+
+class BitnetGlobals(C.Structure):
+    _fields_ = [(n, _vp) for n in ("emb", "emb_scale", "rms_final", "signs_dim", "signs_q", "signs_hidden", "wcls",
+                                    "wcls_scale")]
+
+
 # name: (restype, argtypes) for every exported symbol this module binds.
 _SIGS = {
+    "eif_hip_qlinear_prep": (_i, [_vp, C.POINTER(PrepSpec), _vp, _vp, _i, _i, _vp]),
+    "eif_hip_qlinear_prep_acc": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _vp]),
+    "eif_hip_bitnet_create": (_i, [C.POINTER(_vp), C.POINTER(BitnetConfig)]),
+    "eif_hip_bitnet_set_layer": (_i, [_vp, _i, C.POINTER(BitnetLayer)]),
+    "eif_hip_bitnet_set_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
+    "eif_hip_bitnet_reset": (_i, [_vp, _vp, _i, _vp]),
+    "eif_hip_bitnet_steps": (_i, [_vp, _i, _i, _vp]),
+    "eif_hip_bitnet_tokens": (_i, [_vp, _vp, _i, _vp]),
+    "eif_hip_bitnet_logits": (_i, [_vp, _vp, _vp]),
+    "eif_hip_bitnet_position": (_i, [_vp, _vp]),
+    "eif_hip_bitnet_kv_cache": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),
+    "eif_hip_bitnet_weight_bytes": (_sz, [_vp]),
+    "eif_hip_bitnet_kv_bytes": (_sz, [_vp, _i]),
+    "eif_hip_bitnet_destroy": (None, [_vp]),
     "eif_hip_init": (_i, [_i]),
     "eif_hip_strerror": (C.c_char_p, [_i]),
     "eif_hip_wht_norm": (_f, [_i]),
@@ -159,3 +201,101 @@ class QWeight:
     def acc_f32(self, x, acc, block, norm, signs=None, stream=None):
         check(load().eif_hip_qlinear_f32_acc(self.h, ptr(x), x.stride(0), ptr(signs), block, norm, ptr(acc),
                                              x.shape[0], stream_ptr(stream)), "eif_hip_qlinear_f32_acc")
+
+
+def prep_spec(x, pre=PRE_NONE, x2=None, norm_w=None, eps=0.0, signs=None, block=0, norm=1.0):
+    """An eif_hip_prep_spec over device tensors (kept alive by the caller)."""
+    return PrepSpec(x=ptr(x).value, ldx=x.stride(0) if x.dim() > 1 else x.shape[-1], x2=ptr(x2).value if x2 is not None else None,
+                    norm_w=ptr(norm_w).value if norm_w is not None else None, eps=eps, pre=pre,
+                    signs=ptr(signs).value if signs is not None else None, wht_block=block, wht_norm=norm)
+
+
+class BitnetModel:
+    """The GPU BitNet decoder (include/eif_hip_decode.h) loaded from a configuration and reference-format
+    weights as synth.bitnet_model builds them (per-layer arrays concatenated over layers)."""
+
+    def __init__(self, cfg, w):
+        import numpy as np
+        lib = load()
+        self.cfg = cfg
+        self.c = BitnetConfig(**{k: cfg[k] for k, _ in BitnetConfig._fields_})
+        h = C.c_void_p()
+        check(lib.eif_hip_bitnet_create(C.byref(h), C.byref(self.c)), "eif_hip_bitnet_create")
+        self.h = h
+        d, hid, L = cfg["dim"], cfg["hidden"], cfg["n_layers"]
+        qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+        rows = {"q": qd, "k": kvd, "v": kvd, "o": d, "1": hid, "3": hid, "2": d}
+        norms = {"rms_att": d, "rms_ffn": d, "rms_sub_att": qd, "rms_sub_ffn": hid}
+
+        def at(a, l, n):
+            a = np.ascontiguousarray(a).reshape(L, -1) if a.ndim == 1 else np.ascontiguousarray(a).reshape(L, n, -1)
+            return a[l].ctypes.data, a
+
+        keep = []
+        for l in range(L):
+            f = {}
+            for k, n in rows.items():
+                pw, a = at(w["w" + k], l, n)
+                pg, b = at(w["g" + k], l, n)
+                keep += [a, b]
+                f["w" + k], f["g" + k] = pw, pg
+            for k, n in norms.items():
+                pn, a = at(w[k], l, n)
+                keep.append(a)
+                f[k] = pn
+            check(lib.eif_hip_bitnet_set_layer(h, l, C.byref(BitnetLayer(**f))), "eif_hip_bitnet_set_layer")
+        g = BitnetGlobals(**{k: (w[k].ctypes.data if w.get(k) is not None else None)
+                             for k, _ in BitnetGlobals._fields_})
+        check(lib.eif_hip_bitnet_set_globals(h, C.byref(g)), "eif_hip_bitnet_set_globals")
+
+    def reset(self, prompt, stream=None):
+        import numpy as np
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        check(load().eif_hip_bitnet_reset(self.h, p.ctypes.data, len(p), stream_ptr(stream)), "eif_hip_bitnet_reset")
+
+    def steps(self, n, graph=False, stream=None):
+        check(load().eif_hip_bitnet_steps(self.h, n, 1 if graph else 0, stream_ptr(stream)), "eif_hip_bitnet_steps")
+
+    def tokens(self, n, stream=None):
+        import numpy as np
+        out = np.zeros(n, np.int32)
+        check(load().eif_hip_bitnet_tokens(self.h, out.ctypes.data, n, stream_ptr(stream)), "eif_hip_bitnet_tokens")
+        return out
+
+    def logits(self, stream=None):
+        import numpy as np
+        out = np.zeros(self.cfg["vocab"], np.float32)
+        check(load().eif_hip_bitnet_logits(self.h, out.ctypes.data, stream_ptr(stream)), "eif_hip_bitnet_logits")
+        return out
+
+    def position(self, stream=None):
+        p = load().eif_hip_bitnet_position(self.h, stream_ptr(stream))
+        if p < 0:
+            check(p, "eif_hip_bitnet_position")
+        return p
+
+    def kv_cache(self, layer, pos0, n, stream=None):
+        """Keys and values of one layer at positions [pos0, pos0 + n), float [n, kv_dim] each."""
+        import numpy as np
+        kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        k, v = np.zeros((n, kvd), np.float32), np.zeros((n, kvd), np.float32)
+        check(load().eif_hip_bitnet_kv_cache(self.h, layer, pos0, n, k.ctypes.data, v.ctypes.data, stream_ptr(stream)),
+              "eif_hip_bitnet_kv_cache")
+        return k, v
+
+    def weight_bytes(self):
+        return load().eif_hip_bitnet_weight_bytes(self.h)
+
+    def kv_bytes(self, pos):
+        return load().eif_hip_bitnet_kv_bytes(self.h, pos)
+
+    def close(self):
+        if self.h:
+            load().eif_hip_bitnet_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,536 @@
+// decode.hip -- BitNet-b1.58 decoder step on one MI355X (include/eif_hip_decode.h).
+//
+// The step follows tinyllm_forward_embedding_ex's BitNet path (src/eif_tinyllm.c:371-857) with every linear on
+// the fused prep + int8-MFMA GEMV of qlinear.hip (eif_hip_qlinear_prep: RMSNorm / SiLU-gate + RMSNorm, WHT,
+// absmax INT8, group-scaled ternary GEMV, residual as the epilogue bias) and three small kernels of its own:
+//   embed_kernel        x = INT8 embedding row * per-token scale (src/eif_tinyllm.c:902-916)
+//   attn_decode_kernel  RoPE of q and k (:396-405, :476-507), fp16 KV append, softmax attention (:555-650);
+//                       one workgroup per query head
+//   sample_kernel       greedy argmax (first maximum, src/eif_tinyllm.c:1519-1530) or the next prompt token,
+//                       stored in the sequence; position + 1
+// Device state (position, current token, prompt, sequence) lets one captured HIP graph serve every step.
+#include <hip/hip_fp16.h>
+
+#include <new>
+#include <vector>
+
+#include "hip_common.h"
+#include "../../include/eif_hip_decode.h"
+
+namespace {
+
+constexpr int kMaxSeq = 4096;
+constexpr int kAttnThreads = 256;
+
+// state[0] = position of the step about to run, state[1] = its token, state[2] = prompt length
+__global__ __launch_bounds__(256) void embed_kernel(const int8_t *emb, const float *emb_scale, const int *state,
+                                                    float *x, int dim, int vocab)
+{
+    int tok = state[1];
+    tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+    const float sc = emb_scale ? emb_scale[tok] : 1.0f;
+    const int8_t *row = emb + (size_t)tok * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = (float)row[i] * sc;
+}
+
+// One workgroup per query head h (kv head g = h / kv_mul). Threads hold 8 of the HD dimensions of one key /
+// value row: DPR threads per row, RPP rows per pass over the positions.
+//   1. RoPE of q_h and of k_g at position pos (the rotated k and v rounded to fp16, as the cache stores them);
+//      the first query head of each kv head appends them to the cache
+//   2. scores s_t = (q . k_t) / sqrt(HD), t <= pos (the current position from the workgroup's own copy)
+//   3. softmax: max, exp(s - max), sum, times 1 / sum
+//   4. out_h = sum_t p_t v_t
+// Cache layout: [kv_head][seq_len][HD] fp16 per layer.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *qkv, __half *kc, __half *vc,
+                                                                   const int *state, float *out, int n_heads,
+                                                                   int n_kv, int seq_len, float theta,
+                                                                   float inv_sqrt_hd)
+{
+    constexpr int DPR = HD / 8, RPP = kAttnThreads / DPR, HALF = HD / 2;
+    __shared__ float q_l[HD], k_l[HD], v_l[HD];
+    __shared__ float s_l[kMaxSeq];
+    __shared__ float red[kAttnThreads / 64];
+    __shared__ float acc_l[RPP][HD + 4];
+    const int h = blockIdx.x, kv_mul = n_heads / n_kv, g = h / kv_mul;
+    const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
+    const int pos = state[0];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    __half *kcg = kc + (size_t)g * seq_len * HD, *vcg = vc + (size_t)g * seq_len * HD;
+
+    // 1. RoPE (half-split pairs j, j + HD/2) and the current k, v
+    if (t < HALF) {
+        const float freq = 1.0f / powf(theta, (float)(2 * t) / (float)HD);
+        const float val = (float)pos * freq;
+        const float c = cosf(val), sn = sinf(val);
+        const float *qh = qkv + h * HD, *kh = qkv + q_dim + g * HD, *vh = qkv + q_dim + kv_dim + g * HD;
+        float a = qh[t], b = qh[t + HALF];
+        q_l[t] = a * c - b * sn;
+        q_l[t + HALF] = b * c + a * sn;
+        a = kh[t], b = kh[t + HALF];
+        const __half k0 = __float2half(a * c - b * sn), k1 = __float2half(b * c + a * sn);
+        const __half v0 = __float2half(vh[t]), v1 = __float2half(vh[t + HALF]);
+        k_l[t] = __half2float(k0), k_l[t + HALF] = __half2float(k1);
+        v_l[t] = __half2float(v0), v_l[t + HALF] = __half2float(v1);
+        if (h % kv_mul == 0) {
+            kcg[(size_t)pos * HD + t] = k0, kcg[(size_t)pos * HD + t + HALF] = k1;
+            vcg[(size_t)pos * HD + t] = v0, vcg[(size_t)pos * HD + t + HALF] = v1;
+        }
+    }
+    __syncthreads();
+
+    // 2. scores
+    const int sub = t % DPR, r0 = t / DPR;
+    float qv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qv[i] = q_l[8 * sub + i];
+    for (int tt = r0; tt <= pos; tt += RPP) {
+        float kv8[8];
+        if (tt == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) kv8[i] = k_l[8 * sub + i];
+        } else {
+            const uint4 raw = *reinterpret_cast<const uint4 *>(kcg + (size_t)tt * HD + 8 * sub);
+            const __half2 *hp = reinterpret_cast<const __half2 *>(&raw);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 f = __half22float2(hp[i]);
+                kv8[2 * i] = f.x, kv8[2 * i + 1] = f.y;
+            }
+        }
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d = fmaf(qv[i], kv8[i], d);
+#pragma unroll
+        for (int off = 1; off < DPR; off <<= 1) d += __shfl_xor(d, off, 64);
+        if (sub == 0) s_l[tt] = d * inv_sqrt_hd;
+    }
+    __syncthreads();
+
+    // 3. softmax over s_l[0 .. pos]
+    float mx = -INFINITY;
+    for (int tt = t; tt <= pos; tt += kAttnThreads) mx = fmaxf(mx, s_l[tt]);
+    mx = eif_wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+    __syncthreads();
+    float sum = 0.0f;
+    for (int tt = t; tt <= pos; tt += kAttnThreads) {
+        const float e = expf(s_l[tt] - mx);
+        s_l[tt] = e;
+        sum += e;
+    }
+    sum = eif_wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = red[0];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; ++w) sum += red[w];
+    const float inv = 1.0f / sum;
+
+    // 4. weighted sum of the values
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+    for (int tt = r0; tt <= pos; tt += RPP) {
+        const float p = s_l[tt] * inv;
+        if (tt == pos) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, v_l[8 * sub + i], acc[i]);
+        } else {
+            const uint4 raw = *reinterpret_cast<const uint4 *>(vcg + (size_t)tt * HD + 8 * sub);
+            const __half2 *hp = reinterpret_cast<const __half2 *>(&raw);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float2 f = __half22float2(hp[i]);
+                acc[2 * i] = fmaf(p, f.x, acc[2 * i]);
+                acc[2 * i + 1] = fmaf(p, f.y, acc[2 * i + 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc_l[r0][8 * sub + i] = acc[i];
+    __syncthreads();
+    if (t < HD) {
+        float o = 0.0f;
+        for (int r = 0; r < RPP; ++r) o += acc_l[r][t];
+        out[h * HD + t] = o;
+    }
+}
+
+// Greedy token: first index of the largest logit (NaN never wins). While the prompt lasts the next token is
+// the prompt's; the made token is stored at position pos + 1 of the sequence and the position advances.
+__global__ __launch_bounds__(1024) void sample_kernel(const float *logits, int vocab, int *state, const int *prompt,
+                                                      int *seq, int seq_len)
+{
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = t; i < vocab; i += blockDim.x) {
+        const float x = logits[i];
+        if (x > v) v = x, idx = i;   // i increases: the first maximum of this thread's share
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ov > v || (ov == v && oi < idx)) v = ov, idx = oi;
+    }
+    if (lane == 0) bv[wave] = v, bi[wave] = idx;
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) v = bv[w], idx = bi[w];
+        if (idx == 0x7fffffff) idx = 0;
+        const int pos = state[0], np = state[2];
+        const int next = pos + 1 < np ? prompt[pos + 1] : idx;
+        if (pos + 1 < seq_len) seq[pos + 1] = next;
+        state[1] = next;
+        state[0] = pos + 1;
+    }
+}
+
+__global__ void fill_half_kernel(__half *p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = __float2half(0.0f);
+}
+
+__global__ void start_kernel(int *state, int *seq, const int *prompt, int n_prompt)
+{
+    state[0] = 0;
+    state[1] = prompt[0];
+    state[2] = n_prompt;
+    seq[0] = prompt[0];
+}
+
+template <typename T>
+int dev_upload(T **dst, const T *src, size_t n)
+{
+    *dst = nullptr;
+    if (!src) return EIF_HIP_OK;
+    EIF_HIP_TRY(hipMalloc(dst, n * sizeof(T)));
+    EIF_HIP_TRY(hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return EIF_HIP_OK;
+}
+
+}  // namespace
+
+struct eif_hip_bitnet {
+    eif_hip_bitnet_config c{};
+    int q_dim = 0, kv_dim = 0;
+    std::vector<eif_hip_qweight *> wqkv, wo, w13, w2;
+    eif_hip_qweight *head = nullptr;
+    std::vector<float *> rms_att, rms_ffn, rms_sub_att, rms_sub_ffn;
+    float *rms_final = nullptr, *signs_dim = nullptr, *signs_q = nullptr, *signs_hidden = nullptr;
+    int8_t *emb = nullptr;
+    float *emb_scale = nullptr;
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *hb = nullptr, *logits = nullptr;
+    __half *kc = nullptr, *vc = nullptr;
+    int *state = nullptr, *prompt = nullptr, *seq = nullptr;
+    int hpos = 0;                    // host copy of the position (steps are deterministic)
+    size_t weight_bytes = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    hipStream_t cap = nullptr;       // the stream the step is captured on (the legacy stream cannot capture)
+};
+
+namespace {
+
+int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
+{
+    const eif_hip_bitnet_config &c = m->c;
+    embed_kernel<<<1, 256, 0, st>>>(m->emb, m->emb_scale, m->state, m->x, c.dim, c.vocab);
+    EIF_HIP_LAUNCHED();
+    const float inv_sqrt_hd = 1.0f / sqrtf((float)c.head_dim);
+    for (int l = 0; l < c.n_layers; ++l) {
+        eif_hip_prep_spec sp{};
+        sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_att[l], sp.eps = c.rms_eps;
+        sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
+        int rc = eif_hip_qlinear_prep(m->wqkv[l], &sp, nullptr, m->qkv, m->q_dim + 2 * m->kv_dim, 1, st);
+        if (rc) return rc;
+        const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
+        auto attn = c.head_dim == 128 ? attn_decode_kernel<128>
+                    : (c.head_dim == 64 ? attn_decode_kernel<64> : attn_decode_kernel<32>);
+        attn<<<c.n_heads, kAttnThreads, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state, m->xb,
+                                                 c.n_heads, c.n_kv_heads, c.seq_len, c.rope_theta, inv_sqrt_hd);
+        EIF_HIP_LAUNCHED();
+        sp = eif_hip_prep_spec{};
+        sp.x = m->xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l], sp.eps = c.sub_eps;
+        sp.signs = m->signs_q, sp.wht_block = c.wht_q, sp.wht_norm = c.wht_norm_q;
+        if ((rc = eif_hip_qlinear_prep(m->wo[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += O xb
+        sp = eif_hip_prep_spec{};
+        sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_ffn[l], sp.eps = c.rms_eps;
+        sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
+        if ((rc = eif_hip_qlinear_prep(m->w13[l], &sp, nullptr, m->hb, 2 * c.hidden, 1, st))) return rc;
+        sp = eif_hip_prep_spec{};
+        sp.x = m->hb, sp.x2 = m->hb + c.hidden, sp.ldx = c.hidden, sp.pre = EIF_HIP_PRE_SWIGLU_RMS;
+        sp.norm_w = m->rms_sub_ffn[l], sp.eps = c.sub_eps;
+        sp.signs = m->signs_hidden, sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
+        if ((rc = eif_hip_qlinear_prep(m->w2[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += W2 h
+    }
+    eif_hip_prep_spec sp{};
+    sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_final, sp.eps = c.rms_eps;
+    int rc = eif_hip_qlinear_prep(m->head, &sp, nullptr, m->logits, c.vocab, 1, st);
+    if (rc) return rc;
+    sample_kernel<<<1, 1024, 0, st>>>(m->logits, c.vocab, m->state, m->prompt, m->seq, c.seq_len);
+    EIF_HIP_LAUNCHED();
+    return EIF_HIP_OK;
+}
+
+// Rows of two reference-format ternary matrices stacked (same columns): codes and grouped scales.
+void stack_rows(std::vector<uint8_t> &codes, std::vector<float> &scales, const uint8_t *w, const float *s, int rows,
+                int cols, int group)
+{
+    const size_t rb = (size_t)(cols + 3) / 4, ng = (size_t)(cols + group - 1) / group;
+    codes.insert(codes.end(), w, w + rows * rb);
+    scales.insert(scales.end(), s, s + rows * ng);
+}
+
+int make_tern(eif_hip_qweight **q, const std::vector<uint8_t> &codes, const std::vector<float> &scales, int rows,
+              int cols, int group, size_t *bytes)
+{
+    const int rc = eif_hip_qweight_create(q, EIF_HIP_W_TERNARY, rows, cols, group, codes.data(), scales.data(), 0,
+                                          nullptr);
+    if (rc == EIF_HIP_OK) {
+        size_t b = 0;
+        eif_hip_qweight_info(*q, nullptr, nullptr, nullptr, nullptr, &b);
+        *bytes += b;
+    }
+    return rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg)
+{
+    if (!out || !cfg) return EIF_HIP_E_ARG;
+    *out = nullptr;
+    const eif_hip_bitnet_config &c = *cfg;
+    if (c.dim <= 0 || c.hidden <= 0 || c.n_layers <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.vocab <= 0 ||
+        c.n_heads % c.n_kv_heads || (c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128) || c.seq_len <= 0 ||
+        c.seq_len > kMaxSeq || c.dim % 32 || c.hidden % 32 || (c.n_heads * c.head_dim) % 32)
+        return EIF_HIP_E_ARG;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return EIF_HIP_E_DEVICE;
+    int rc = eif_hip_init(dev);
+    if (rc) return rc;
+    eif_hip_bitnet *m = new (std::nothrow) eif_hip_bitnet;
+    if (!m) return EIF_HIP_E_NOMEM;
+    m->c = c;
+    m->q_dim = c.n_heads * c.head_dim;
+    m->kv_dim = c.n_kv_heads * c.head_dim;
+    const size_t cache = (size_t)c.n_layers * c.n_kv_heads * c.seq_len * c.head_dim;
+    m->wqkv.assign(c.n_layers, nullptr), m->wo.assign(c.n_layers, nullptr);
+    m->w13.assign(c.n_layers, nullptr), m->w2.assign(c.n_layers, nullptr);
+    m->rms_att.assign(c.n_layers, nullptr), m->rms_ffn.assign(c.n_layers, nullptr);
+    m->rms_sub_att.assign(c.n_layers, nullptr), m->rms_sub_ffn.assign(c.n_layers, nullptr);
+    if (hipMalloc(&m->x, sizeof(float) * c.dim) != hipSuccess ||
+        hipMalloc(&m->xb, sizeof(float) * m->q_dim) != hipSuccess ||
+        hipMalloc(&m->qkv, sizeof(float) * (m->q_dim + 2 * m->kv_dim)) != hipSuccess ||
+        hipMalloc(&m->hb, sizeof(float) * 2 * c.hidden) != hipSuccess ||
+        hipMalloc(&m->logits, sizeof(float) * c.vocab) != hipSuccess ||
+        hipMalloc(&m->kc, sizeof(__half) * cache) != hipSuccess ||
+        hipMalloc(&m->vc, sizeof(__half) * cache) != hipSuccess ||
+        hipMalloc(&m->state, sizeof(int) * 4) != hipSuccess ||
+        hipMalloc(&m->prompt, sizeof(int) * c.seq_len) != hipSuccess ||
+        hipMalloc(&m->seq, sizeof(int) * c.seq_len) != hipSuccess) {
+        eif_hip_bitnet_destroy(m);
+        return EIF_HIP_E_NOMEM;
+    }
+    *out = m;
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_set_layer(eif_hip_bitnet *m, int l, const eif_hip_bitnet_layer *w)
+{
+    if (!m || !w || l < 0 || l >= m->c.n_layers || !w->wq || !w->wk || !w->wv || !w->wo || !w->w1 || !w->w3 ||
+        !w->w2 || !w->gq || !w->gk || !w->gv || !w->go || !w->g1 || !w->g3 || !w->g2)
+        return EIF_HIP_E_ARG;
+    const eif_hip_bitnet_config &c = m->c;
+    if (m->exec) return EIF_HIP_E_ARG;   // weights are baked into the captured step
+    std::vector<uint8_t> codes;
+    std::vector<float> scales;
+    int rc;
+    stack_rows(codes, scales, w->wq, w->gq, m->q_dim, c.dim, c.g_q);
+    stack_rows(codes, scales, w->wk, w->gk, m->kv_dim, c.dim, c.g_q);
+    stack_rows(codes, scales, w->wv, w->gv, m->kv_dim, c.dim, c.g_q);
+    if ((rc = make_tern(&m->wqkv[l], codes, scales, m->q_dim + 2 * m->kv_dim, c.dim, c.g_q, &m->weight_bytes))) return rc;
+    codes.clear(), scales.clear();
+    stack_rows(codes, scales, w->wo, w->go, c.dim, m->q_dim, c.g_o);
+    if ((rc = make_tern(&m->wo[l], codes, scales, c.dim, m->q_dim, c.g_o, &m->weight_bytes))) return rc;
+    codes.clear(), scales.clear();
+    stack_rows(codes, scales, w->w1, w->g1, c.hidden, c.dim, c.g_13);
+    stack_rows(codes, scales, w->w3, w->g3, c.hidden, c.dim, c.g_13);
+    if ((rc = make_tern(&m->w13[l], codes, scales, 2 * c.hidden, c.dim, c.g_13, &m->weight_bytes))) return rc;
+    codes.clear(), scales.clear();
+    stack_rows(codes, scales, w->w2, w->g2, c.dim, c.hidden, c.g_2);
+    if ((rc = make_tern(&m->w2[l], codes, scales, c.dim, c.hidden, c.g_2, &m->weight_bytes))) return rc;
+    if ((rc = dev_upload(&m->rms_att[l], w->rms_att, c.dim)) || (rc = dev_upload(&m->rms_ffn[l], w->rms_ffn, c.dim)) ||
+        (rc = dev_upload(&m->rms_sub_att[l], w->rms_sub_att, m->q_dim)) ||
+        (rc = dev_upload(&m->rms_sub_ffn[l], w->rms_sub_ffn, c.hidden)))
+        return rc;
+    m->weight_bytes += sizeof(float) * (2 * c.dim + m->q_dim + c.hidden);
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *g)
+{
+    if (!m || !g || !g->emb || !g->wcls) return EIF_HIP_E_ARG;
+    if (m->exec) return EIF_HIP_E_ARG;
+    const eif_hip_bitnet_config &c = m->c;
+    int rc;
+    if ((rc = dev_upload(&m->emb, g->emb, (size_t)c.vocab * c.dim)) ||
+        (rc = dev_upload(&m->emb_scale, g->emb_scale, (size_t)c.vocab)) ||
+        (rc = dev_upload(&m->rms_final, g->rms_final, (size_t)c.dim)) ||
+        (rc = dev_upload(&m->signs_dim, g->signs_dim, (size_t)c.dim)) ||
+        (rc = dev_upload(&m->signs_q, g->signs_q, (size_t)m->q_dim)) ||
+        (rc = dev_upload(&m->signs_hidden, g->signs_hidden, (size_t)c.hidden)))
+        return rc;
+    if ((rc = eif_hip_qweight_create(&m->head, EIF_HIP_W_INT8, c.vocab, c.dim, 0, g->wcls, g->wcls_scale, 0,
+                                     nullptr)))
+        return rc;
+    size_t b = 0;
+    eif_hip_qweight_info(m->head, nullptr, nullptr, nullptr, nullptr, &b);
+    m->weight_bytes += b + sizeof(float) * c.dim;
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, void *stream)
+{
+    if (!m || !prompt || n_prompt < 1 || n_prompt > m->c.seq_len) return EIF_HIP_E_ARG;
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt[i] < 0 || prompt[i] >= m->c.vocab) return EIF_HIP_E_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    const eif_hip_bitnet_config &c = m->c;
+    const size_t cache = (size_t)c.n_layers * c.n_kv_heads * c.seq_len * c.head_dim;
+    EIF_HIP_TRY(hipMemcpyAsync(m->prompt, prompt, sizeof(int) * n_prompt, hipMemcpyHostToDevice, st));
+    fill_half_kernel<<<1024, 256, 0, st>>>(m->kc, cache);
+    EIF_HIP_LAUNCHED();
+    fill_half_kernel<<<1024, 256, 0, st>>>(m->vc, cache);
+    EIF_HIP_LAUNCHED();
+    start_kernel<<<1, 1, 0, st>>>(m->state, m->seq, m->prompt, n_prompt);
+    EIF_HIP_LAUNCHED();
+    EIF_HIP_TRY(hipStreamSynchronize(st));   // the prompt buffer is the caller's
+    m->hpos = 0;
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream)
+{
+    if (!m || n < 0 || !m->head || !m->emb) return EIF_HIP_E_ARG;
+    for (int l = 0; l < m->c.n_layers; ++l)
+        if (!m->wqkv[l]) return EIF_HIP_E_ARG;
+    if (m->hpos + n > m->c.seq_len) return EIF_HIP_E_LIMIT;
+    hipStream_t st = (hipStream_t)stream;
+    if (use_graph && !m->exec) {   // capture once, on the model's own stream; replay on the caller's
+        if (!m->cap) EIF_HIP_TRY(hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking));
+        EIF_HIP_TRY(hipStreamBeginCapture(m->cap, hipStreamCaptureModeRelaxed));
+        const int rc = enqueue_step(m, m->cap);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(m->cap, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        EIF_HIP_TRY(e);
+        m->graph = g;
+        EIF_HIP_TRY(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    }
+    for (int i = 0; i < n; ++i) {
+        if (use_graph) {
+            EIF_HIP_TRY(hipGraphLaunch(m->exec, st));
+        } else {
+            const int rc = enqueue_step(m, st);
+            if (rc) return rc;
+        }
+        ++m->hpos;
+    }
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_tokens(eif_hip_bitnet *m, int *out, int n, void *stream)
+{
+    if (!m || !out || n < 0 || n > m->c.seq_len) return EIF_HIP_E_ARG;
+    EIF_HIP_TRY(hipMemcpyAsync(out, m->seq, sizeof(int) * n, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    EIF_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_logits(eif_hip_bitnet *m, float *out, void *stream)
+{
+    if (!m || !out) return EIF_HIP_E_ARG;
+    EIF_HIP_TRY(hipMemcpyAsync(out, m->logits, sizeof(float) * m->c.vocab, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    EIF_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_position(eif_hip_bitnet *m, void *stream)
+{
+    if (!m) return EIF_HIP_E_ARG;
+    int s[4];
+    EIF_HIP_TRY(hipMemcpyAsync(s, m->state, sizeof(s), hipMemcpyDeviceToHost, (hipStream_t)stream));
+    EIF_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return s[0];
+}
+
+int eif_hip_bitnet_kv_cache(eif_hip_bitnet *m, int layer, int pos0, int n, float *k, float *v, void *stream)
+{
+    if (!m || !k || !v || layer < 0 || layer >= m->c.n_layers || pos0 < 0 || n < 0 || pos0 + n > m->c.seq_len)
+        return EIF_HIP_E_ARG;
+    const eif_hip_bitnet_config &c = m->c;
+    std::vector<__half> hk((size_t)c.n_kv_heads * n * c.head_dim), hv(hk.size());
+    const size_t cache_l = (size_t)layer * c.n_kv_heads * c.seq_len * c.head_dim;
+    hipStream_t st = (hipStream_t)stream;
+    for (int g = 0; g < c.n_kv_heads; ++g) {
+        const size_t src = cache_l + ((size_t)g * c.seq_len + pos0) * c.head_dim, cnt = (size_t)n * c.head_dim;
+        EIF_HIP_TRY(hipMemcpyAsync(hk.data() + g * cnt, m->kc + src, cnt * sizeof(__half), hipMemcpyDeviceToHost, st));
+        EIF_HIP_TRY(hipMemcpyAsync(hv.data() + g * cnt, m->vc + src, cnt * sizeof(__half), hipMemcpyDeviceToHost, st));
+    }
+    EIF_HIP_TRY(hipStreamSynchronize(st));
+    for (int g = 0; g < c.n_kv_heads; ++g)
+        for (int p = 0; p < n; ++p)
+            for (int i = 0; i < c.head_dim; ++i) {
+                const size_t s = ((size_t)g * n + p) * c.head_dim + i, d = (size_t)p * m->kv_dim + g * c.head_dim + i;
+                k[d] = __half2float(hk[s]);
+                v[d] = __half2float(hv[s]);
+            }
+    return EIF_HIP_OK;
+}
+
+size_t eif_hip_bitnet_weight_bytes(const eif_hip_bitnet *m) { return m ? m->weight_bytes : 0; }
+
+size_t eif_hip_bitnet_kv_bytes(const eif_hip_bitnet *m, int p)
+{
+    if (!m) return 0;
+    return (size_t)m->c.n_layers * m->c.n_kv_heads * (size_t)(p + 1) * m->c.head_dim * 2 * sizeof(__half);
+}
+
+void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
+{
+    if (!m) return;
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    if (m->cap) (void)hipStreamDestroy(m->cap);
+    for (auto *v : {&m->wqkv, &m->wo, &m->w13, &m->w2})
+        for (eif_hip_qweight *q : *v) eif_hip_qweight_destroy(q);
+    eif_hip_qweight_destroy(m->head);
+    for (auto *v : {&m->rms_att, &m->rms_ffn, &m->rms_sub_att, &m->rms_sub_ffn})
+        for (float *p : *v)
+            if (p) (void)hipFree(p);
+    for (void *p : {(void *)m->rms_final, (void *)m->signs_dim, (void *)m->signs_q, (void *)m->signs_hidden,
+                    (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->hb,
+                    (void *)m->logits, (void *)m->kc, (void *)m->vc, (void *)m->state, (void *)m->prompt,
+                    (void *)m->seq})
+        if (p) (void)hipFree(p);
+    delete m;
+}
+
+}  // extern "C"

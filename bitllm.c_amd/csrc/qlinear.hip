@@ -511,7 +511,7 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
     if (p.pre != EIF_HIP_PRE_NONE) {   // uniform
         if (p.pre == EIF_HIP_PRE_SWIGLU_RMS) {
 #pragma unroll
-            for (int e = 0; e < E; ++e) v[e] = (v[e] / (1.0f + expf(-v[e]))) * (live ? v2[e] : 0.0f);
+            for (int e = 0; e < E; ++e) v[e] = (v[e] * (1.0f / (1.0f + expf(-v[e])))) * (live ? v2[e] : 0.0f);
         }
         // RMSNorm over the K columns: (v * (1 / sqrtf(sum(v^2) / K + eps))) * weight
         float ss = 0.0f;

@@ -106,7 +106,7 @@ int eif_hip_qlinear_f32_acc(const eif_hip_qweight *w, const float *x, int ldx, c
  *   EIF_HIP_PRE_NONE        the rows as given;
  *   EIF_HIP_PRE_RMS         RMSNorm: (x * (1 / sqrtf(sum(x^2) / K + eps))) * norm_w, the decoder's pre-norm
  *                           (src/eif_tinyllm.c:196-330, weight NULL = 1);
- *   EIF_HIP_PRE_SWIGLU_RMS  h = (x / (1 + expf(-x))) * x2 (SiLU gate times up, src/eif_tinyllm.c:740-780), then
+ *   EIF_HIP_PRE_SWIGLU_RMS  h = (x * (1 / (1 + expf(-x)))) * x2 (SiLU gate times up, src/eif_tinyllm.c:774-780), then
  *                           RMSNorm of h (the BitNet sub-norm before the down projection).            */
 #define EIF_HIP_PRE_NONE 0
 #define EIF_HIP_PRE_RMS 1

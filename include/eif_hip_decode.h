@@ -1,0 +1,92 @@
+/*
+ * eif_hip_decode.h -- BitNet-b1.58 decoder on one MI355X, built on the quantized-linear kernels of eif_hip.h.
+ *
+ * Replaces the token loop of the reference's tinyllm engine for the BitNet path: tinyllm_forward /
+ * tinyllm_forward_embedding_ex (src/eif_tinyllm.c:371-857, :1502-1506) and its greedy sampler
+ * tinyllm_sample_greedy (src/eif_tinyllm.c:1519-1530). One token step is 5 launches per layer plus 4:
+ *   embedding row (INT8 table x per-token scale)
+ *   per layer: [RMSNorm + WHT + INT8] QKV GEMV | RoPE + fp16 KV append + attention |
+ *              [sub-RMSNorm + WHT + INT8] O GEMV + residual | [RMSNorm + WHT + INT8] gate/up GEMV |
+ *              [SiLU(gate) * up + sub-RMSNorm + WHT + INT8] down GEMV + residual
+ *   [RMSNorm + INT8] INT8 head GEMV | argmax (greedy) or the next prompt token, position + 1
+ * The position and the current token live in device memory, so the step is captured once as a HIP graph and
+ * replayed per token with no host work in between.
+ *
+ * Weights are passed in the reference's formats (host pointers): 2-bit ternary rows as eif_pack_ternary writes
+ * them with grouped FP32 scales [rows, cols / group] (tinyllm_weights_t.bitnet_gscale, include/eif_tinyllm.h),
+ * RMSNorm weights, +-1 rotation signs, an INT8 embedding with per-token scales and an INT8 head with per-row
+ * scales. Compute: the linears on int8 activations (the contract of eif_hip_qlinear_prep), fp32 everything
+ * else, the KV cache in fp16. Calls on one model are not thread-safe; the stream argument orders them.
+ */
+#ifndef EIF_HIP_DECODE_H
+#define EIF_HIP_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct eif_hip_bitnet eif_hip_bitnet;
+
+typedef struct eif_hip_bitnet_config {
+    int dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len;
+    float rope_theta;                       /* RoPE base (half-split pairs, src/eif_tinyllm.c:476-507) */
+    float rms_eps;                          /* attention / FFN / final RMSNorm epsilon */
+    float sub_eps;                          /* sub-norm epsilon (1e-5 in the reference) */
+    int wht_dim, wht_q, wht_hidden;         /* WHT blocks of the inputs of wq/wk/wv/w1/w3, wo, w2 (0: none) */
+    float wht_norm_dim, wht_norm_q, wht_norm_hidden;   /* their scales, e.g. eif_hip_wht_norm(block) */
+    int g_q, g_o, g_13, g_2;                /* ternary groups of wq/wk/wv, wo, w1/w3, w2 */
+} eif_hip_bitnet_config;
+
+typedef struct eif_hip_bitnet_layer {       /* one layer, host pointers */
+    const uint8_t *wq, *wk, *wv, *wo, *w1, *w3, *w2;
+    const float *gq, *gk, *gv, *go, *g1, *g3, *g2;
+    const float *rms_att, *rms_ffn, *rms_sub_att, *rms_sub_ffn;   /* NULL = 1 */
+} eif_hip_bitnet_layer;
+
+typedef struct eif_hip_bitnet_globals {    /* host pointers */
+    const int8_t *emb;                      /* [vocab, dim] */
+    const float *emb_scale;                 /* [vocab] or NULL (= 1) */
+    const float *rms_final;                 /* [dim] or NULL */
+    const float *signs_dim, *signs_q, *signs_hidden;   /* or NULL */
+    const int8_t *wcls;                     /* [vocab, dim] */
+    const float *wcls_scale;                /* [vocab] or NULL */
+} eif_hip_bitnet_globals;
+
+/* Allocates the model (weights are set separately). Limits: head_dim 32, 64 or 128, n_heads a multiple of
+ * n_kv_heads, seq_len <= 4096, dim / q_dim / hidden multiples of 32 with the WHT blocks dividing them.      */
+int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg);
+int eif_hip_bitnet_set_layer(eif_hip_bitnet *m, int layer, const eif_hip_bitnet_layer *w);
+int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *g);
+
+/* Starts a sequence: clears the KV cache, uploads the prompt (n_prompt >= 1 ids), position 0.             */
+int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, void *stream);
+
+/* Runs n token steps from the current position. The step at position p consumes the current token and
+ * makes the next: the prompt's token p + 1 while the prompt lasts, the argmax of the logits after. Each
+ * made token is stored at index p + 1 of the sequence. Steps past seq_len return EIF_HIP_E_LIMIT.
+ * use_graph != 0 replays the step as a HIP graph (captured on the first such call) on the stream.       */
+int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream);
+
+/* The sequence so far (ids at positions 0 .. n-1) and the logits of the last step, copied to the host
+ * (synchronous).                                                                                        */
+int eif_hip_bitnet_tokens(eif_hip_bitnet *m, int *out, int n, void *stream);
+int eif_hip_bitnet_logits(eif_hip_bitnet *m, float *out, void *stream);
+int eif_hip_bitnet_position(eif_hip_bitnet *m, void *stream);   /* current position, or a negative error */
+
+/* Cached keys and values of one layer at positions [pos0, pos0 + n), as floats in the reference's cache layout
+ * [position][kv_head * head_dim + i] (src/eif_tinyllm.c:414-418), copied to the host (synchronous).           */
+int eif_hip_bitnet_kv_cache(eif_hip_bitnet *m, int layer, int pos0, int n, float *k, float *v, void *stream);
+
+/* Bytes of weights, scales and norms resident on the device, and the KV bytes one step reads at position p. */
+size_t eif_hip_bitnet_weight_bytes(const eif_hip_bitnet *m);
+size_t eif_hip_bitnet_kv_bytes(const eif_hip_bitnet *m, int p);
+
+void eif_hip_bitnet_destroy(eif_hip_bitnet *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

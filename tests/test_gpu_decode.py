@@ -1,0 +1,129 @@
+"""The GPU BitNet decoder (include/eif_hip_decode.h) against the decode oracle's INT8-activation form.
+
+Before each step the oracle is given the token and the KV cache the GPU holds (teacher forcing), so each
+comparison covers one step. The GPU sums RMSNorm, attention and softmax in another order than the oracle, so
+now and then an activation that sits on an int8 rounding boundary takes the neighbouring code: on these models
+the oracle's own logits move by up to 2.3% of their largest magnitude for a 3e-7 relative change of one norm
+weight. Per step the logits agree to 3e-2 of their largest magnitude with a correlation above 0.9995; over a
+run, the median step agrees to 2e-3. The greedy token agrees wherever the oracle's top-two margin exceeds the
+step's bound. A captured step replayed as a HIP graph gives the eager step's bits.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, P
+
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+import synth  # noqa: E402
+import oracle_api  # noqa: E402
+import make_golden  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+REL, REL_MEDIAN = 3e-2, 2e-3
+
+
+class OracleRun:
+    def __init__(self, oracle, cfg, w):
+        self.oracle, self.cfg = oracle, cfg
+        self.c, self.ws = oracle_api.bitnet_structs(cfg, w)
+        kv = cfg["n_kv_heads"] * cfg["head_dim"]
+        self.kc = np.zeros((cfg["n_layers"], cfg["seq_len"], kv), np.float32)
+        self.vc = np.zeros_like(self.kc)
+
+    def step(self, tok, pos):
+        lo = np.zeros(self.cfg["vocab"], np.float32)
+        assert self.oracle.orc_bitnet_forward(C.byref(self.c), C.byref(self.ws), P(self.kc), P(self.vc), int(tok), pos,
+                                              oracle_api.ORC_LIN_INT8, P(lo)) == 0
+        return lo
+
+
+def compare_steps(gpu, oracle, cfg, w, prompt, n_steps, graph):
+    m = gpu.BitnetModel(cfg, w)
+    orc = OracleRun(oracle, cfg, w)
+    try:
+        m.reset(prompt)
+        errs = []
+        for pos in range(n_steps):
+            for layer in range(cfg["n_layers"]):       # the GPU's cache for the positions before this step
+                if pos > 0:
+                    orc.kc[layer, :pos], orc.vc[layer, :pos] = m.kv_cache(layer, 0, pos)
+            m.steps(1, graph=graph)
+            lg = m.logits()
+            seq = m.tokens(pos + 2)
+            lo = orc.step(seq[pos], pos)
+            err = np.abs(lg - lo).max() / np.abs(lo).max()
+            errs.append(err)
+            assert err <= REL and np.corrcoef(lg, lo)[0, 1] > 0.9995, (pos, err)
+            if pos + 1 >= len(prompt):
+                assert seq[pos + 1] == int(np.argmax(lg))
+                top2 = np.sort(lo)[-2:]
+                if top2[1] - top2[0] > 2 * err * np.abs(lo).max() + 1e-6:   # a clear winner: the same token
+                    assert seq[pos + 1] == int(np.argmax(lo)), pos
+            else:
+                assert seq[pos + 1] == prompt[pos + 1]
+        assert np.median(errs) <= REL_MEDIAN, errs
+        assert m.position() == n_steps
+        return m.tokens(n_steps + 1), m.logits()
+    finally:
+        m.close()
+
+
+def tiny():
+    cfg = make_golden.decode_config()
+    return cfg, synth.bitnet_model(make_golden.DECODE_KEY, cfg)
+
+
+def test_decode_tiny_vs_oracle(gpu, oracle):
+    cfg, w = tiny()
+    compare_steps(gpu, oracle, cfg, w, [5], 16, graph=False)
+
+
+def test_decode_prompt_then_greedy(gpu, oracle):
+    cfg, w = tiny()
+    prompt = list(np.random.default_rng(3).integers(0, cfg["vocab"], 10))
+    toks, _ = compare_steps(gpu, oracle, cfg, w, prompt, 20, graph=False)
+    assert list(toks[:10]) == prompt
+
+
+def test_decode_head128_gqa(gpu, oracle):
+    # head_dim 128, 4 query heads per kv head, g128 inputs / g96 down, WHT-128 everywhere, two 64-token prompts
+    cfg = synth.bitnet_config(512, 768, 3, 8, 2, 128, 1000, 96, 128, 96, 128, 128, 128)
+    w = synth.bitnet_model((8,), cfg)
+    prompt = list(np.random.default_rng(4).integers(0, cfg["vocab"], 64))
+    compare_steps(gpu, oracle, cfg, w, prompt, 80, graph=False)
+
+
+def test_decode_graph_equals_eager(gpu, oracle):
+    cfg, w = tiny()
+    prompt = [7, 11, 13]
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        m.reset(prompt)
+        m.steps(20, graph=False)
+        eager_t, eager_l = m.tokens(21), m.logits()
+        m.reset(prompt)
+        m.steps(5, graph=True)
+        m.steps(15, graph=True)
+        graph_t, graph_l = m.tokens(21), m.logits()
+    finally:
+        m.close()
+    assert np.array_equal(eager_t, graph_t)
+    assert np.array_equal(eager_l.view(np.uint32), graph_l.view(np.uint32))
+
+
+def test_decode_limits(gpu):
+    cfg, w = tiny()
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        with pytest.raises(gpu.HipError):
+            m.reset([cfg["vocab"]])            # token out of range
+        m.reset([1])
+        m.steps(cfg["seq_len"])
+        with pytest.raises(gpu.HipError):
+            m.steps(1)                         # past the context
+    finally:
+        m.close()
