@@ -34,6 +34,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-decode", action="store_true", help="skip the 30-layer decode")
+    ap.add_argument("--decode-tokens", type=int, default=128)
+    ap.add_argument("--decode-prompt", type=int, default=512)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (known bytes for counter calibration)")
     return ap.parse_args()
@@ -228,6 +231,9 @@ def main():
         for w in cs.values():
             w.close()
 
+    if not args.no_decode:
+        out["decode"] = decode_workload(args, torch, bh, synth, np)
+
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args, np, synth, step_bytes)
         if out["cpu_baseline"].get("value"):
@@ -344,6 +350,90 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
     ex["d2d_copy_GBps"] = round(2 * src.numel() * 4 / t / 1e9, 1)
     del src, dst
     return ex
+
+
+def decode_workload(args, torch, bh, synth, np):
+    """Greedy decode on the 30-layer BitNet-b1.58-2B-shaped model (random init): a random-id prompt of
+    --decode-prompt tokens (fed one step per token, not timed), then --decode-tokens greedy tokens timed as HIP
+    graph replays of the token step. Bytes per token = the resident weights the step reads (ternary codes,
+    group scales, norms, INT8 head) + the fp16 KV cache read at that position."""
+    c = dict(synth.BITNET_2B_DECODE)
+    cfg = synth.bitnet_config(c.pop("dim"), c.pop("hidden"), c.pop("n_layers"), c.pop("n_heads"), c.pop("n_kv_heads"),
+                              c.pop("head_dim"), c.pop("vocab"), c.pop("seq_len"), c.pop("group_in"),
+                              c.pop("group_down"), c.pop("wht_dim"), c.pop("wht_q"), c.pop("wht_hidden"))
+    t0 = time.perf_counter()
+    w = synth.bitnet_model((300,), cfg)
+    gen_s = time.perf_counter() - t0
+    m = bh.BitnetModel(cfg, w)
+    npr, ntok = args.decode_prompt, args.decode_tokens
+    prompt = synth.rng(301).integers(0, cfg["vocab"], npr).astype(np.int32)
+    m.reset(prompt)
+    m.steps(npr - 1, graph=True)   # the prompt, teacher-forced
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    m.steps(ntok, graph=True)
+    b.record(s)
+    b.synchronize()
+    sec = a.elapsed_time(b) * 1e-3
+    toks = m.tokens(npr + ntok)
+    assert list(toks[:npr]) == list(prompt)
+    wb = m.weight_bytes()
+    kv = float(np.mean([m.kv_bytes(p) for p in range(npr - 1, npr - 1 + ntok)]))
+    per_tok = wb + kv
+    res = {"model": "bitnet-b1.58-2B-shaped, 30 layers, dim 2560, ffn 6912, 20/5 heads x 128, vocab 128256 (INT8 head)",
+           "prompt": npr, "tokens": ntok, "context": cfg["seq_len"], "kv": "fp16",
+           "ms_per_token": round(sec / ntok * 1e3, 4), "tok_per_s": round(ntok / sec, 1),
+           "bytes_per_token": int(per_tok), "weight_bytes": int(wb), "GBps": round(per_tok * ntok / sec / 1e9, 1),
+           "frac_hbm": round(per_tok * ntok / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "launches_per_token": 5 * cfg["n_layers"] + 3, "timing": "HIP graph of one token step, replayed; HIP events",
+           "weights_generated_s": round(gen_s, 1), "greedy_tail": [int(t) for t in toks[-8:]]}
+    m.close()
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_decode_baseline(args, np, synth, cfg, w)
+        if res["cpu_baseline"].get("ms_per_token"):
+            res["gpu_over_cpu"] = round(res["cpu_baseline"]["ms_per_token"] / res["ms_per_token"], 1)
+    return res
+
+
+def cpu_decode_baseline(args, np, synth, cfg, w):
+    """The reference's own tinyllm BitNet decode (oracle/ref_tinyllm_wrap.c over its sources, reference flags) of
+    the same weights on the host cores: g128 scales for every matrix (its one group bound cannot give the down
+    projection g96 alone; it reads 54 of the 72 scales of each down row), its own WHT blocks (512 / 256),
+    fp32 KV cache. A short prompt, then greedy steps for about --cpu-seconds."""
+    import ctypes as C
+    nthreads = min(16, os.cpu_count() or 1)
+    for k, v in (("OMP_NUM_THREADS", str(nthreads)), ("OMP_PROC_BIND", "close"), ("OMP_WAIT_POLICY", "ACTIVE"),
+                 ("GOMP_SPINCOUNT", "100000")):
+        os.environ.setdefault(k, v)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_api
+    path = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+    if not os.path.exists(path):
+        return {"ms_per_token": None, "kind": "none", "sample": "oracle/_ref/libref.so not built"}
+    ref = oracle_api.load_ref_tinyllm(path)
+    c, ws = oracle_api.bitnet_structs(cfg, w)
+    h = ref.ref_bitnet_create(C.byref(c), C.byref(ws), 128)
+    if not h:
+        return {"ms_per_token": None, "kind": "reference", "sample": "model construction failed"}
+    try:
+        tok, times, pos = 1, [], 0
+        t_end = time.perf_counter() + args.cpu_seconds
+        while pos < 64 and (time.perf_counter() < t_end or len(times) < 3):
+            t0 = time.perf_counter()
+            lp = ref.ref_bitnet_forward(h, tok, pos)
+            lo = np.ctypeslib.as_array(lp, shape=(cfg["vocab"],))
+            tok = int(np.argmax(lo))
+            if pos >= 2:
+                times.append(time.perf_counter() - t0)
+            pos += 1
+    finally:
+        ref.ref_bitnet_destroy(h)
+    med = float(np.median(times))
+    return {"ms_per_token": round(med * 1e3, 2), "tok_per_s": round(1.0 / med, 2), "cores": nthreads,
+            "kind": "reference",
+            "sample": f"{len(times)} greedy steps at positions 2..{pos - 1}, median; OMP_NUM_THREADS={os.environ['OMP_NUM_THREADS']}"}
 
 
 def cpu_baseline(args, np, synth, step_bytes):

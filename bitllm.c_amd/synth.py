@@ -115,6 +115,17 @@ def int_linear_bytes(N, K, bits, M):
     return N * ((K * bits + 7) // 8) + 4 * N + M * (K + 4) + 4 * M * N
 
 
+# byte value of 4 ternary codes (t0 + 3 t1 + 9 t2 + 27 t3, digit d = value + 1) in the 2-bit packing
+_TERN4 = np.array([sum({0: 2, 1: 0, 2: 1}[(v // 3 ** p) % 3] << (2 * p) for p in range(4)) for v in range(81)], np.uint8)
+
+
+def ternary_packed(key, rows, cols):
+    """Packed 2-bit rows [rows, cols/4] of codes uniform over {-1, 0, +1} (cols a multiple of 4): one uniform
+    draw in [0, 81) per byte, mapped through the 81 four-code combinations."""
+    assert cols % 4 == 0
+    return _TERN4[rng(*key).integers(0, 81, size=(rows, cols // 4), dtype=np.uint8)]
+
+
 def bitnet_config(dim, hidden, n_layers, n_heads, n_kv_heads, head_dim, vocab, seq_len, group_in, group_down,
                   wht_dim, wht_q, wht_hidden, rope_theta=500000.0, rms_eps=None, sub_eps=1e-5):
     """A BitNet-b1.58 decoder configuration (the reference's tinyllm BitNet model, src/eif_tinyllm.c:371-857).
@@ -151,8 +162,7 @@ def bitnet_model(key, cfg):
     shapes = {"q": (qd, d, cfg["g_q"]), "k": (kvd, d, cfg["g_q"]), "v": (kvd, d, cfg["g_q"]), "o": (d, qd, cfg["g_o"]),
               "1": (h, d, cfg["g_13"]), "3": (h, d, cfg["g_13"]), "2": (d, h, cfg["g_2"])}
     for i, (name, (N, K, g)) in enumerate(shapes.items()):
-        codes = rng(*key, 20 + i).integers(-1, 2, size=(L * N, K), dtype=np.int8)
-        w["w" + name] = pack_ternary(codes)
+        w["w" + name] = ternary_packed((*key, 20 + i), L * N, K)
         ng = -(-K // g)
         w["g" + name] = (np.abs(rng(*key, 30 + i).standard_normal((L * N, ng))) * 0.02 + 0.005).astype(np.float32)
     for i, (name, n) in enumerate((("rms_att", d), ("rms_ffn", d), ("rms_sub_att", qd), ("rms_sub_ffn", h))):
