@@ -47,6 +47,7 @@ class BitnetGlobals(C.Structure):
 _SIGS = {
     "eif_hip_qlinear_prep": (_i, [_vp, C.POINTER(PrepSpec), _vp, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_prep_acc": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _vp]),
+    "eif_hip_prep_spec_rows": (_i, [C.POINTER(PrepSpec), _i, _vp, _i, _vp, _i, _vp]),
     "eif_hip_bitnet_create": (_i, [C.POINTER(_vp), C.POINTER(BitnetConfig)]),
     "eif_hip_bitnet_set_layer": (_i, [_vp, _i, C.POINTER(BitnetLayer)]),
     "eif_hip_bitnet_set_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
@@ -208,6 +209,12 @@ def prep_spec(x, pre=PRE_NONE, x2=None, norm_w=None, eps=0.0, signs=None, block=
     return PrepSpec(x=ptr(x).value, ldx=x.stride(0) if x.dim() > 1 else x.shape[-1], x2=ptr(x2).value if x2 is not None else None,
                     norm_w=ptr(norm_w).value if norm_w is not None else None, eps=eps, pre=pre,
                     signs=ptr(signs).value if signs is not None else None, wht_block=block, wht_norm=norm)
+
+
+def prep_spec_rows(spec, K, xq, xs, M, stream=None):
+    """The prep of a spec on its own: M rows of K columns -> xq [M, ldq] int8 + xs [M] (device tensors)."""
+    check(load().eif_hip_prep_spec_rows(C.byref(spec), K, ptr(xq), xq.stride(0), ptr(xs), M, stream_ptr(stream)),
+          "eif_hip_prep_spec_rows")
 
 
 class BitnetModel:

@@ -2,12 +2,14 @@
 //
 // The step follows tinyllm_forward_embedding_ex's BitNet path (src/eif_tinyllm.c:371-857) with every linear on
 // the fused prep + int8-MFMA GEMV of qlinear.hip (eif_hip_qlinear_prep: RMSNorm / SiLU-gate + RMSNorm, WHT,
-// absmax INT8, group-scaled ternary GEMV, residual as the epilogue bias) and three small kernels of its own:
-//   embed_kernel        x = INT8 embedding row * per-token scale (src/eif_tinyllm.c:902-916)
+// absmax INT8, group-scaled ternary GEMV, residual as the epilogue bias), the INT8 head as a prep launch plus
+// the GEMV with per-tile maxima (the argmax's first stage), and kernels of its own:
 //   attn_decode_kernel  RoPE of q and k (:396-405, :476-507), fp16 KV append, softmax attention (:555-650);
-//                       one workgroup per query head
-//   sample_kernel       greedy argmax (first maximum, src/eif_tinyllm.c:1519-1530) or the next prompt token,
-//                       stored in the sequence; position + 1
+//                       one workgroup per query head, one pass over the cache
+//   sample_kernel       greedy argmax over the head's tile maxima (first maximum, src/eif_tinyllm.c:1519-1530)
+//                       or the next prompt token, stored in the sequence; position + 1; x = the next token's
+//                       INT8 embedding row * its scale (src/eif_tinyllm.c:902-916)
+//   embed_kernel        the same embedding for the first token, at reset
 // Device state (position, current token, prompt, sequence) lets one captured HIP graph serve every step.
 #include <hip/hip_fp16.h>
 
@@ -20,7 +22,7 @@
 namespace {
 
 constexpr int kMaxSeq = 4096;
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 1024;
 
 // state[0] = position of the step about to run, state[1] = its token, state[2] = prompt length
 __global__ __launch_bounds__(256) void embed_kernel(const int8_t *emb, const float *emb_scale, const int *state,
@@ -33,30 +35,47 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *emb, const flo
     for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = (float)row[i] * sc;
 }
 
-// One workgroup per query head h (kv head g = h / kv_mul). Threads hold 8 of the HD dimensions of one key /
-// value row: DPR threads per row, RPP rows per pass over the positions.
+// 8 consecutive fp16 values -> float.
+EIF_DEV void half8_to_float(const uint4 &raw, float (&f)[8])
+{
+    const __half2 *hp = reinterpret_cast<const __half2 *>(&raw);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float2 v = __half22float2(hp[i]);
+        f[2 * i] = v.x, f[2 * i + 1] = v.y;
+    }
+}
+
+// One workgroup per query head h (kv head g = h / kv_mul), kAttnThreads threads, one pass over the cache.
+// A thread holds 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG row groups;
+// row group r takes positions r, r + RG, r + 2 RG, ... in batches of UNR rows whose keys and values are loaded
+// together, and keeps a running softmax over them (max m, sum l, the weighted value sums o of its 8 dims).
 //   1. RoPE of q_h and of k_g at position pos (the rotated k and v rounded to fp16, as the cache stores them);
 //      the first query head of each kv head appends them to the cache
-//   2. scores s_t = (q . k_t) / sqrt(HD), t <= pos (the current position from the workgroup's own copy)
-//   3. softmax: max, exp(s - max), sum, times 1 / sum
-//   4. out_h = sum_t p_t v_t
-// Cache layout: [kv_head][seq_len][HD] fp16 per layer.
+//   2. per row group, per batch: s_t = (q . k_t) / sqrt(HD), m' = max(m, s_t), l = l e^(m - m') +
+//      sum e^(s_t - m'), o = o e^(m - m') + sum e^(s_t - m') v_t; position pos (row group 0) from the
+//      workgroup's own copy of k and v
+//   3. the row groups combined: M = max_r m_r, out = sum_r e^(m_r - M) o_r / sum_r e^(m_r - M) l_r
+// This is the softmax of the scores over positions 0 .. pos followed by the weighted sum of the values, with
+// the sums taken in another order. Cache layout: [kv_head][seq_len][HD] fp16 per layer.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *qkv, __half *kc, __half *vc,
                                                                    const int *state, float *out, int n_heads,
                                                                    int n_kv, int seq_len, float theta,
                                                                    float inv_sqrt_hd)
 {
-    constexpr int DPR = HD / 8, RPP = kAttnThreads / DPR, HALF = HD / 2;
+    constexpr int DPR = HD / 8, RG = kAttnThreads / DPR, HALF = HD / 2, UNR = 8;
+    constexpr int PARTS = kAttnThreads / HD;   // threads per output dimension in the combine
     __shared__ float q_l[HD], k_l[HD], v_l[HD];
-    __shared__ float s_l[kMaxSeq];
-    __shared__ float red[kAttnThreads / 64];
-    __shared__ float acc_l[RPP][HD + 4];
+    __shared__ __align__(16) float m_l[RG];
+    __shared__ float l_l[RG];
+    __shared__ float o_l[RG][HD + 4];
+    __shared__ float po_l[PARTS][HD], pl_l[PARTS];
     const int h = blockIdx.x, kv_mul = n_heads / n_kv, g = h / kv_mul;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
     const int pos = state[0];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    __half *kcg = kc + (size_t)g * seq_len * HD, *vcg = vc + (size_t)g * seq_len * HD;
+    const int t = threadIdx.x;
+    const __half *kcg = kc + (size_t)g * seq_len * HD, *vcg = vc + (size_t)g * seq_len * HD;
 
     // 1. RoPE (half-split pairs j, j + HD/2) and the current k, v
     if (t < HALF) {
@@ -73,107 +92,127 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *
         k_l[t] = __half2float(k0), k_l[t + HALF] = __half2float(k1);
         v_l[t] = __half2float(v0), v_l[t + HALF] = __half2float(v1);
         if (h % kv_mul == 0) {
-            kcg[(size_t)pos * HD + t] = k0, kcg[(size_t)pos * HD + t + HALF] = k1;
-            vcg[(size_t)pos * HD + t] = v0, vcg[(size_t)pos * HD + t + HALF] = v1;
+            __half *kw = kc + ((size_t)g * seq_len + pos) * HD, *vw = vc + ((size_t)g * seq_len + pos) * HD;
+            kw[t] = k0, kw[t + HALF] = k1;
+            vw[t] = v0, vw[t + HALF] = v1;
         }
     }
     __syncthreads();
 
-    // 2. scores
+    // 2. one pass over positions 0 .. pos - 1 of the cache, then position pos
     const int sub = t % DPR, r0 = t / DPR;
-    float qv[8];
+    float qv[8], o[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qv[i] = q_l[8 * sub + i];
-    for (int tt = r0; tt <= pos; tt += RPP) {
-        float kv8[8];
-        if (tt == pos) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) kv8[i] = k_l[8 * sub + i];
-        } else {
-            const uint4 raw = *reinterpret_cast<const uint4 *>(kcg + (size_t)tt * HD + 8 * sub);
-            const __half2 *hp = reinterpret_cast<const __half2 *>(&raw);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float2 f = __half22float2(hp[i]);
-                kv8[2 * i] = f.x, kv8[2 * i + 1] = f.y;
-            }
-        }
+    for (int i = 0; i < 8; ++i) qv[i] = q_l[8 * sub + i], o[i] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    auto score = [&](const float (&k8)[8]) {
         float d = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d = fmaf(qv[i], kv8[i], d);
+        for (int i = 0; i < 8; ++i) d = fmaf(qv[i], k8[i], d);
 #pragma unroll
         for (int off = 1; off < DPR; off <<= 1) d += __shfl_xor(d, off, 64);
-        if (sub == 0) s_l[tt] = d * inv_sqrt_hd;
-    }
-    __syncthreads();
-
-    // 3. softmax over s_l[0 .. pos]
-    float mx = -INFINITY;
-    for (int tt = t; tt <= pos; tt += kAttnThreads) mx = fmaxf(mx, s_l[tt]);
-    mx = eif_wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = red[0];
+        return d * inv_sqrt_hd;
+    };
+    for (int base = 0; base < pos; base += RG * UNR) {
+        uint4 kr[UNR], vr[UNR];
 #pragma unroll
-    for (int w = 1; w < kAttnThreads / 64; ++w) mx = fmaxf(mx, red[w]);
-    __syncthreads();
-    float sum = 0.0f;
-    for (int tt = t; tt <= pos; tt += kAttnThreads) {
-        const float e = expf(s_l[tt] - mx);
-        s_l[tt] = e;
-        sum += e;
-    }
-    sum = eif_wave_sum(sum);
-    if (lane == 0) red[wave] = sum;
-    __syncthreads();
-    sum = red[0];
+        for (int u = 0; u < UNR; ++u) {
+            const int tt = base + u * RG + r0;
+            const size_t off = (size_t)(tt < pos ? tt : 0) * HD + 8 * sub;
+            kr[u] = *reinterpret_cast<const uint4 *>(kcg + off);
+            vr[u] = *reinterpret_cast<const uint4 *>(vcg + off);
+        }
+        float sv[UNR];
+        float bm = -INFINITY;
 #pragma unroll
-    for (int w = 1; w < kAttnThreads / 64; ++w) sum += red[w];
-    const float inv = 1.0f / sum;
-
-    // 4. weighted sum of the values
-    float acc[8];
+        for (int u = 0; u < UNR; ++u) {
+            float k8[8];
+            half8_to_float(kr[u], k8);
+            const float d = score(k8);
+            sv[u] = base + u * RG + r0 < pos ? d : -INFINITY;
+            bm = fmaxf(bm, sv[u]);
+        }
+        const float mn = fmaxf(m, bm);
+        if (mn != -INFINITY) {   // the row group has rows in this batch or before
+            const float sc = expf(m - mn);
+            l = l * sc;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-    for (int tt = r0; tt <= pos; tt += RPP) {
-        const float p = s_l[tt] * inv;
-        if (tt == pos) {
+            for (int i = 0; i < 8; ++i) o[i] = o[i] * sc;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = fmaf(p, v_l[8 * sub + i], acc[i]);
-        } else {
-            const uint4 raw = *reinterpret_cast<const uint4 *>(vcg + (size_t)tt * HD + 8 * sub);
-            const __half2 *hp = reinterpret_cast<const __half2 *>(&raw);
+            for (int u = 0; u < UNR; ++u) {
+                const float pw = expf(sv[u] - mn);
+                float v8[8];
+                half8_to_float(vr[u], v8);
+                l = l + pw;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float2 f = __half22float2(hp[i]);
-                acc[2 * i] = fmaf(p, f.x, acc[2 * i]);
-                acc[2 * i + 1] = fmaf(p, f.y, acc[2 * i + 1]);
+                for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, v8[i], o[i]);
             }
+            m = mn;
         }
     }
+    {
+        float k8[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc_l[r0][8 * sub + i] = acc[i];
+        for (int i = 0; i < 8; ++i) k8[i] = k_l[8 * sub + i];
+        const float d = score(k8);   // every row group computes it (uniform shuffles); row group 0 keeps it
+        if (r0 == 0) {
+            const float mn = fmaxf(m, d);
+            const float sc = expf(m - mn), pw = expf(d - mn);
+            l = l * sc + pw;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, v_l[8 * sub + i], o[i] * sc);
+            m = mn;
+        }
+    }
+
+    // 3. combine the row groups
+    if (sub == 0) m_l[r0] = m, l_l[r0] = l;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o_l[r0][8 * sub + i] = o[i];
+    __syncthreads();
+    float mx = -INFINITY;
+#pragma unroll 4
+    for (int r = 0; r < RG; r += 4) {
+        const float4 m4 = *reinterpret_cast<const float4 *>(&m_l[r]);
+        mx = fmaxf(mx, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
+    }
+    {
+        const int d = t % HD, part = t / HD;
+        float os = 0.0f, ls = 0.0f;
+        for (int r = part; r < RG; r += PARTS) {
+            const float w = expf(m_l[r] - mx);   // 0 for a row group without rows
+            os = fmaf(w, o_l[r][d], os);
+            ls = fmaf(w, l_l[r], ls);
+        }
+        po_l[part][d] = os;
+        if (d == 0) pl_l[part] = ls;
+    }
     __syncthreads();
     if (t < HD) {
-        float o = 0.0f;
-        for (int r = 0; r < RPP; ++r) o += acc_l[r][t];
-        out[h * HD + t] = o;
+        float os = po_l[0][t], ls = pl_l[0];
+#pragma unroll
+        for (int q = 1; q < PARTS; ++q) os += po_l[q][t], ls += pl_l[q];
+        out[h * HD + t] = os / ls;
     }
 }
 
-// Greedy token: first index of the largest logit (NaN never wins). While the prompt lasts the next token is
-// the prompt's; the made token is stored at position pos + 1 of the sequence and the position advances.
-__global__ __launch_bounds__(1024) void sample_kernel(const float *logits, int vocab, int *state, const int *prompt,
-                                                      int *seq, int seq_len)
+// Greedy token: first index of the largest logit (NaN never wins), from the head GEMV's per-tile maxima (value,
+// row) pairs; while the prompt lasts the next token is the prompt's. The made token is stored at position
+// pos + 1 of the sequence, the position advances, and x becomes the next token's embedding row.
+__global__ __launch_bounds__(1024) void sample_kernel(const float *part_v, const int *part_i, int n_part, int *state,
+                                                      const int *prompt, int *seq, int seq_len, const int8_t *emb,
+                                                      const float *emb_scale, float *x, int dim, int vocab)
 {
     __shared__ float bv[16];
     __shared__ int bi[16];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    __shared__ int next_l;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = t; i < vocab; i += blockDim.x) {
-        const float x = logits[i];
-        if (x > v) v = x, idx = i;   // i increases: the first maximum of this thread's share
+    for (int i = t; i < n_part; i += nt) {
+        const float pv = part_v[i];
+        const int pi = part_i[i];
+        if (pv > v || (pv == v && pi < idx)) v = pv, idx = pi;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -184,15 +223,21 @@ __global__ __launch_bounds__(1024) void sample_kernel(const float *logits, int v
     if (lane == 0) bv[wave] = v, bi[wave] = idx;
     __syncthreads();
     if (t == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
+        for (int w = 1; w < nt / 64; ++w)
             if (bv[w] > v || (bv[w] == v && bi[w] < idx)) v = bv[w], idx = bi[w];
-        if (idx == 0x7fffffff) idx = 0;
+        if (idx < 0 || idx >= vocab) idx = 0;   // every logit NaN or -inf
         const int pos = state[0], np = state[2];
         const int next = pos + 1 < np ? prompt[pos + 1] : idx;
         if (pos + 1 < seq_len) seq[pos + 1] = next;
         state[1] = next;
         state[0] = pos + 1;
+        next_l = next;
     }
+    __syncthreads();
+    const int tok = next_l;
+    const float sc = emb_scale ? emb_scale[tok] : 1.0f;
+    const int8_t *row = emb + (size_t)tok * dim;
+    for (int i = t; i < dim; i += nt) x[i] = (float)row[i] * sc;
 }
 
 __global__ void fill_half_kernel(__half *p, size_t n)
@@ -233,6 +278,11 @@ struct eif_hip_bitnet {
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *hb = nullptr, *logits = nullptr;
     __half *kc = nullptr, *vc = nullptr;
     int *state = nullptr, *prompt = nullptr, *seq = nullptr;
+    int8_t *hq = nullptr;            // the head's prepped input row [head_kpad] and its scale
+    float *hs = nullptr;
+    float *amax_v = nullptr;         // the head's per-tile maxima [head_tiles]
+    int *amax_i = nullptr;
+    int head_kpad = 0, head_tiles = 0;
     int hpos = 0;                    // host copy of the position (steps are deterministic)
     size_t weight_bytes = 0;
     hipGraph_t graph = nullptr;
@@ -245,8 +295,6 @@ namespace {
 int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
 {
     const eif_hip_bitnet_config &c = m->c;
-    embed_kernel<<<1, 256, 0, st>>>(m->emb, m->emb_scale, m->state, m->x, c.dim, c.vocab);
-    EIF_HIP_LAUNCHED();
     const float inv_sqrt_hd = 1.0f / sqrtf((float)c.head_dim);
     for (int l = 0; l < c.n_layers; ++l) {
         eif_hip_prep_spec sp{};
@@ -274,11 +322,15 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         sp.signs = m->signs_hidden, sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
         if ((rc = eif_hip_qlinear_prep(m->w2[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += W2 h
     }
+    // head: RMSNorm + INT8 prep once, the INT8 GEMV with per-tile maxima, then the argmax over the tiles
     eif_hip_prep_spec sp{};
     sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_final, sp.eps = c.rms_eps;
-    int rc = eif_hip_qlinear_prep(m->head, &sp, nullptr, m->logits, c.vocab, 1, st);
+    int rc = eif_hip_prep_spec_rows(&sp, c.dim, m->hq, m->head_kpad, m->hs, 1, st);
     if (rc) return rc;
-    sample_kernel<<<1, 1024, 0, st>>>(m->logits, c.vocab, m->state, m->prompt, m->seq, c.seq_len);
+    if ((rc = eif::qlinear_argmax(m->head, m->hq, m->head_kpad, m->hs, m->logits, m->amax_v, m->amax_i, st)))
+        return rc;
+    sample_kernel<<<1, 1024, 0, st>>>(m->amax_v, m->amax_i, m->head_tiles, m->state, m->prompt, m->seq, c.seq_len,
+                                      m->emb, m->emb_scale, m->x, c.dim, c.vocab);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
@@ -384,7 +436,7 @@ int eif_hip_bitnet_set_layer(eif_hip_bitnet *m, int l, const eif_hip_bitnet_laye
 int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *g)
 {
     if (!m || !g || !g->emb || !g->wcls) return EIF_HIP_E_ARG;
-    if (m->exec) return EIF_HIP_E_ARG;
+    if (m->exec || m->head) return EIF_HIP_E_ARG;   // once, before the first captured step
     const eif_hip_bitnet_config &c = m->c;
     int rc;
     if ((rc = dev_upload(&m->emb, g->emb, (size_t)c.vocab * c.dim)) ||
@@ -398,14 +450,21 @@ int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *
                                      nullptr)))
         return rc;
     size_t b = 0;
-    eif_hip_qweight_info(m->head, nullptr, nullptr, nullptr, nullptr, &b);
+    int kp = 0;
+    eif_hip_qweight_info(m->head, nullptr, nullptr, &kp, nullptr, &b);
     m->weight_bytes += b + sizeof(float) * c.dim;
+    m->head_kpad = kp;
+    m->head_tiles = eif::qweight_row_tiles(m->head);
+    if (hipMalloc(&m->hq, (size_t)kp) != hipSuccess || hipMalloc(&m->hs, sizeof(float) * 4) != hipSuccess ||
+        hipMalloc(&m->amax_v, sizeof(float) * m->head_tiles) != hipSuccess ||
+        hipMalloc(&m->amax_i, sizeof(int) * m->head_tiles) != hipSuccess)
+        return EIF_HIP_E_NOMEM;
     return EIF_HIP_OK;
 }
 
 int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, void *stream)
 {
-    if (!m || !prompt || n_prompt < 1 || n_prompt > m->c.seq_len) return EIF_HIP_E_ARG;
+    if (!m || !prompt || n_prompt < 1 || n_prompt > m->c.seq_len || !m->emb || !m->head) return EIF_HIP_E_ARG;
     for (int i = 0; i < n_prompt; ++i)
         if (prompt[i] < 0 || prompt[i] >= m->c.vocab) return EIF_HIP_E_ARG;
     hipStream_t st = (hipStream_t)stream;
@@ -418,6 +477,8 @@ int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, voi
     EIF_HIP_LAUNCHED();
     start_kernel<<<1, 1, 0, st>>>(m->state, m->seq, m->prompt, n_prompt);
     EIF_HIP_LAUNCHED();
+    embed_kernel<<<1, 256, 0, st>>>(m->emb, m->emb_scale, m->state, m->x, c.dim, c.vocab);   // each step
+    EIF_HIP_LAUNCHED();                                                                      // leaves the next
     EIF_HIP_TRY(hipStreamSynchronize(st));   // the prompt buffer is the caller's
     m->hpos = 0;
     return EIF_HIP_OK;
@@ -528,7 +589,7 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
     for (void *p : {(void *)m->rms_final, (void *)m->signs_dim, (void *)m->signs_q, (void *)m->signs_hidden,
                     (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->hb,
                     (void *)m->logits, (void *)m->kc, (void *)m->vc, (void *)m->state, (void *)m->prompt,
-                    (void *)m->seq})
+                    (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_v, (void *)m->amax_i})
         if (p) (void)hipFree(p);
     delete m;
 }

@@ -53,6 +53,9 @@ int launch_quant_rows(const float *x, int ldx, int M, int K, int8_t *xq, int ldq
 
 int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *xq, int ldq, const float *xs,
                    const float *bias, float *y, int ldy, int M, int path, hipStream_t st);
+int qweight_row_tiles(const eif_hip_qweight *w);
+int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y, float *amax_v,
+                   int *amax_i, hipStream_t st);
 
 int launch_tern_f32(const uint8_t *W, const float *scales, int mode, int block, const float *x, const float *bias,
                     float *y, int rows, int cols, int il, hipStream_t st);

@@ -160,6 +160,8 @@ struct QArgs {
     int32_t *acc;          // parity output or NULL
     int M, N, nsteps;
     float *part;           // GEMM split along K: partial sums [split][M][N]
+    float *amax_v;         // row-scaled GEMV, M = 1: per 16-row tile, the largest output and its row
+    int *amax_i;           //   (first of equal maxima; NaN never wins), or NULL
 };
 
 // ---- tiled GEMM (token batches above the small-batch GEMV) ----
@@ -470,30 +472,22 @@ EIF_DEV void load4(const float *p, float (&v)[E])
 }
 
 // Thread t holds columns [E*t, E*t + E) of token row m (zeros past K). The loads are unconditional (clamped to
-// the row) or under uniform branches, and nothing consumes them here, so the weight loads issued next are not
-// held behind them; the pre-op, the sign flip and the zeroing past K happen in prep_finish.
-//   v: x; sg: signs; v2: x2 (SwiGLU); nw: the RMSNorm weight.
+// the row) and nothing consumes them here, so the weight loads issued next are not held behind them; the
+// pre-op, the sign flip and the zeroing past K happen in prep_finish.
+//   v: x; sg: signs; v2: x2 (SwiGLU); nw: the RMSNorm weight (operands that are absent hold x).
 template <int E>
 EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E], float (&v2)[E], float (&nw)[E])
 {
+    // Every load is issued, from x where an operand is absent (scalar pointer selects, no branches): a load
+    // count that is the same on every path lets the compiler wait for these loads alone, behind which the
+    // weight and scale loads stay in flight.
     const int i0 = E * threadIdx.x;
     const int ic = i0 < p.K ? i0 : 0;
-    load4<E>(p.x + (size_t)m * p.ldx + ic, v);
-    if (p.signs) {   // uniform: a scalar branch
-        load4<E>(p.signs + ic, sg);
-    } else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) sg[e] = 1.0f;
-    }
-    if (p.pre == EIF_HIP_PRE_SWIGLU_RMS) load4<E>(p.x2 + (size_t)m * p.ldx + ic, v2);
-    if (p.pre != EIF_HIP_PRE_NONE) {
-        if (p.nw) {
-            load4<E>(p.nw + ic, nw);
-        } else {
-#pragma unroll
-            for (int e = 0; e < E; ++e) nw[e] = 1.0f;
-        }
-    }
+    const float *xr = p.x + (size_t)m * p.ldx;
+    load4<E>(xr + ic, v);
+    load4<E>((p.signs ? p.signs : xr) + ic, sg);
+    load4<E>((p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 + (size_t)m * p.ldx : xr) + ic, v2);
+    load4<E>((p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : xr) + ic, nw);
 }
 
 // Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
@@ -524,7 +518,7 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
         for (int w = 0; w < nw; ++w) ss += red_ss[w];
         const float inv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = (v[e] * inv) * nwv[e];
+        for (int e = 0; e < E; ++e) v[e] = (v[e] * inv) * (p.nw ? nwv[e] : 1.0f);
     }
     if (flip) {
 #pragma unroll
@@ -647,21 +641,8 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         xs_v = a.xs[(int)threadIdx.x < a.M ? threadIdx.x : 0];
     }
 
-    // the workgroup's group scales, rows row0 .. row0 + TR - 1: one contiguous block of the [N, G] array,
-    // loaded flat (kMaxScLoads per thread at most, clamped to the array) and staged in LDS after the prep
-    float scv[kMaxScLoads];
-    const int nsc = TR * a.G, last_sc = a.N * a.G - 1;
-    if constexpr (GROUPED && !ACC) {
-#pragma unroll
-        for (int i = 0; i < kMaxScLoads; ++i) {
-            if (i > 0 && i * (int)blockDim.x >= nsc) break;   // uniform bound
-            const int idx = row0 * a.G + (int)threadIdx.x + i * (int)blockDim.x;
-            scv[i] = a.scales[idx < last_sc ? idx : last_sc];
-        }
-    }
-
-    // Keep the activation and scale loads ahead of the weight loads: loads complete in issue order, so staging
-    // them waits for them alone.
+    // Keep the activation loads ahead of the weight loads: loads complete in issue order, so staging them waits
+    // for them alone.
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. weight loads: unconditional, with the step clamped into the row (steps past nj are loaded from the
@@ -678,6 +659,31 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         }
     };
     load_chunk(0);
+
+    // the workgroup's group scales, rows row0 .. row0 + TR - 1: one contiguous block of the [N, G] array,
+    // loaded flat (kMaxScLoads per thread at most, clamped to the array) and staged in LDS after the prep. They
+    // are issued after the weight loads: the prep waits for the activation loads only (the oldest), and the
+    // scales are not needed before the weights.
+    __builtin_amdgcn_sched_barrier(0);
+    float scv[kMaxScLoads];
+    const int nsc = TR * a.G, last_sc = a.N * a.G - 1;
+    if constexpr (GROUPED && !ACC) {
+#pragma unroll
+        for (int i = 0; i < kMaxScLoads; ++i) {
+            if (i > 0 && i * (int)blockDim.x >= nsc) break;   // uniform bound
+            const int idx = row0 * a.G + (int)threadIdx.x + i * (int)blockDim.x;
+            scv[i] = a.scales[idx < last_sc ? idx : last_sc];
+        }
+    }
+    // row-scaled: the row's scale and bias, loaded now (from the weights' first word where absent, selected
+    // at use) so the epilogue does not wait on them
+    float rs_raw = 0.0f, bb_raw = 0.0f;
+    if constexpr (!GROUPED && !ACC) {
+        const int rc = row_ok ? row : a.N - 1;
+        const float *w0 = reinterpret_cast<const float *>(a.W);
+        rs_raw = *(a.scales ? a.scales + rc : w0);
+        bb_raw = *(a.bias ? a.bias + rc : w0);
+    }
 
     // 3. activations -> LDS
     if constexpr (E > 0) {
@@ -801,25 +807,53 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 #pragma unroll
                 for (int vv = 0; vv < 4; ++vv) C[vv] += red[((k * RT + rt) * 4 + vv) * 64 + lane];
         }
-        if (!row_ok) return;
-        const float rs = a.scales ? a.scales[row] : 1.0f;
-        const float bb = a.bias ? a.bias[row] : 0.0f;
+        const float rs = a.scales ? rs_raw : 1.0f;
+        float out0 = -INFINITY;
 #pragma unroll
         for (int vv = 0; vv < 4; ++vv) {
             const int tok = 4 * s + vv;
-            if (tok >= a.M) continue;
+            if (tok >= a.M || !row_ok) continue;
             const int isum = C[vv] >> GE::SHIFT;
             if constexpr (ACC) {
                 a.acc[(size_t)tok * a.N + row] = isum;
                 continue;
             }
             float out = ((float)isum * xs_l[tok]) * rs;
-            if (a.bias) out = out + bb;
+            if (a.bias) out = out + bb_raw;
             a.y[(size_t)tok * a.ldy + row] = out;
+            if (vv == 0) out0 = out;
+        }
+        if constexpr (!ACC) {
+            if (a.amax_v) {   // M = 1: lanes 0..15 (s = 0) hold the tile's rows; the tile's first largest
+                float bv = s == 0 && out0 == out0 ? out0 : -INFINITY;
+                int bi = s == 0 && row_ok ? row : 0x7fffffff;
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    const float ov = __shfl_xor(bv, off, 64);
+                    const int oi = __shfl_xor(bi, off, 64);
+                    if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+                }
+                if (lane == 0) {
+                    a.amax_v[blockIdx.x * RT + rt] = bv;
+                    a.amax_i[blockIdx.x * RT + rt] = bi;
+                }
+            }
         }
     }
 }
 
+
+// The fused prep on its own: token row m = blockIdx.x -> int8 codes xq[m, 0 .. ldq) (zeros past K) and xs[m].
+// E columns per thread, the threads covering ldq; LB as in prep_finish.
+template <int E, int LB>
+__global__ __launch_bounds__(1024) void prep_spec_kernel(PrepArgs p, int8_t *xq, float *xs)
+{
+    __shared__ float red_max[16], red_ss[16];
+    float v[E], sg[E], v2[E], nwv[E];
+    const int m = blockIdx.x;
+    prep_load<E>(p, m, v, sg, v2, nwv);
+    prep_finish<E, LB>(p, m, p.ldl, v, sg, v2, nwv, xq, xs, red_max, red_ss);
+}
 
 // ---- repack kernels: reference formats -> GPU layouts (one thread per destination dword) ----
 
@@ -902,16 +936,18 @@ int g_gemv_rt = 0;       // row tiles per workgroup of the GEMV, 0 = chosen from
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
 
-// Per-stream workspace of the GEMM's split along K (launches on one stream run in order, so one buffer per
-// stream suffices), grown outside graph capture. Buffers are never freed before the process ends, also when
-// replaced by larger ones: a graph captured on the stream keeps using the buffers it was captured with.
+// Per-stream workspaces (launches on one stream run in order, so one buffer per stream and purpose suffices):
+// slot 0 the GEMM's split along K, slot 1 the int8 rows of a separate prep. Grown outside graph capture (inside
+// a capture a missing buffer returns NULL and the caller takes another path). Buffers are never freed before the
+// process ends, also when replaced by larger ones: a graph captured on the stream keeps using the buffers it was
+// captured with.
 std::mutex g_ws_mu;
-std::unordered_map<hipStream_t, std::pair<float *, size_t>> g_ws;
+std::unordered_map<hipStream_t, std::pair<float *, size_t>> g_ws[2];
 
-float *split_ws(hipStream_t st, size_t bytes)
+float *split_ws(hipStream_t st, size_t bytes, int slot = 0)
 {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto &w = g_ws[st];
+    auto &w = g_ws[slot][st];
     if (w.second < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
@@ -979,6 +1015,11 @@ int launch_gemm(const QArgs &a, int rows_pad, hipStream_t st)
 // Waves per tile of the small-batch GEMV (measured on MI355X with graph-chained launches): two steps per wave
 // for the 1-9 MB matrices of a layer, four for long rows (>= 24 steps), eight when the tiles alone fill the
 // chip (vocabulary heads), at most 16 waves.
+// Row tiles from which a row-scaled GEMV of prepped activations is shaped for streaming (one tile per
+// workgroup, about 10 KiB of weights per wave) and from which eif_hip_qlinear_prep runs its prep separately once
+// instead of in every workgroup (the vocabulary heads).
+constexpr int kBigTiles = 4096;
+
 int pick_ks_gemv(int row_tiles, int nsteps)
 {
     const int spw = row_tiles >= 4096 ? 8 : (nsteps >= 24 ? 4 : 2);
@@ -1044,13 +1085,15 @@ int launch_gemv_rt(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int 
     return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 1>(a, p, rows_pad, ks, st);
 }
 
-// Fused prep: E columns per thread. The WHT-128 of the BitNet configurations is compiled with the block
-// fixed; other blocks read it at run time.
+// Fused prep: E columns per thread. The WHT-128 of the BitNet configurations and no rotation (the INT8 head)
+// are compiled with the block fixed; other blocks read it at run time.
 template <int FMT, int UD, bool GROUPED, bool ACC, int E>
 int launch_gemv_fused(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int ks, hipStream_t st)
 {
-    if constexpr (E <= 8 && gemv_tuned<FMT, UD, GROUPED>())
+    if constexpr (E <= 8 && gemv_tuned<FMT, UD, GROUPED>()) {
         if (p.block == 128) return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 7>(a, p, rows_pad, rt, ks, st);
+        if (p.block == 0 && !ACC) return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 0>(a, p, rows_pad, rt, ks, st);
+    }
     return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, -1>(a, p, rows_pad, rt, ks, st);
 }
 
@@ -1064,6 +1107,12 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     const int kpad = a.nsteps * Geo<FMT, UD>::SC;
     const int maxks = 16 / rt;
     int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(rows_pad / 16, a.nsteps);
+    if (!GROUPED && !p.x && rows_pad / 16 >= kBigTiles && g_gemv_ksplit <= 0) {
+        // row-scaled, many tiles, prepped activations: about 10 KiB of weights per wave
+        const int row_bytes = a.nsteps * 4 * Geo<FMT, UD>::SB;
+        ks = (16 * row_bytes + 5120) / 10240;
+        ks = ks < 1 ? 1 : ks;
+    }
     if (ks > maxks) ks = maxks;
     auto scales_fit = [&](int k) { return !GROUPED || ACC || a.G <= kMaxScLoads * 4 * k; };
     auto lds_fit = [&](int k) { return gemv_lds_bytes(GROUPED, a, p.ldl, rt, k) <= gemv_max_lds(); };
@@ -1098,7 +1147,7 @@ int launch_gemv(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
     p.ldl = a.nsteps * Geo<FMT, UD>::SC + 16;
     int rt = 1;
     if constexpr (gemv_tuned<FMT, UD, GROUPED>())
-        rt = g_gemv_rt > 0 ? g_gemv_rt : (rows_pad / 16 >= 768 ? 4 : 1);
+        rt = g_gemv_rt > 0 ? g_gemv_rt : (rows_pad / 16 >= 768 && (GROUPED || p.x || rows_pad / 16 < kBigTiles) ? 4 : 1);
     if (rt > 1) {
         const int rc = launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, rt, st);
         if (rc == EIF_HIP_OK || rc == EIF_HIP_E_DEVICE) return rc;
@@ -1133,13 +1182,11 @@ int dispatch(const eif_hip_qweight *w, const QArgs &a, const PrepArgs &p, int pa
     }
 }
 
-// Fused-prep arguments: x [M, ldx] FP32 with K == cols, K % 32 == 0, 16-byte aligned rows and signs.
-int make_prep(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int block, float norm, int M,
-              PrepArgs *p)
+// Prep arguments: x [M, ldx] FP32 with K columns, K % 32 == 0, 16-byte aligned rows and signs.
+int make_prep_cols(int K, const float *x, int ldx, const float *signs, int block, float norm, PrepArgs *p)
 {
     *p = PrepArgs{};
-    if (!w || !x || M < 1 || M > kGemvMaxM) return M > kGemvMaxM ? EIF_HIP_E_LIMIT : EIF_HIP_E_ARG;
-    const int K = w->cols;
+    if (!x || K < 32) return EIF_HIP_E_ARG;
     if (K % 32 != 0 || ldx < K || ldx % 4 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)signs & 15))
         return EIF_HIP_E_ARG;
     if (block < 0 || block > 1024 || (block > 0 && ((block & (block - 1)) || K % block != 0))) return EIF_HIP_E_ARG;
@@ -1153,11 +1200,18 @@ int make_prep(const eif_hip_qweight *w, const float *x, int ldx, const float *si
     return EIF_HIP_OK;
 }
 
-int make_prep_spec(const eif_hip_qweight *w, const eif_hip_prep_spec *sp, int M, PrepArgs *p)
+// Fused-prep arguments of a linear: K == cols, at most kGemvMaxM token rows.
+int make_prep(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int block, float norm, int M,
+              PrepArgs *p)
 {
-    if (!sp) return EIF_HIP_E_ARG;
-    int rc = make_prep(w, sp->x, sp->ldx, sp->signs, sp->wht_block, sp->wht_norm, M, p);
-    if (rc) return rc;
+    *p = PrepArgs{};
+    if (!w || !x || M < 1 || M > kGemvMaxM) return M > kGemvMaxM ? EIF_HIP_E_LIMIT : EIF_HIP_E_ARG;
+    return make_prep_cols(w->cols, x, ldx, signs, block, norm, p);
+}
+
+// The pre-op fields of a prep spec (p already holds the rotation arguments).
+int apply_pre(const eif_hip_prep_spec *sp, PrepArgs *p)
+{
     if (sp->pre != EIF_HIP_PRE_NONE && sp->pre != EIF_HIP_PRE_RMS && sp->pre != EIF_HIP_PRE_SWIGLU_RMS)
         return EIF_HIP_E_ARG;
     if (sp->pre == EIF_HIP_PRE_SWIGLU_RMS && (!sp->x2 || ((uintptr_t)sp->x2 & 15))) return EIF_HIP_E_ARG;
@@ -1167,6 +1221,50 @@ int make_prep_spec(const eif_hip_qweight *w, const eif_hip_prep_spec *sp, int M,
     p->nw = sp->norm_w;
     p->eps = sp->eps;
     return EIF_HIP_OK;
+}
+
+// The prep kernel on its own, M token rows into xq [M, ldq] (ldq >= K, a multiple of 16) and xs [M]: E columns
+// per thread, the fewest that cover ldq with at most 1024 threads and hold a WHT block within one wave.
+template <int E>
+int launch_prep_spec_e(PrepArgs p, int8_t *xq, float *xs, int M, hipStream_t st)
+{
+    const int threads = eif_ceil_div(eif_ceil_div(p.ldl, E), 64) * 64;
+    if (p.block == 128) prep_spec_kernel<E, 7><<<M, threads, 0, st>>>(p, xq, xs);
+    else if (p.block == 0) prep_spec_kernel<E, 0><<<M, threads, 0, st>>>(p, xq, xs);
+    else prep_spec_kernel<E, -1><<<M, threads, 0, st>>>(p, xq, xs);
+    EIF_HIP_LAUNCHED();
+    return EIF_HIP_OK;
+}
+
+int launch_prep_spec(PrepArgs p, int8_t *xq, int ldq, float *xs, int M, hipStream_t st)
+{
+    if (!xq || !xs || ldq < p.K || ldq % 16 != 0 || ((uintptr_t)xq & 15) || M < 1) return EIF_HIP_E_ARG;
+    p.ldl = ldq;
+    for (int e = 4; e <= 16; e *= 2) {
+        if (64 * e < p.block || eif_ceil_div(ldq, e) > 1024) continue;
+        if (e == 4) return launch_prep_spec_e<4>(p, xq, xs, M, st);
+        if (e == 8) return launch_prep_spec_e<8>(p, xq, xs, M, st);
+        return launch_prep_spec_e<16>(p, xq, xs, M, st);
+    }
+    return EIF_HIP_E_LIMIT;
+}
+
+int make_prep_spec(const eif_hip_qweight *w, const eif_hip_prep_spec *sp, int M, PrepArgs *p)
+{
+    if (!sp) return EIF_HIP_E_ARG;
+    int rc = make_prep(w, sp->x, sp->ldx, sp->signs, sp->wht_block, sp->wht_norm, M, p);
+    if (rc) return rc;
+    return apply_pre(sp, p);
+}
+
+// A row-scaled GEMV launch only (no GEMM fallback): 1 when the shape does not fit the GEMV.
+int gemv_rowscaled(const eif_hip_qweight *w, const QArgs &a, hipStream_t st)
+{
+    const PrepArgs p{};
+    if (w->fmt == kI8) return launch_gemv<kI8, 0, false, false>(a, p, w->rows_pad, st);
+    if (w->fmt == kI4) return launch_gemv<kI4, 0, false, false>(a, p, w->rows_pad, st);
+    if (w->group == 0) return launch_gemv<kTern, 4, false, false>(a, p, w->rows_pad, st);
+    return EIF_HIP_E_ARG;
 }
 
 int check_linear_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
@@ -1200,6 +1298,26 @@ QArgs make_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
 }  // namespace
 
 namespace eif {
+
+int qweight_row_tiles(const eif_hip_qweight *w) { return w ? w->rows_pad / 16 : 0; }
+
+// Row-scaled GEMV of one prepped token row with, per 16-row tile, the largest output and its row (first of
+// equal maxima) in amax_v / amax_i [qweight_row_tiles(w)]: the greedy argmax's first stage.
+int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y, float *amax_v,
+                   int *amax_i, hipStream_t st)
+{
+    int rc = check_linear_args(w, xq, ldq, 1);
+    if (rc) return rc;
+    if (!xs || !y || !amax_v || !amax_i || (w->fmt == kTern && w->group > 0)) return EIF_HIP_E_ARG;
+    QArgs a = make_args(w, xq, ldq, 1);
+    a.xs = xs;
+    a.y = y;
+    a.ldy = w->rows;
+    a.amax_v = amax_v;
+    a.amax_i = amax_i;
+    rc = gemv_rowscaled(w, a, st);
+    return rc == 1 ? EIF_HIP_E_LIMIT : rc;
+}
 
 // The linear with an explicit scale array (the host drop-in passes per-call row scales for resident codes).
 int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *xq, int ldq, const float *xs,
@@ -1243,11 +1361,36 @@ extern "C" int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep
     int rc = make_prep_spec(w, spec, M, &p);
     if (rc) return rc;
     if (!y || ldy < w->rows) return EIF_HIP_E_ARG;
+    const hipStream_t st = (hipStream_t)stream;
     QArgs a = make_args(w, nullptr, 0, M);
     a.bias = bias;
     a.y = y;
     a.ldy = ldy;
-    return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
+    if (M == 1 && w->rows_pad / 16 >= kBigTiles && !(w->fmt == kTern && w->group > 0)) {
+        // a vocabulary-sized row-scaled matrix: one prep, then the GEMV of the prepped row (the same codes
+        // and scale as the fused prep, so the same output bits)
+        int8_t *xq = reinterpret_cast<int8_t *>(split_ws(st, (size_t)w->kpad + 16, 1));
+        if (xq) {
+            float *xs = reinterpret_cast<float *>(xq + w->kpad);
+            if ((rc = launch_prep_spec(p, xq, w->kpad, xs, 1, st))) return rc;
+            a.xq = xq, a.ldq = w->kpad, a.xs = xs;
+            rc = gemv_rowscaled(w, a, st);
+            if (rc != 1) return rc;
+        }
+    }
+    return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, st);
+}
+
+extern "C" int eif_hip_prep_spec_rows(const eif_hip_prep_spec *spec, int K, int8_t *xq, int ldq, float *xs, int M,
+                                      void *stream)
+{
+    if (!spec || M < 0) return EIF_HIP_E_ARG;
+    PrepArgs p;
+    int rc = make_prep_cols(K, spec->x, spec->ldx, spec->signs, spec->wht_block, spec->wht_norm, &p);
+    if (rc) return rc;
+    if ((rc = apply_pre(spec, &p))) return rc;
+    if (M == 0) return EIF_HIP_OK;
+    return launch_prep_spec(p, xq, ldq, xs, M, (hipStream_t)stream);
 }
 
 extern "C" int eif_hip_qlinear_prep_acc(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, int32_t *acc, int M,

@@ -124,10 +124,18 @@ typedef struct eif_hip_prep_spec {
     float wht_norm;       /* the WHT scale, e.g. eif_hip_wht_norm(wht_block) */
 } eif_hip_prep_spec;
 
-/* eif_hip_qlinear_f32 with a pre-op: y = linear(prep(pre(x))) (+ bias) for M <= 8 rows, one launch. The
- * bias may be the residual stream itself (y == bias: each output reads its own bias element first).     */
+/* eif_hip_qlinear_f32 with a pre-op: y = linear(prep(pre(x))) (+ bias) for M <= 8 rows, one launch (a
+ * row-scaled matrix of 65536 rows or more at M = 1, e.g. a vocabulary head: a prep launch, then the GEMV of
+ * the prepped row, with the same output bits). The bias may be the residual stream itself (y == bias: each
+ * output reads its own bias element first).                                                            */
 int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias, float *y,
                          int ldy, int M, void *stream);
+
+/* The prep of a spec on its own, for any M (e.g. a prompt batch before the MFMA GEMM of eif_hip_qlinear):
+ * M rows of K columns (K % 32 == 0) -> xq [M, ldq] int8 (ldq >= K, a multiple of 16, zeros past K) and
+ * xs [M]. The codes and scales equal those the fused prep of eif_hip_qlinear_prep stages.              */
+int eif_hip_prep_spec_rows(const eif_hip_prep_spec *spec, int K, int8_t *xq, int ldq, float *xs, int M,
+                           void *stream);
 int eif_hip_qlinear_prep_acc(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, int32_t *acc, int M,
                              void *stream);
 

@@ -3,12 +3,12 @@
  *
  * Replaces the token loop of the reference's tinyllm engine for the BitNet path: tinyllm_forward /
  * tinyllm_forward_embedding_ex (src/eif_tinyllm.c:371-857, :1502-1506) and its greedy sampler
- * tinyllm_sample_greedy (src/eif_tinyllm.c:1519-1530). One token step is 5 launches per layer plus 4:
- *   embedding row (INT8 table x per-token scale)
+ * tinyllm_sample_greedy (src/eif_tinyllm.c:1519-1530). One token step is 5 launches per layer plus 3:
  *   per layer: [RMSNorm + WHT + INT8] QKV GEMV | RoPE + fp16 KV append + attention |
  *              [sub-RMSNorm + WHT + INT8] O GEMV + residual | [RMSNorm + WHT + INT8] gate/up GEMV |
  *              [SiLU(gate) * up + sub-RMSNorm + WHT + INT8] down GEMV + residual
- *   [RMSNorm + INT8] INT8 head GEMV | argmax (greedy) or the next prompt token, position + 1
+ *   RMSNorm + INT8 prep | INT8 head GEMV with per-tile maxima | argmax (greedy) or the next prompt token,
+ *   position + 1, the next token's embedding row (INT8 table x per-token scale)
  * The position and the current token live in device memory, so the step is captured once as a HIP graph and
  * replayed per token with no host work in between.
  *
@@ -61,7 +61,8 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
 int eif_hip_bitnet_set_layer(eif_hip_bitnet *m, int layer, const eif_hip_bitnet_layer *w);
 int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *g);
 
-/* Starts a sequence: clears the KV cache, uploads the prompt (n_prompt >= 1 ids), position 0.             */
+/* Starts a sequence: clears the KV cache, uploads the prompt (n_prompt >= 1 ids), position 0. The globals
+ * must be set.                                                                                          */
 int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, void *stream);
 
 /* Runs n token steps from the current position. The step at position p consumes the current token and
