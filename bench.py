@@ -354,9 +354,10 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
 
 def decode_workload(args, torch, bh, synth, np):
     """Greedy decode on the 30-layer BitNet-b1.58-2B-shaped model (random init): a random-id prompt of
-    --decode-prompt tokens (fed one step per token, not timed), then --decode-tokens greedy tokens timed as HIP
-    graph replays of the token step. Bytes per token = the resident weights the step reads (ternary codes,
-    group scales, norms, INT8 head) + the fp16 KV cache read at that position."""
+    --decode-prompt tokens, all but the last as one prefill batch (timed on its own), the last prompt token's
+    step (the first greedy token; it captures the step graph), then --decode-tokens greedy token steps timed as
+    HIP graph replays of the token step. Bytes per token = the resident weights the step reads (ternary codes, group scales, norms, INT8 head)
+    + the fp16 KV cache read at that position."""
     c = dict(synth.BITNET_2B_DECODE)
     cfg = synth.bitnet_config(c.pop("dim"), c.pop("hidden"), c.pop("n_layers"), c.pop("n_heads"), c.pop("n_kv_heads"),
                               c.pop("head_dim"), c.pop("vocab"), c.pop("seq_len"), c.pop("group_in"),
@@ -367,27 +368,37 @@ def decode_workload(args, torch, bh, synth, np):
     m = bh.BitnetModel(cfg, w)
     npr, ntok = args.decode_prompt, args.decode_tokens
     prompt = synth.rng(301).integers(0, cfg["vocab"], npr).astype(np.int32)
-    m.reset(prompt)
-    m.steps(npr - 1, graph=True)   # the prompt, teacher-forced
-    torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    m.reset(prompt)
+    m.prefill(npr - 1)             # allocates the batch buffers
+    m.reset(prompt)
+    torch.cuda.synchronize()
+    a.record(s)
+    m.prefill(npr - 1)             # the prompt but its last token, one batch
+    b.record(s)
+    b.synchronize()
+    pre_sec = a.elapsed_time(b) * 1e-3
+    m.steps(1, graph=True)         # the last prompt token (captures the step graph), not timed
+    torch.cuda.synchronize()
     a.record(s)
     m.steps(ntok, graph=True)
     b.record(s)
     b.synchronize()
     sec = a.elapsed_time(b) * 1e-3
-    toks = m.tokens(npr + ntok)
+    toks = m.tokens(npr + ntok + 1)
     assert list(toks[:npr]) == list(prompt)
     wb = m.weight_bytes()
-    kv = float(np.mean([m.kv_bytes(p) for p in range(npr - 1, npr - 1 + ntok)]))
+    kv = float(np.mean([m.kv_bytes(p) for p in range(npr, npr + ntok)]))
     per_tok = wb + kv
     res = {"model": "bitnet-b1.58-2B-shaped, 30 layers, dim 2560, ffn 6912, 20/5 heads x 128, vocab 128256 (INT8 head)",
            "prompt": npr, "tokens": ntok, "context": cfg["seq_len"], "kv": "fp16",
            "ms_per_token": round(sec / ntok * 1e3, 4), "tok_per_s": round(ntok / sec, 1),
            "bytes_per_token": int(per_tok), "weight_bytes": int(wb), "GBps": round(per_tok * ntok / sec / 1e9, 1),
            "frac_hbm": round(per_tok * ntok / sec / 1e9 / HBM_PEAK_GBS, 4),
-           "launches_per_token": 5 * cfg["n_layers"] + 3, "timing": "HIP graph of one token step, replayed; HIP events",
+           "launches_per_token": 6 * cfg["n_layers"] + 3, "timing": "HIP graph of one token step, replayed; HIP events",
+           "prefill": {"tokens": npr - 1, "ms": round(pre_sec * 1e3, 3), "tok_per_s": round((npr - 1) / pre_sec, 1),
+                       "path": "prep + int8-MFMA GEMM per linear over the batch, causal attention per (head, token)"},
            "weights_generated_s": round(gen_s, 1), "greedy_tail": [int(t) for t in toks[-8:]]}
     m.close()
     if not args.no_cpu:

@@ -53,6 +53,7 @@ _SIGS = {
     "eif_hip_bitnet_set_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
     "eif_hip_bitnet_reset": (_i, [_vp, _vp, _i, _vp]),
     "eif_hip_bitnet_steps": (_i, [_vp, _i, _i, _vp]),
+    "eif_hip_bitnet_prefill": (_i, [_vp, _i, _vp]),
     "eif_hip_bitnet_tokens": (_i, [_vp, _vp, _i, _vp]),
     "eif_hip_bitnet_logits": (_i, [_vp, _vp, _vp]),
     "eif_hip_bitnet_position": (_i, [_vp, _vp]),
@@ -262,6 +263,9 @@ class BitnetModel:
 
     def steps(self, n, graph=False, stream=None):
         check(load().eif_hip_bitnet_steps(self.h, n, 1 if graph else 0, stream_ptr(stream)), "eif_hip_bitnet_steps")
+
+    def prefill(self, n, stream=None):
+        check(load().eif_hip_bitnet_prefill(self.h, n, stream_ptr(stream)), "eif_hip_bitnet_prefill")
 
     def tokens(self, n, stream=None):
         import numpy as np

@@ -4,8 +4,10 @@
 // the fused prep + int8-MFMA GEMV of qlinear.hip (eif_hip_qlinear_prep: RMSNorm / SiLU-gate + RMSNorm, WHT,
 // absmax INT8, group-scaled ternary GEMV, residual as the epilogue bias), the INT8 head as a prep launch plus
 // the GEMV with per-tile maxima (the argmax's first stage), and kernels of its own:
-//   attn_decode_kernel  RoPE of q and k (:396-405, :476-507), fp16 KV append, softmax attention (:555-650);
-//                       one workgroup per query head, one pass over the cache
+//   attn_split_kernel   RoPE of q and k (:396-405, :476-507; angles from a table made once), fp16 KV append,
+//                       softmax attention (:555-650) of each query head over one chunk of the positions per
+//                       workgroup, one pass over the chunk
+//   attn_combine_kernel the chunks' shares of each head combined
 //   sample_kernel       greedy argmax over the head's tile maxima (first maximum, src/eif_tinyllm.c:1519-1530)
 //                       or the next prompt token, stored in the sequence; position + 1; x = the next token's
 //                       INT8 embedding row * its scale (src/eif_tinyllm.c:902-916)
@@ -13,6 +15,7 @@
 // Device state (position, current token, prompt, sequence) lets one captured HIP graph serve every step.
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
 #include <new>
 #include <vector>
 
@@ -22,7 +25,6 @@
 namespace {
 
 constexpr int kMaxSeq = 4096;
-constexpr int kAttnThreads = 1024;
 
 // state[0] = position of the step about to run, state[1] = its token, state[2] = prompt length
 __global__ __launch_bounds__(256) void embed_kernel(const int8_t *emb, const float *emb_scale, const int *state,
@@ -46,60 +48,49 @@ EIF_DEV void half8_to_float(const uint4 &raw, float (&f)[8])
     }
 }
 
-// One workgroup per query head h (kv head g = h / kv_mul), kAttnThreads threads, one pass over the cache.
-// A thread holds 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG row groups;
-// row group r takes positions r, r + RG, r + 2 RG, ... in batches of UNR rows whose keys and values are loaded
-// together, and keeps a running softmax over them (max m, sum l, the weighted value sums o of its 8 dims).
-//   1. RoPE of q_h and of k_g at position pos (the rotated k and v rounded to fp16, as the cache stores them);
-//      the first query head of each kv head appends them to the cache
-//   2. per row group, per batch: s_t = (q . k_t) / sqrt(HD), m' = max(m, s_t), l = l e^(m - m') +
-//      sum e^(s_t - m'), o = o e^(m - m') + sum e^(s_t - m') v_t; position pos (row group 0) from the
-//      workgroup's own copy of k and v
-//   3. the row groups combined: M = max_r m_r, out = sum_r e^(m_r - M) o_r / sum_r e^(m_r - M) l_r
-// This is the softmax of the scores over positions 0 .. pos followed by the weighted sum of the values, with
-// the sums taken in another order. Cache layout: [kv_head][seq_len][HD] fp16 per layer.
-template <int HD>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *qkv, __half *kc, __half *vc,
-                                                                   const int *state, float *out, int n_heads,
-                                                                   int n_kv, int seq_len, float theta,
-                                                                   float inv_sqrt_hd)
+// RoPE angle of pair j (dims j, j + HD/2) at position pos: freq = 1 / powf(theta, 2j / HD), val = pos * freq;
+// rope_table_kernel stores (cos, sin) of every (pos, j) once per model.
+EIF_DEV void rope_cs(int pos, int j, int hd, float theta, float &c, float &sn)
 {
-    constexpr int DPR = HD / 8, RG = kAttnThreads / DPR, HALF = HD / 2, UNR = 8;
-    constexpr int PARTS = kAttnThreads / HD;   // threads per output dimension in the combine
-    __shared__ float q_l[HD], k_l[HD], v_l[HD];
+    const float freq = 1.0f / powf(theta, (float)(2 * j) / (float)hd);
+    const float val = (float)pos * freq;
+    c = cosf(val), sn = sinf(val);
+}
+
+__global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
+{
+    const int half = hd / 2;
+    const size_t n = (size_t)seq_len * half;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float c, sn;
+        rope_cs((int)(i / half), (int)(i % half), hd, theta, c, sn);
+        tab[i] = make_float2(c, sn);
+    }
+}
+
+// Softmax attention of one query (q_l, HD floats in LDS) over cache rows 0 .. n_cache - 1 (fp16 [HD] rows at
+// kcg / vcg) and, when k_x is not NULL, one more row (k_x, v_x in LDS) after them; out[0 .. HD) = the result.
+// NT threads. A thread holds 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG
+// row groups; row group r takes rows r, r + RG, r + 2 RG, ... in batches of UNR rows whose keys and values are
+// loaded together, and keeps a running softmax over them (max m, sum l, the weighted value sums o of its dims):
+//   s_t = (q . k_t) / sqrt(HD), m' = max(m, s_t), l = l e^(m - m') + sum e^(s_t - m'),
+//   o = o e^(m - m') + sum e^(s_t - m') v_t;
+// the row groups are then combined: M = max_r m_r, out = sum_r e^(m_r - M) o_r / sum_r e^(m_r - M) l_r.
+// This is the softmax of the scores followed by the weighted sum of the values, with the sums taken in another
+// order.
+// PARTIAL: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized, out[HD] = M, out[HD + 1] = sum_r e^(m_r - M) l_r
+// (a chunk's share, combined with the others by attn_combine_kernel).
+template <int HD, int NT, bool PARTIAL = false>
+EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int n_cache, const float *k_x,
+                    const float *v_x, float inv_sqrt_hd, float *out)
+{
+    constexpr int DPR = HD / 8, RG = NT / DPR, UNR = 8;
+    constexpr int PARTS = NT / HD;   // threads per output dimension in the combine
     __shared__ __align__(16) float m_l[RG];
     __shared__ float l_l[RG];
     __shared__ float o_l[RG][HD + 4];
     __shared__ float po_l[PARTS][HD], pl_l[PARTS];
-    const int h = blockIdx.x, kv_mul = n_heads / n_kv, g = h / kv_mul;
-    const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
-    const int pos = state[0];
     const int t = threadIdx.x;
-    const __half *kcg = kc + (size_t)g * seq_len * HD, *vcg = vc + (size_t)g * seq_len * HD;
-
-    // 1. RoPE (half-split pairs j, j + HD/2) and the current k, v
-    if (t < HALF) {
-        const float freq = 1.0f / powf(theta, (float)(2 * t) / (float)HD);
-        const float val = (float)pos * freq;
-        const float c = cosf(val), sn = sinf(val);
-        const float *qh = qkv + h * HD, *kh = qkv + q_dim + g * HD, *vh = qkv + q_dim + kv_dim + g * HD;
-        float a = qh[t], b = qh[t + HALF];
-        q_l[t] = a * c - b * sn;
-        q_l[t + HALF] = b * c + a * sn;
-        a = kh[t], b = kh[t + HALF];
-        const __half k0 = __float2half(a * c - b * sn), k1 = __float2half(b * c + a * sn);
-        const __half v0 = __float2half(vh[t]), v1 = __float2half(vh[t + HALF]);
-        k_l[t] = __half2float(k0), k_l[t + HALF] = __half2float(k1);
-        v_l[t] = __half2float(v0), v_l[t + HALF] = __half2float(v1);
-        if (h % kv_mul == 0) {
-            __half *kw = kc + ((size_t)g * seq_len + pos) * HD, *vw = vc + ((size_t)g * seq_len + pos) * HD;
-            kw[t] = k0, kw[t + HALF] = k1;
-            vw[t] = v0, vw[t + HALF] = v1;
-        }
-    }
-    __syncthreads();
-
-    // 2. one pass over positions 0 .. pos - 1 of the cache, then position pos
     const int sub = t % DPR, r0 = t / DPR;
     float qv[8], o[8];
 #pragma unroll
@@ -113,12 +104,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *
         for (int off = 1; off < DPR; off <<= 1) d += __shfl_xor(d, off, 64);
         return d * inv_sqrt_hd;
     };
-    for (int base = 0; base < pos; base += RG * UNR) {
+    for (int base = 0; base < n_cache; base += RG * UNR) {
         uint4 kr[UNR], vr[UNR];
 #pragma unroll
         for (int u = 0; u < UNR; ++u) {
             const int tt = base + u * RG + r0;
-            const size_t off = (size_t)(tt < pos ? tt : 0) * HD + 8 * sub;
+            const size_t off = (size_t)(tt < n_cache ? tt : 0) * HD + 8 * sub;
             kr[u] = *reinterpret_cast<const uint4 *>(kcg + off);
             vr[u] = *reinterpret_cast<const uint4 *>(vcg + off);
         }
@@ -129,7 +120,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *
             float k8[8];
             half8_to_float(kr[u], k8);
             const float d = score(k8);
-            sv[u] = base + u * RG + r0 < pos ? d : -INFINITY;
+            sv[u] = base + u * RG + r0 < n_cache ? d : -INFINITY;
             bm = fmaxf(bm, sv[u]);
         }
         const float mn = fmaxf(m, bm);
@@ -141,31 +132,32 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *
 #pragma unroll
             for (int u = 0; u < UNR; ++u) {
                 const float pw = expf(sv[u] - mn);
+                const bool ok = base + u * RG + r0 < n_cache;   // a row past the end holds a stand-in row
                 float v8[8];
                 half8_to_float(vr[u], v8);
                 l = l + pw;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, v8[i], o[i]);
+                for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, ok ? v8[i] : 0.0f, o[i]);
             }
             m = mn;
         }
     }
-    {
+    if (k_x) {   // uniform
         float k8[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) k8[i] = k_l[8 * sub + i];
+        for (int i = 0; i < 8; ++i) k8[i] = k_x[8 * sub + i];
         const float d = score(k8);   // every row group computes it (uniform shuffles); row group 0 keeps it
         if (r0 == 0) {
             const float mn = fmaxf(m, d);
             const float sc = expf(m - mn), pw = expf(d - mn);
             l = l * sc + pw;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, v_l[8 * sub + i], o[i] * sc);
+            for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, v_x[8 * sub + i], o[i] * sc);
             m = mn;
         }
     }
 
-    // 3. combine the row groups
+    // combine the row groups
     if (sub == 0) m_l[r0] = m, l_l[r0] = l;
 #pragma unroll
     for (int i = 0; i < 8; ++i) o_l[r0][8 * sub + i] = o[i];
@@ -192,8 +184,159 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(const float *
         float os = po_l[0][t], ls = pl_l[0];
 #pragma unroll
         for (int q = 1; q < PARTS; ++q) os += po_l[q][t], ls += pl_l[q];
-        out[h * HD + t] = os / ls;
+        if constexpr (PARTIAL) {
+            out[t] = os;
+            if (t == 0) out[HD] = mx, out[HD + 1] = ls;
+        } else {
+            out[t] = os / ls;
+        }
     }
+}
+
+// Decode, split over the positions: workgroup (h, s) takes query head h (kv head g = h / kv_mul) over the cache
+// rows of chunk s, [s CH, min((s + 1) CH, pos)), CH = the rows one batch of attend<HD, 256> covers; chunk
+// pos / CH also takes row pos itself. Chunks past pos write an empty share (max -inf, sum 0) and exit. Every workgroup rotates q_h (RoPE from the table);
+// the workgroup of the last chunk also rotates k_g, rounds k and v to fp16 and, for the first query head of
+// the kv head, appends them to the cache. Each writes its share (attend's partial form) to
+// part[(h * n_chunks + s) * (HD + 2)].
+// Cache layout: [kv_head][seq_len][HD] fp16 per layer.
+template <int HD>
+constexpr int attn_chunk() { return (256 / (HD / 8)) * 8; }
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __half *kc, __half *vc, const int *state,
+                                                         const float2 *rope, float *part, int n_chunks, int n_heads,
+                                                         int n_kv, int seq_len, float inv_sqrt_hd)
+{
+    constexpr int HALF = HD / 2, CH = attn_chunk<HD>();
+    __shared__ float q_l[HD], k_l[HD], v_l[HD];
+    const int h = blockIdx.x, sc = blockIdx.y, kv_mul = n_heads / n_kv, g = h / kv_mul;
+    const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
+    const int pos = state[0];
+    const int c0 = sc * CH;
+    if (c0 > pos) {   // uniform over the workgroup: an empty share
+        float *pe = part + ((size_t)h * n_chunks + sc) * (HD + 2);
+        if (threadIdx.x == 0) pe[HD] = -INFINITY, pe[HD + 1] = 0.0f;
+        return;
+    }
+    const bool last = pos < c0 + CH;
+    const int t = threadIdx.x;
+    if (t < HALF) {
+        const float2 cs = rope[(size_t)pos * HALF + t];
+        const float c = cs.x, sn = cs.y;
+        const float *qh = qkv + h * HD;
+        const float a = qh[t], b = qh[t + HALF];
+        q_l[t] = a * c - b * sn;
+        q_l[t + HALF] = b * c + a * sn;
+        if (last) {
+            const float *kh = qkv + q_dim + g * HD, *vh = qkv + q_dim + kv_dim + g * HD;
+            const float ka = kh[t], kb = kh[t + HALF];
+            const __half k0 = __float2half(ka * c - kb * sn), k1 = __float2half(kb * c + ka * sn);
+            const __half v0 = __float2half(vh[t]), v1 = __float2half(vh[t + HALF]);
+            k_l[t] = __half2float(k0), k_l[t + HALF] = __half2float(k1);
+            v_l[t] = __half2float(v0), v_l[t + HALF] = __half2float(v1);
+            if (h % kv_mul == 0) {
+                __half *kw = kc + ((size_t)g * seq_len + pos) * HD, *vw = vc + ((size_t)g * seq_len + pos) * HD;
+                kw[t] = k0, kw[t + HALF] = k1;
+                vw[t] = v0, vw[t + HALF] = v1;
+            }
+        }
+    }
+    __syncthreads();
+    const size_t base = ((size_t)g * seq_len + c0) * HD;
+    const int rows = (last ? pos : c0 + CH) - c0;
+    attend<HD, 256, true>(q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr, inv_sqrt_hd,
+                          part + ((size_t)h * n_chunks + sc) * (HD + 2));
+}
+
+// The chunks' shares of query head h combined: M = max_s M_s, out = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s
+// over all chunks (an empty share weighs 0, its stale O is not read into the sum).
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float *part, float *out, int n_chunks)
+{
+    const int h = blockIdx.x, t = threadIdx.x;
+    const float *ph = part + (size_t)h * n_chunks * (HD + 2);
+    float mx = -INFINITY;
+    for (int sc = 0; sc < n_chunks; ++sc) mx = fmaxf(mx, ph[(size_t)sc * (HD + 2) + HD]);
+    float os = 0.0f, ls = 0.0f;
+    for (int sc = 0; sc < n_chunks; ++sc) {
+        const float *p = ph + (size_t)sc * (HD + 2);
+        const float ms = p[HD], o = p[t], l = p[HD + 1];
+        const bool live = ms != -INFINITY;
+        const float w = live ? expf(ms - mx) : 0.0f;
+        os = fmaf(w, live ? o : 0.0f, os);
+        ls = fmaf(w, l, ls);
+    }
+    out[h * HD + t] = os / ls;
+}
+
+// Prefill, step 1: token i of a batch at position pos0 + i (one workgroup per token). RoPE of every query head
+// in place in its qkv row, RoPE of every key head, the keys and values rounded to fp16 into the cache.
+template <int HD>
+__global__ __launch_bounds__(256) void rope_append_kernel(float *qkv, int ldqkv, __half *kc, __half *vc, int pos0,
+                                                          int n_heads, int n_kv, int seq_len, const float2 *rope)
+{
+    constexpr int HALF = HD / 2;
+    const int i = blockIdx.x, pos = pos0 + i;
+    const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
+    float *row = qkv + (size_t)i * ldqkv;
+    for (int idx = threadIdx.x; idx < (n_heads + n_kv) * HALF; idx += blockDim.x) {
+        const int hh = idx / HALF, j = idx % HALF;
+        const float2 cs = rope[(size_t)pos * HALF + j];
+        const float c = cs.x, sn = cs.y;
+        if (hh < n_heads) {
+            float *qh = row + hh * HD;
+            const float a = qh[j], b = qh[j + HALF];
+            qh[j] = a * c - b * sn;
+            qh[j + HALF] = b * c + a * sn;
+        } else {
+            const int g = hh - n_heads;
+            const float *kh = row + q_dim + g * HD, *vh = row + q_dim + kv_dim + g * HD;
+            const float a = kh[j], b = kh[j + HALF];
+            __half *kw = kc + ((size_t)g * seq_len + pos) * HD, *vw = vc + ((size_t)g * seq_len + pos) * HD;
+            kw[j] = __float2half(a * c - b * sn), kw[j + HALF] = __float2half(b * c + a * sn);
+            vw[j] = __float2half(vh[j]), vw[j + HALF] = __float2half(vh[j + HALF]);
+        }
+    }
+}
+
+// Prefill, step 2: query head h of token i (workgroup (h, i)) over cache rows 0 .. pos0 + i (causal).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int ldqkv, const __half *kc,
+                                                           const __half *vc, float *out, int ldo, int pos0,
+                                                           int n_heads, int n_kv, int seq_len, float inv_sqrt_hd)
+{
+    __shared__ float q_l[HD];
+    const int h = blockIdx.x, i = blockIdx.y, g = h / (n_heads / n_kv);
+    if ((int)threadIdx.x < HD) q_l[threadIdx.x] = qkv[(size_t)i * ldqkv + h * HD + threadIdx.x];
+    __syncthreads();
+    attend<HD, 256>(q_l, kc + (size_t)g * seq_len * HD, vc + (size_t)g * seq_len * HD, pos0 + i + 1, nullptr,
+                    nullptr, inv_sqrt_hd, out + (size_t)i * ldo + h * HD);
+}
+
+// Prefill: the embedding rows of prompt tokens pos0 .. pos0 + n - 1 (one workgroup per token).
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int8_t *emb, const float *emb_scale, const int *prompt,
+                                                         int pos0, float *x, int dim)
+{
+    const int i = blockIdx.x, tok = prompt[pos0 + i];
+    const float sc = emb_scale ? emb_scale[tok] : 1.0f;
+    const int8_t *row = emb + (size_t)tok * dim;
+    for (int c = threadIdx.x; c < dim; c += blockDim.x) x[(size_t)i * dim + c] = (float)row[c] * sc;
+}
+
+// Prefill: the residual stream x += y over n floats.
+__global__ void add_rows_kernel(float *x, const float *y, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        x[i] = y[i] + x[i];
+}
+
+// Prefill: the sequence entries of a batch's prompt tokens and the position of its last token (the sampler then
+// makes the step of that token as a decode step would).
+__global__ void prefill_state_kernel(int *state, int *seq, const int *prompt, int pos0, int n)
+{
+    for (int i = threadIdx.x; i + 1 < n; i += blockDim.x) seq[pos0 + 1 + i] = prompt[pos0 + 1 + i];
+    if (threadIdx.x == 0) state[0] = pos0 + n - 1;
 }
 
 // Greedy token: first index of the largest logit (NaN never wins), from the head GEMV's per-tile maxima (value,
@@ -278,12 +421,21 @@ struct eif_hip_bitnet {
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *hb = nullptr, *logits = nullptr;
     __half *kc = nullptr, *vc = nullptr;
     int *state = nullptr, *prompt = nullptr, *seq = nullptr;
+    float2 *rope = nullptr;          // RoPE (cos, sin) [seq_len][head_dim / 2]
+    float *apart = nullptr;          // attention chunk shares [n_heads][n_chunks][head_dim + 2]
+    int n_chunks = 0;
     int8_t *hq = nullptr;            // the head's prepped input row [head_kpad] and its scale
     float *hs = nullptr;
     float *amax_v = nullptr;         // the head's per-tile maxima [head_tiles]
     int *amax_i = nullptr;
     int head_kpad = 0, head_tiles = 0;
     int hpos = 0;                    // host copy of the position (steps are deterministic)
+    int n_prompt = 0;                // host copy of the prompt length
+    // prefill batch buffers for up to pf_cap tokens (allocated by the first eif_hip_bitnet_prefill):
+    // residual x, attention output, qkv, gate|up, a linear's output, int8 rows and their scales
+    int pf_cap = 0;
+    float *p_x = nullptr, *p_xb = nullptr, *p_qkv = nullptr, *p_h = nullptr, *p_y = nullptr, *p_xs = nullptr;
+    int8_t *p_xq = nullptr;
     size_t weight_bytes = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -291,6 +443,8 @@ struct eif_hip_bitnet {
 };
 
 namespace {
+
+int enqueue_head(eif_hip_bitnet *m, hipStream_t st);
 
 int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
 {
@@ -303,10 +457,15 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         int rc = eif_hip_qlinear_prep(m->wqkv[l], &sp, nullptr, m->qkv, m->q_dim + 2 * m->kv_dim, 1, st);
         if (rc) return rc;
         const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
-        auto attn = c.head_dim == 128 ? attn_decode_kernel<128>
-                    : (c.head_dim == 64 ? attn_decode_kernel<64> : attn_decode_kernel<32>);
-        attn<<<c.n_heads, kAttnThreads, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state, m->xb,
-                                                 c.n_heads, c.n_kv_heads, c.seq_len, c.rope_theta, inv_sqrt_hd);
+        auto attn = c.head_dim == 128 ? attn_split_kernel<128>
+                    : (c.head_dim == 64 ? attn_split_kernel<64> : attn_split_kernel<32>);
+        attn<<<dim3(c.n_heads, m->n_chunks), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
+                                                           m->rope, m->apart, m->n_chunks, c.n_heads, c.n_kv_heads,
+                                                           c.seq_len, inv_sqrt_hd);
+        EIF_HIP_LAUNCHED();
+        auto comb = c.head_dim == 128 ? attn_combine_kernel<128>
+                    : (c.head_dim == 64 ? attn_combine_kernel<64> : attn_combine_kernel<32>);
+        comb<<<c.n_heads, c.head_dim, 0, st>>>(m->apart, m->xb, m->n_chunks);
         EIF_HIP_LAUNCHED();
         sp = eif_hip_prep_spec{};
         sp.x = m->xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l], sp.eps = c.sub_eps;
@@ -322,7 +481,14 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         sp.signs = m->signs_hidden, sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
         if ((rc = eif_hip_qlinear_prep(m->w2[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += W2 h
     }
-    // head: RMSNorm + INT8 prep once, the INT8 GEMV with per-tile maxima, then the argmax over the tiles
+    return enqueue_head(m, st);
+}
+
+// The head and the sampler on x: RMSNorm + INT8 prep once, the INT8 GEMV with per-tile maxima, then the argmax
+// over the tiles (or the next prompt token), position + 1, x = the next token's embedding row.
+int enqueue_head(eif_hip_bitnet *m, hipStream_t st)
+{
+    const eif_hip_bitnet_config &c = m->c;
     eif_hip_prep_spec sp{};
     sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_final, sp.eps = c.rms_eps;
     int rc = eif_hip_prep_spec_rows(&sp, c.dim, m->hq, m->head_kpad, m->hs, 1, st);
@@ -333,6 +499,104 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
                                       m->emb, m->emb_scale, m->x, c.dim, c.vocab);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
+}
+
+int kpad_of(const eif_hip_qweight *w)
+{
+    int kp = 0;
+    eif_hip_qweight_info(w, nullptr, nullptr, &kp, nullptr, nullptr);
+    return kp;
+}
+
+void free_prefill(eif_hip_bitnet *m)
+{
+    for (void *p : {(void *)m->p_x, (void *)m->p_xb, (void *)m->p_qkv, (void *)m->p_h, (void *)m->p_y,
+                    (void *)m->p_xs, (void *)m->p_xq})
+        if (p) (void)hipFree(p);
+    m->p_x = m->p_xb = m->p_qkv = m->p_h = m->p_y = m->p_xs = nullptr;
+    m->p_xq = nullptr;
+    m->pf_cap = 0;
+}
+
+int ensure_prefill(eif_hip_bitnet *m, int n)
+{
+    if (n <= m->pf_cap) return EIF_HIP_OK;
+    const eif_hip_bitnet_config &c = m->c;
+    int kmax = kpad_of(m->head);
+    for (int l = 0; l < c.n_layers; ++l)
+        for (const eif_hip_qweight *w : {m->wqkv[l], m->wo[l], m->w13[l], m->w2[l]}) kmax = std::max(kmax, kpad_of(w));
+    free_prefill(m);   // synchronizes with work that used the old buffers
+    const size_t N = (size_t)n;
+    if (hipMalloc(&m->p_x, sizeof(float) * N * c.dim) != hipSuccess ||
+        hipMalloc(&m->p_xb, sizeof(float) * N * m->q_dim) != hipSuccess ||
+        hipMalloc(&m->p_qkv, sizeof(float) * N * (m->q_dim + 2 * m->kv_dim)) != hipSuccess ||
+        hipMalloc(&m->p_h, sizeof(float) * N * 2 * c.hidden) != hipSuccess ||
+        hipMalloc(&m->p_y, sizeof(float) * N * std::max(c.dim, m->q_dim)) != hipSuccess ||
+        hipMalloc(&m->p_xs, sizeof(float) * N) != hipSuccess || hipMalloc(&m->p_xq, N * kmax) != hipSuccess) {
+        free_prefill(m);
+        return EIF_HIP_E_NOMEM;
+    }
+    m->pf_cap = n;
+    return EIF_HIP_OK;
+}
+
+// The prompt tokens at positions pos0 .. pos0 + n - 1 as one batch: every linear as prep + MFMA GEMM over the
+// n rows, RoPE + KV append for the batch, causal attention per (head, token), the residual adds; then the head
+// and the sampler for the last token, as its decode step would run them.
+int enqueue_prefill(eif_hip_bitnet *m, int pos0, int n, hipStream_t st)
+{
+    const eif_hip_bitnet_config &c = m->c;
+    const float inv_sqrt_hd = 1.0f / sqrtf((float)c.head_dim);
+    const int ldqkv = m->q_dim + 2 * m->kv_dim;
+    const unsigned add_blocks = (unsigned)std::min<size_t>(1024, ((size_t)n * c.dim + 255) / 256);
+    auto prep_linear = [&](const eif_hip_qweight *w, const eif_hip_prep_spec &sp, int K, float *y, int ldy) {
+        const int kp = kpad_of(w);
+        int rc = eif_hip_prep_spec_rows(&sp, K, m->p_xq, kp, m->p_xs, n, st);
+        if (rc) return rc;
+        return eif_hip_qlinear_ex(w, m->p_xq, kp, m->p_xs, nullptr, y, ldy, n, EIF_HIP_PATH_AUTO, st);
+    };
+    embed_rows_kernel<<<n, 256, 0, st>>>(m->emb, m->emb_scale, m->prompt, pos0, m->p_x, c.dim);
+    EIF_HIP_LAUNCHED();
+    for (int l = 0; l < c.n_layers; ++l) {
+        eif_hip_prep_spec sp{};
+        sp.x = m->p_x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_att[l], sp.eps = c.rms_eps;
+        sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
+        int rc = prep_linear(m->wqkv[l], sp, c.dim, m->p_qkv, ldqkv);
+        if (rc) return rc;
+        const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
+        auto rope = c.head_dim == 128 ? rope_append_kernel<128>
+                    : (c.head_dim == 64 ? rope_append_kernel<64> : rope_append_kernel<32>);
+        rope<<<n, 256, 0, st>>>(m->p_qkv, ldqkv, m->kc + cache_l, m->vc + cache_l, pos0, c.n_heads, c.n_kv_heads,
+                                c.seq_len, m->rope);
+        EIF_HIP_LAUNCHED();
+        auto attn = c.head_dim == 128 ? attn_prefill_kernel<128>
+                    : (c.head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<32>);
+        attn<<<dim3(c.n_heads, n), 256, 0, st>>>(m->p_qkv, ldqkv, m->kc + cache_l, m->vc + cache_l, m->p_xb,
+                                                 m->q_dim, pos0, c.n_heads, c.n_kv_heads, c.seq_len, inv_sqrt_hd);
+        EIF_HIP_LAUNCHED();
+        sp = eif_hip_prep_spec{};
+        sp.x = m->p_xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l];
+        sp.eps = c.sub_eps, sp.signs = m->signs_q, sp.wht_block = c.wht_q, sp.wht_norm = c.wht_norm_q;
+        if ((rc = prep_linear(m->wo[l], sp, m->q_dim, m->p_y, c.dim))) return rc;
+        add_rows_kernel<<<add_blocks, 256, 0, st>>>(m->p_x, m->p_y, (size_t)n * c.dim);   // x += O xb
+        EIF_HIP_LAUNCHED();
+        sp = eif_hip_prep_spec{};
+        sp.x = m->p_x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_ffn[l], sp.eps = c.rms_eps;
+        sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
+        if ((rc = prep_linear(m->w13[l], sp, c.dim, m->p_h, 2 * c.hidden))) return rc;
+        sp = eif_hip_prep_spec{};
+        sp.x = m->p_h, sp.x2 = m->p_h + c.hidden, sp.ldx = 2 * c.hidden, sp.pre = EIF_HIP_PRE_SWIGLU_RMS;
+        sp.norm_w = m->rms_sub_ffn[l], sp.eps = c.sub_eps;
+        sp.signs = m->signs_hidden, sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
+        if ((rc = prep_linear(m->w2[l], sp, c.hidden, m->p_y, c.dim))) return rc;
+        add_rows_kernel<<<add_blocks, 256, 0, st>>>(m->p_x, m->p_y, (size_t)n * c.dim);   // x += W2 h
+        EIF_HIP_LAUNCHED();
+    }
+    EIF_HIP_TRY(hipMemcpyAsync(m->x, m->p_x + (size_t)(n - 1) * c.dim, sizeof(float) * c.dim,
+                               hipMemcpyDeviceToDevice, st));
+    prefill_state_kernel<<<1, 256, 0, st>>>(m->state, m->seq, m->prompt, pos0, n);
+    EIF_HIP_LAUNCHED();
+    return enqueue_head(m, st);
 }
 
 // Rows of two reference-format ternary matrices stacked (same columns): codes and grouped scales.
@@ -396,6 +660,18 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
         hipMalloc(&m->seq, sizeof(int) * c.seq_len) != hipSuccess) {
         eif_hip_bitnet_destroy(m);
         return EIF_HIP_E_NOMEM;
+    }
+    const int ch = c.head_dim == 128 ? attn_chunk<128>() : (c.head_dim == 64 ? attn_chunk<64>() : attn_chunk<32>());
+    m->n_chunks = (c.seq_len + ch - 1) / ch;
+    if (hipMalloc(&m->rope, sizeof(float2) * c.seq_len * (c.head_dim / 2)) != hipSuccess ||
+        hipMalloc(&m->apart, sizeof(float) * c.n_heads * m->n_chunks * (c.head_dim + 2)) != hipSuccess) {
+        eif_hip_bitnet_destroy(m);
+        return EIF_HIP_E_NOMEM;
+    }
+    rope_table_kernel<<<256, 256, 0, nullptr>>>(m->rope, c.seq_len, c.head_dim, c.rope_theta);
+    if (hipGetLastError() != hipSuccess || hipStreamSynchronize(nullptr) != hipSuccess) {
+        eif_hip_bitnet_destroy(m);
+        return EIF_HIP_E_DEVICE;
     }
     *out = m;
     return EIF_HIP_OK;
@@ -481,6 +757,7 @@ int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, voi
     EIF_HIP_LAUNCHED();                                                                      // leaves the next
     EIF_HIP_TRY(hipStreamSynchronize(st));   // the prompt buffer is the caller's
     m->hpos = 0;
+    m->n_prompt = n_prompt;
     return EIF_HIP_OK;
 }
 
@@ -514,6 +791,19 @@ int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream)
         }
         ++m->hpos;
     }
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_prefill(eif_hip_bitnet *m, int n, void *stream)
+{
+    if (!m || n < 1 || !m->head || !m->emb) return EIF_HIP_E_ARG;
+    for (int l = 0; l < m->c.n_layers; ++l)
+        if (!m->wqkv[l]) return EIF_HIP_E_ARG;
+    if (m->hpos + n > m->n_prompt) return EIF_HIP_E_ARG;   // prompt tokens only
+    int rc = ensure_prefill(m, n);
+    if (rc) return rc;
+    if ((rc = enqueue_prefill(m, m->hpos, n, (hipStream_t)stream))) return rc;
+    m->hpos += n;
     return EIF_HIP_OK;
 }
 
@@ -580,6 +870,7 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
     if (m->cap) (void)hipStreamDestroy(m->cap);
+    free_prefill(m);
     for (auto *v : {&m->wqkv, &m->wo, &m->w13, &m->w2})
         for (eif_hip_qweight *q : *v) eif_hip_qweight_destroy(q);
     eif_hip_qweight_destroy(m->head);
@@ -589,7 +880,8 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
     for (void *p : {(void *)m->rms_final, (void *)m->signs_dim, (void *)m->signs_q, (void *)m->signs_hidden,
                     (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->hb,
                     (void *)m->logits, (void *)m->kc, (void *)m->vc, (void *)m->state, (void *)m->prompt,
-                    (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_v, (void *)m->amax_i})
+                    (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_v, (void *)m->amax_i,
+                    (void *)m->rope, (void *)m->apart})
         if (p) (void)hipFree(p);
     delete m;
 }

@@ -3,8 +3,9 @@
  *
  * Replaces the token loop of the reference's tinyllm engine for the BitNet path: tinyllm_forward /
  * tinyllm_forward_embedding_ex (src/eif_tinyllm.c:371-857, :1502-1506) and its greedy sampler
- * tinyllm_sample_greedy (src/eif_tinyllm.c:1519-1530). One token step is 5 launches per layer plus 3:
- *   per layer: [RMSNorm + WHT + INT8] QKV GEMV | RoPE + fp16 KV append + attention |
+ * tinyllm_sample_greedy (src/eif_tinyllm.c:1519-1530). One token step is 6 launches per layer plus 3:
+ *   per layer: [RMSNorm + WHT + INT8] QKV GEMV | RoPE + fp16 KV append + attention over chunks of the
+ *              positions | the chunks combined |
  *              [sub-RMSNorm + WHT + INT8] O GEMV + residual | [RMSNorm + WHT + INT8] gate/up GEMV |
  *              [SiLU(gate) * up + sub-RMSNorm + WHT + INT8] down GEMV + residual
  *   RMSNorm + INT8 prep | INT8 head GEMV with per-tile maxima | argmax (greedy) or the next prompt token,
@@ -70,6 +71,14 @@ int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, voi
  * made token is stored at index p + 1 of the sequence. Steps past seq_len return EIF_HIP_E_LIMIT.
  * use_graph != 0 replays the step as a HIP graph (captured on the first such call) on the stream.       */
 int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream);
+
+/* Runs the next n prompt tokens (positions p .. p + n - 1, all within the prompt) as one batch: every linear
+ * through the prep + int8-MFMA GEMM of the n rows (the prefill of tinyllm_forward_batch_embeddings,
+ * src/eif_tinyllm.c:930-1500), RoPE and KV append for the batch, causal attention per (head, token). The
+ * state afterwards is that of n token steps: the KV cache holds the n positions, the logits are the last
+ * token's, and the current token is the prompt's next or, at the prompt's end, the argmax. Batch buffers
+ * for n tokens are allocated on the first call with that n (not during graph capture).               */
+int eif_hip_bitnet_prefill(eif_hip_bitnet *m, int n, void *stream);
 
 /* The sequence so far (ids at positions 0 .. n-1) and the logits of the last step, copied to the host
  * (synchronous).                                                                                        */

@@ -41,13 +41,15 @@ class OracleRun:
         return lo
 
 
-def compare_steps(gpu, oracle, cfg, w, prompt, n_steps, graph):
+def compare_steps(gpu, oracle, cfg, w, prompt, n_steps, graph, prefill=0):
     m = gpu.BitnetModel(cfg, w)
     orc = OracleRun(oracle, cfg, w)
     try:
         m.reset(prompt)
+        if prefill:
+            m.prefill(prefill)
         errs = []
-        for pos in range(n_steps):
+        for pos in range(prefill, n_steps):
             for layer in range(cfg["n_layers"]):       # the GPU's cache for the positions before this step
                 if pos > 0:
                     orc.kc[layer, :pos], orc.vc[layer, :pos] = m.kv_cache(layer, 0, pos)
@@ -125,5 +127,81 @@ def test_decode_limits(gpu):
         m.steps(cfg["seq_len"])
         with pytest.raises(gpu.HipError):
             m.steps(1)                         # past the context
+    finally:
+        m.close()
+
+
+def check_prefill(gpu, oracle, cfg, w, prompt, chunks):
+    """Prefill in the given chunks; every prompt position checked one step at a time against the oracle given
+    the GPU's cache of the positions before it: that position's keys and values in every layer and, at the
+    last position, the logits and the next token."""
+    m = gpu.BitnetModel(cfg, w)
+    orc = OracleRun(oracle, cfg, w)
+    L, n = cfg["n_layers"], sum(chunks)
+    try:
+        m.reset(prompt)
+        for c in chunks:
+            m.prefill(c)
+        assert m.position() == n
+        seq = m.tokens(n + 1)
+        assert list(seq[:n]) == list(prompt[:n])
+        kv = [m.kv_cache(layer, 0, n) for layer in range(L)]
+        lg = m.logits()
+        kv_errs = []
+        for p in range(n):
+            for layer in range(L):
+                orc.kc[layer, :p], orc.vc[layer, :p] = kv[layer][0][:p], kv[layer][1][:p]
+            lo = orc.step(prompt[p], p)
+            for layer in range(L):
+                for got, want in ((kv[layer][0][p], orc.kc[layer, p]), (kv[layer][1][p], orc.vc[layer, p])):
+                    e = np.abs(got - want).max() / np.abs(want).max()
+                    kv_errs.append(e)
+                    assert e <= REL, (p, layer, e)
+        assert np.median(kv_errs) <= REL_MEDIAN, kv_errs
+        err = np.abs(lg - lo).max() / np.abs(lo).max()
+        assert err <= REL and np.corrcoef(lg, lo)[0, 1] > 0.9995, err
+        if n < len(prompt):
+            assert seq[n] == prompt[n]
+        else:
+            assert seq[n] == int(np.argmax(lg))
+        return m.logits()
+    finally:
+        m.close()
+
+
+def test_prefill_tiny(gpu, oracle):
+    cfg, w = tiny()
+    prompt = list(np.random.default_rng(5).integers(0, cfg["vocab"], 20))
+    check_prefill(gpu, oracle, cfg, w, prompt, [20])          # the whole prompt, GEMM path (M >= 16)
+    check_prefill(gpu, oracle, cfg, w, prompt, [5, 3, 9])     # chunks below the GEMM threshold, stops early
+
+
+def test_prefill_head128_gqa(gpu, oracle):
+    cfg = synth.bitnet_config(512, 768, 3, 8, 2, 128, 1000, 96, 128, 96, 128, 128, 128)
+    w = synth.bitnet_model((8,), cfg)
+    prompt = list(np.random.default_rng(6).integers(0, cfg["vocab"], 70))
+    check_prefill(gpu, oracle, cfg, w, prompt, [64, 6])
+
+
+def test_prefill_then_greedy(gpu, oracle):
+    cfg, w = tiny()
+    prompt = list(np.random.default_rng(7).integers(0, cfg["vocab"], 12))
+    toks, _ = compare_steps(gpu, oracle, cfg, w, prompt, 24, graph=True, prefill=12)
+    assert list(toks[:12]) == prompt
+
+
+def test_prefill_limits(gpu):
+    cfg, w = tiny()
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        m.reset([1, 2, 3])
+        with pytest.raises(gpu.HipError):
+            m.prefill(4)                       # past the prompt
+        with pytest.raises(gpu.HipError):
+            m.prefill(0)
+        m.prefill(3)
+        assert m.position() == 3
+        with pytest.raises(gpu.HipError):
+            m.prefill(1)                       # the prompt is consumed
     finally:
         m.close()
