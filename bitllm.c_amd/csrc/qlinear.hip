@@ -502,23 +502,23 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
     const bool live = i0 < p.K, flip = block > 0 && p.signs;
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = live ? v[e] : 0.0f;
-    if (p.pre != EIF_HIP_PRE_NONE) {   // uniform
+    // RMSNorm over the K columns, (v * r) * weight with r = 1 / sqrtf(sum(v^2) / K + eps): r > 0 is one factor of
+    // the whole row, and the absmax codes of a row do not change when the row is scaled, so the rotation and the
+    // codes take v * weight and r enters the row's scale only; its sum of squares is reduced with the absmax
+    // (one barrier). Codes equal those of the normalized row up to the rounding of values on a code boundary.
+    const bool rms = p.pre != EIF_HIP_PRE_NONE;
+    float ss = 0.0f;
+    if (rms) {   // uniform
         if (p.pre == EIF_HIP_PRE_SWIGLU_RMS) {
 #pragma unroll
             for (int e = 0; e < E; ++e) v[e] = (v[e] * (1.0f / (1.0f + expf(-v[e])))) * (live ? v2[e] : 0.0f);
         }
-        // RMSNorm over the K columns: (v * (1 / sqrtf(sum(v^2) / K + eps))) * weight
-        float ss = 0.0f;
 #pragma unroll
         for (int e = 0; e < E; ++e) ss = fmaf(v[e], v[e], ss);
-        ss = wave_sum_dpp(ss);
-        if ((t & 63) == 0) red_ss[t >> 6] = ss;
-        __syncthreads();
-        ss = 0.0f;
-        for (int w = 0; w < nw; ++w) ss += red_ss[w];
-        const float inv = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+        if (p.nw) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = (v[e] * inv) * (p.nw ? nwv[e] : 1.0f);
+            for (int e = 0; e < E; ++e) v[e] = v[e] * nwv[e];
+        }
     }
     if (flip) {
 #pragma unroll
@@ -548,13 +548,21 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
         amax = fmaxf(amax, fabsf(v[e]));
     }
     amax = wave_max_dpp(amax);
-    if ((t & 63) == 0) red[t >> 6] = amax;
+    if (rms) ss = wave_sum_dpp(ss);
+    if ((t & 63) == 0) red[t >> 6] = amax, red_ss[t >> 6] = ss;
     __syncthreads();
-    // the per-wave maxima, one per lane, reduced again across the wave
-    amax = wave_max_dpp(red[(t & 63) < nw ? (t & 63) : 0]);
-    const bool zero = amax < 1e-12f;
+    // the per-wave maxima (and sums), one per lane, reduced again across the wave
+    const int ln = t & 63;
+    amax = wave_max_dpp(red[ln < nw ? ln : 0]);
+    float r = 1.0f;
+    if (rms) {
+        ss = wave_sum_dpp(ln < nw ? red_ss[ln] : 0.0f);
+        r = 1.0f / sqrtf(ss / (float)p.K + p.eps);
+    }
+    const float amax_n = amax * r;   // the absmax of the normalized row (amax itself without a pre-op)
+    const bool zero = amax_n < 1e-12f;
     const float inv = zero ? 0.0f : 127.0f / amax;
-    if (t == 0) xs_l[m] = zero ? 1.0f : amax * (1.0f / 127.0f);
+    if (t == 0) xs_l[m] = zero ? 1.0f : amax_n * (1.0f / 127.0f);
     if (i0 < kpad) {
         uint32_t d[E / 4];
 #pragma unroll
