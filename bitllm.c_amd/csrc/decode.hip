@@ -6,8 +6,7 @@
 // the GEMV with per-tile maxima (the argmax's first stage), and kernels of its own:
 //   attn_split_kernel   RoPE of q and k (:396-405, :476-507; angles from a table made once), fp16 KV append,
 //                       softmax attention (:555-650) of each query head over one chunk of the positions per
-//                       workgroup, one pass over the chunk
-//   attn_combine_kernel the chunks' shares of each head combined
+//                       workgroup, one pass over the chunk; the head's last chunk to finish combines the shares
 //   sample_kernel       greedy argmax over the head's tile maxima (first maximum, src/eif_tinyllm.c:1519-1530)
 //                       or the next prompt token, stored in the sequence; position + 1; x = the next token's
 //                       INT8 embedding row * its scale (src/eif_tinyllm.c:902-916)
@@ -79,7 +78,7 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
 // This is the softmax of the scores followed by the weighted sum of the values, with the sums taken in another
 // order.
 // PARTIAL: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized, out[HD] = M, out[HD + 1] = sum_r e^(m_r - M) l_r
-// (a chunk's share, combined with the others by attn_combine_kernel).
+// (a chunk's share; the head's last chunk to finish combines the shares).
 template <int HD, int NT, bool PARTIAL = false>
 EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int n_cache, const float *k_x,
                     const float *v_x, float inv_sqrt_hd, float *out)
@@ -195,30 +194,31 @@ EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int 
 
 // Decode, split over the positions: workgroup (h, s) takes query head h (kv head g = h / kv_mul) over the cache
 // rows of chunk s, [s CH, min((s + 1) CH, pos)), CH = the rows one batch of attend<HD, 256> covers; chunk
-// pos / CH also takes row pos itself. Chunks past pos write an empty share (max -inf, sum 0) and exit. Every workgroup rotates q_h (RoPE from the table);
+// pos / CH also takes row pos itself. Chunks past pos exit. Every workgroup rotates q_h (RoPE from the table);
 // the workgroup of the last chunk also rotates k_g, rounds k and v to fp16 and, for the first query head of
 // the kv head, appends them to the cache. Each writes its share (attend's partial form) to
-// part[(h * n_chunks + s) * (HD + 2)].
+// part[(h * n_chunks + s) * (HD + 2)], then counts itself in cnt[h] (agent-scope release before the count);
+// the workgroup that completes the count (acquire after it) combines the head's shares,
+//   M = max_s M_s, out = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s,
+// and sets cnt[h] back to 0 for the next step. No workgroup waits on another.
 // Cache layout: [kv_head][seq_len][HD] fp16 per layer.
 template <int HD>
 constexpr int attn_chunk() { return (256 / (HD / 8)) * 8; }
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __half *kc, __half *vc, const int *state,
-                                                         const float2 *rope, float *part, int n_chunks, int n_heads,
-                                                         int n_kv, int seq_len, float inv_sqrt_hd)
+                                                         const float2 *rope, float *part, int *cnt, float *out,
+                                                         int n_chunks, int n_heads, int n_kv, int seq_len,
+                                                         float inv_sqrt_hd)
 {
     constexpr int HALF = HD / 2, CH = attn_chunk<HD>();
     __shared__ float q_l[HD], k_l[HD], v_l[HD];
+    __shared__ int last_l;
     const int h = blockIdx.x, sc = blockIdx.y, kv_mul = n_heads / n_kv, g = h / kv_mul;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
     const int pos = state[0];
     const int c0 = sc * CH;
-    if (c0 > pos) {   // uniform over the workgroup: an empty share
-        float *pe = part + ((size_t)h * n_chunks + sc) * (HD + 2);
-        if (threadIdx.x == 0) pe[HD] = -INFINITY, pe[HD + 1] = 0.0f;
-        return;
-    }
+    if (c0 > pos) return;   // uniform over the workgroup
     const bool last = pos < c0 + CH;
     const int t = threadIdx.x;
     if (t < HALF) {
@@ -245,29 +245,31 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __hal
     __syncthreads();
     const size_t base = ((size_t)g * seq_len + c0) * HD;
     const int rows = (last ? pos : c0 + CH) - c0;
+    float *ph = part + (size_t)h * n_chunks * (HD + 2);
     attend<HD, 256, true>(q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr, inv_sqrt_hd,
-                          part + ((size_t)h * n_chunks + sc) * (HD + 2));
-}
-
-// The chunks' shares of query head h combined: M = max_s M_s, out = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s
-// over all chunks (an empty share weighs 0, its stale O is not read into the sum).
-template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const float *part, float *out, int n_chunks)
-{
-    const int h = blockIdx.x, t = threadIdx.x;
-    const float *ph = part + (size_t)h * n_chunks * (HD + 2);
-    float mx = -INFINITY;
-    for (int sc = 0; sc < n_chunks; ++sc) mx = fmaxf(mx, ph[(size_t)sc * (HD + 2) + HD]);
-    float os = 0.0f, ls = 0.0f;
-    for (int sc = 0; sc < n_chunks; ++sc) {
-        const float *p = ph + (size_t)sc * (HD + 2);
-        const float ms = p[HD], o = p[t], l = p[HD + 1];
-        const bool live = ms != -INFINITY;
-        const float w = live ? expf(ms - mx) : 0.0f;
-        os = fmaf(w, live ? o : 0.0f, os);
-        ls = fmaf(w, l, ls);
+                          ph + (size_t)sc * (HD + 2));
+    __syncthreads();   // the workgroup's share is written
+    const int ns = pos / CH + 1;
+    if (t == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        last_l = atomicAdd(&cnt[h], 1) == ns - 1;
     }
-    out[h * HD + t] = os / ls;
+    __syncthreads();
+    if (!last_l) return;   // uniform
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (t < HD) {
+        float mx = -INFINITY;
+        for (int s2 = 0; s2 < ns; ++s2) mx = fmaxf(mx, ph[(size_t)s2 * (HD + 2) + HD]);
+        float os = 0.0f, ls = 0.0f;
+        for (int s2 = 0; s2 < ns; ++s2) {
+            const float *pp = ph + (size_t)s2 * (HD + 2);
+            const float w = expf(pp[HD] - mx);
+            os = fmaf(w, pp[t], os);
+            ls = fmaf(w, pp[HD + 1], ls);
+        }
+        out[h * HD + t] = os / ls;
+    }
+    if (t == 0) cnt[h] = 0;
 }
 
 // Prefill, step 1: token i of a batch at position pos0 + i (one workgroup per token). RoPE of every query head
@@ -423,6 +425,7 @@ struct eif_hip_bitnet {
     int *state = nullptr, *prompt = nullptr, *seq = nullptr;
     float2 *rope = nullptr;          // RoPE (cos, sin) [seq_len][head_dim / 2]
     float *apart = nullptr;          // attention chunk shares [n_heads][n_chunks][head_dim + 2]
+    int *acnt = nullptr;             // per head, the chunks done this step (0 between steps)
     int n_chunks = 0;
     int8_t *hq = nullptr;            // the head's prepped input row [head_kpad] and its scale
     float *hs = nullptr;
@@ -460,12 +463,8 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         auto attn = c.head_dim == 128 ? attn_split_kernel<128>
                     : (c.head_dim == 64 ? attn_split_kernel<64> : attn_split_kernel<32>);
         attn<<<dim3(c.n_heads, m->n_chunks), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
-                                                           m->rope, m->apart, m->n_chunks, c.n_heads, c.n_kv_heads,
-                                                           c.seq_len, inv_sqrt_hd);
-        EIF_HIP_LAUNCHED();
-        auto comb = c.head_dim == 128 ? attn_combine_kernel<128>
-                    : (c.head_dim == 64 ? attn_combine_kernel<64> : attn_combine_kernel<32>);
-        comb<<<c.n_heads, c.head_dim, 0, st>>>(m->apart, m->xb, m->n_chunks);
+                                                           m->rope, m->apart, m->acnt, m->xb, m->n_chunks, c.n_heads,
+                                                           c.n_kv_heads, c.seq_len, inv_sqrt_hd);
         EIF_HIP_LAUNCHED();
         sp = eif_hip_prep_spec{};
         sp.x = m->xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l], sp.eps = c.sub_eps;
@@ -664,7 +663,9 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
     const int ch = c.head_dim == 128 ? attn_chunk<128>() : (c.head_dim == 64 ? attn_chunk<64>() : attn_chunk<32>());
     m->n_chunks = (c.seq_len + ch - 1) / ch;
     if (hipMalloc(&m->rope, sizeof(float2) * c.seq_len * (c.head_dim / 2)) != hipSuccess ||
-        hipMalloc(&m->apart, sizeof(float) * c.n_heads * m->n_chunks * (c.head_dim + 2)) != hipSuccess) {
+        hipMalloc(&m->apart, sizeof(float) * c.n_heads * m->n_chunks * (c.head_dim + 2)) != hipSuccess ||
+        hipMalloc(&m->acnt, sizeof(int) * c.n_heads) != hipSuccess ||
+        hipMemset(m->acnt, 0, sizeof(int) * c.n_heads) != hipSuccess) {
         eif_hip_bitnet_destroy(m);
         return EIF_HIP_E_NOMEM;
     }
@@ -881,7 +882,7 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
                     (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->hb,
                     (void *)m->logits, (void *)m->kc, (void *)m->vc, (void *)m->state, (void *)m->prompt,
                     (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_v, (void *)m->amax_i,
-                    (void *)m->rope, (void *)m->apart})
+                    (void *)m->rope, (void *)m->apart, (void *)m->acnt})
         if (p) (void)hipFree(p);
     delete m;
 }
