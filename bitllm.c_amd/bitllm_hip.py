@@ -54,6 +54,8 @@ _SIGS = {
     "eif_hip_bitnet_reset": (_i, [_vp, _vp, _i, _vp]),
     "eif_hip_bitnet_steps": (_i, [_vp, _i, _i, _vp]),
     "eif_hip_bitnet_prefill": (_i, [_vp, _i, _vp]),
+    "eif_hip_bitnet_load_svlm": (_i, [_vp, C.c_char_p, _i]),
+    "eif_hip_bitnet_get_config": (_i, [_vp, _vp]),
     "eif_hip_bitnet_tokens": (_i, [_vp, _vp, _i, _vp]),
     "eif_hip_bitnet_logits": (_i, [_vp, _vp, _vp]),
     "eif_hip_bitnet_position": (_i, [_vp, _vp]),
@@ -255,6 +257,19 @@ class BitnetModel:
         g = BitnetGlobals(**{k: (w[k].ctypes.data if w.get(k) is not None else None)
                              for k, _ in BitnetGlobals._fields_})
         check(lib.eif_hip_bitnet_set_globals(h, C.byref(g)), "eif_hip_bitnet_set_globals")
+
+    @classmethod
+    def from_svlm(cls, path, seq_len=0):
+        """A model read from a BitNet SVLM file (eif_hip_bitnet_load_svlm)."""
+        lib = load()
+        h = C.c_void_p()
+        check(lib.eif_hip_bitnet_load_svlm(C.byref(h), os.fsencode(path), seq_len), "eif_hip_bitnet_load_svlm")
+        self = cls.__new__(cls)
+        self.h = h
+        self.c = BitnetConfig()
+        check(lib.eif_hip_bitnet_get_config(h, C.byref(self.c)), "eif_hip_bitnet_get_config")
+        self.cfg = {k: getattr(self.c, k) for k, _ in BitnetConfig._fields_}
+        return self
 
     def reset(self, prompt, stream=None):
         import numpy as np

@@ -602,7 +602,7 @@ int enqueue_prefill(eif_hip_bitnet *m, int pos0, int n, hipStream_t st)
 void stack_rows(std::vector<uint8_t> &codes, std::vector<float> &scales, const uint8_t *w, const float *s, int rows,
                 int cols, int group)
 {
-    const size_t rb = (size_t)(cols + 3) / 4, ng = (size_t)(cols + group - 1) / group;
+    const size_t rb = (size_t)(cols + 3) / 4, ng = group > 0 ? (size_t)(cols + group - 1) / group : 1;
     codes.insert(codes.end(), w, w + rows * rb);
     scales.insert(scales.end(), s, s + rows * ng);
 }
@@ -854,6 +854,13 @@ int eif_hip_bitnet_kv_cache(eif_hip_bitnet *m, int layer, int pos0, int n, float
                 k[d] = __half2float(hk[s]);
                 v[d] = __half2float(hv[s]);
             }
+    return EIF_HIP_OK;
+}
+
+int eif_hip_bitnet_get_config(const eif_hip_bitnet *m, eif_hip_bitnet_config *out)
+{
+    if (!m || !out) return EIF_HIP_E_ARG;
+    *out = m->c;
     return EIF_HIP_OK;
 }
 

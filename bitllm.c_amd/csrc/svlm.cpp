@@ -1,0 +1,184 @@
+// svlm.cpp -- a BitNet-b1.58 model file in the reference's SVLM layout -> the GPU decoder (eif_hip_decode.h).
+//
+// The file is what tinyllm_load_quantized_model reads (src/eif_tinyllm.c:2442-2556) with the pointer layout of
+// tinyllm_setup_quantized_pointers for BitNet (:2690-2731) and the configuration that the reference's engine
+// reads from it (src/eif_llm.c:321-342):
+//   header   12 x u32: [0] 'SVLM', [3] weights offset, [4] scales offset, [5] norms offset, [7] weights bytes,
+//            [8] scales bytes, [9] norms bytes (the other words: version and the vision encoder, unused here)
+//   config   32 x i32 at byte 48: dim, hidden, layers, heads, kv heads, head_dim (0: dim / heads), vocab,
+//            seq_len (0: 512); [12] qtype (3 = BitNet b1.58), [14] group bound (0: one scale per row),
+//            [15] Hadamard-rotated weights; RoPE theta 100000
+//   weights  INT8 embedding [vocab][dim]; per kind q, k, v, o, w1, w2, w3 the 2-bit rows of every layer
+//            [layers][rows][(in + 3) / 4]; INT8 head [vocab][dim]
+//   scales   embedding scales [vocab]; per kind q, k, v, o, w1, w3, w2 the group scales [layers][rows][in / g]
+//            with g = eif_bitnet_group_size(in, bound) (the input width itself when 0); head scales [vocab];
+//            with the Hadamard flag, the signs of the dim, q_dim and hidden inputs
+//   norms    attention [layers][dim], FFN [layers][dim], final [dim], then the sub-norms [layers][q_dim] and
+//            [layers][hidden] (absent: weight 1)
+// The model's other choices are tinyllm's: rotation blocks eif_hadamard_block_size(width) with the reference
+// build's 1/sqrt(block) (eif_hip_wht_norm), RMSNorm epsilon 1e-6 above 120000 tokens of vocabulary else 1e-5,
+// sub-norm epsilon 1e-5 (src/eif_tinyllm.c:395-410, :660-670, :790-795).
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/eif_hip.h"
+#include "../../include/eif_hip_decode.h"
+#include "../../include/eif_quantize_bitnet.h"
+
+namespace {
+
+constexpr uint32_t kSvlmMagic = 0x53564C4Du;
+
+struct File {
+    FILE *f = nullptr;
+    ~File()
+    {
+        if (f) std::fclose(f);
+    }
+};
+
+bool read_at(FILE *f, long off, void *dst, size_t bytes)
+{
+    return std::fseek(f, off, SEEK_SET) == 0 && std::fread(dst, 1, bytes, f) == bytes;
+}
+
+}  // namespace
+
+extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, int seq_len)
+{
+    if (!out || !path) return EIF_HIP_E_ARG;
+    *out = nullptr;
+    File file;
+    file.f = std::fopen(path, "rb");
+    if (!file.f) return EIF_HIP_E_ARG;
+    uint32_t hdr[12];
+    int32_t ci[32];
+    if (!read_at(file.f, 0, hdr, sizeof(hdr)) || hdr[0] != kSvlmMagic || !read_at(file.f, 48, ci, sizeof(ci)))
+        return EIF_HIP_E_ARG;
+    const int dim = ci[0], hidden = ci[1], L = ci[2], nh = ci[3], nkv = ci[4], vocab = ci[6];
+    const int hd = ci[5] > 0 ? ci[5] : (nh > 0 ? dim / nh : 0);
+    const int bound = ci[14], had = ci[15];
+    if (ci[12] != 3 || dim <= 0 || hidden <= 0 || L <= 0 || nh <= 0 || nkv <= 0 || vocab <= 0 || hd <= 0 ||
+        bound < 0 || (bound == 0 && !had))   // per-row files without the flag use the row-scale layout
+        return EIF_HIP_E_ARG;
+    const int q_dim = nh * hd, kv_dim = nkv * hd;
+    const int file_seq = ci[7] > 0 ? ci[7] : 512;
+    // group of a kind with input width `in` (0 = one scale per row, as the file stores g = in)
+    auto group_of = [&](int in) {
+        const int g = bound > 0 ? eif_bitnet_group_size(in, bound) : 0;
+        return g <= 0 || g >= in ? 0 : g;
+    };
+    auto ngroups = [&](int in) {
+        const int g = group_of(in);
+        return g > 0 ? (size_t)(in / g) : (size_t)1;
+    };
+    const size_t dp = (size_t)(dim + 3) / 4, qp = (size_t)(q_dim + 3) / 4, hp = (size_t)(hidden + 3) / 4;
+    const size_t w_bytes = (size_t)vocab * dim * 2 +
+                           (size_t)L * ((size_t)q_dim * dp + 2 * (size_t)kv_dim * dp + (size_t)dim * qp +
+                                        2 * (size_t)hidden * dp + (size_t)dim * hp);
+    const size_t rows_in[7][2] = {{(size_t)q_dim, (size_t)dim}, {(size_t)kv_dim, (size_t)dim},
+                                  {(size_t)kv_dim, (size_t)dim}, {(size_t)dim, (size_t)q_dim},
+                                  {(size_t)hidden, (size_t)dim}, {(size_t)hidden, (size_t)dim},
+                                  {(size_t)dim, (size_t)hidden}};   // q, k, v, o, w1, w3, w2 (the scales' order)
+    size_t s_count = 2 * (size_t)vocab;
+    for (const auto &ri : rows_in) s_count += (size_t)L * ri[0] * ngroups((int)ri[1]);
+    if (had) s_count += (size_t)dim + q_dim + hidden;
+    const size_t n_std = (size_t)L * dim * 2 + dim, n_sub = (size_t)L * (q_dim + hidden);
+    if (hdr[7] < w_bytes || hdr[8] < s_count * sizeof(float) || hdr[9] < n_std * sizeof(float)) return EIF_HIP_E_ARG;
+    const bool subs = hdr[9] >= (n_std + n_sub) * sizeof(float);
+    std::vector<uint8_t> wb;
+    std::vector<float> sb, nb;
+    try {
+        wb.resize(w_bytes);
+        sb.resize(s_count);
+        nb.resize(subs ? n_std + n_sub : n_std);
+    } catch (...) {
+        return EIF_HIP_E_NOMEM;
+    }
+    if (!read_at(file.f, (long)hdr[3], wb.data(), wb.size()) ||
+        !read_at(file.f, (long)hdr[4], sb.data(), sb.size() * sizeof(float)) ||
+        !read_at(file.f, (long)hdr[5], nb.data(), nb.size() * sizeof(float)))
+        return EIF_HIP_E_ARG;
+
+    eif_hip_bitnet_config c{};
+    c.dim = dim, c.hidden = hidden, c.n_layers = L, c.n_heads = nh, c.n_kv_heads = nkv, c.head_dim = hd;
+    c.vocab = vocab, c.seq_len = seq_len > 0 ? seq_len : file_seq;
+    c.rope_theta = 100000.0f;
+    c.rms_eps = vocab > 120000 ? 1e-6f : 1e-5f;
+    c.sub_eps = 1e-5f;
+    if (had) {
+        c.wht_dim = eif_hadamard_block_size(dim), c.wht_q = eif_hadamard_block_size(q_dim);
+        c.wht_hidden = eif_hadamard_block_size(hidden);
+        c.wht_norm_dim = eif_hip_wht_norm(c.wht_dim), c.wht_norm_q = eif_hip_wht_norm(c.wht_q);
+        c.wht_norm_hidden = eif_hip_wht_norm(c.wht_hidden);
+    }
+    c.g_q = group_of(dim), c.g_o = group_of(q_dim), c.g_13 = group_of(dim), c.g_2 = group_of(hidden);
+
+    // weights: embedding, then per kind all layers
+    const uint8_t *p = wb.data();
+    const int8_t *emb = reinterpret_cast<const int8_t *>(p);
+    p += (size_t)vocab * dim;
+    const uint8_t *wq = p;
+    p += (size_t)L * q_dim * dp;
+    const uint8_t *wk = p;
+    p += (size_t)L * kv_dim * dp;
+    const uint8_t *wv = p;
+    p += (size_t)L * kv_dim * dp;
+    const uint8_t *wo = p;
+    p += (size_t)L * dim * qp;
+    const uint8_t *w1 = p;
+    p += (size_t)L * hidden * dp;
+    const uint8_t *w2 = p;
+    p += (size_t)L * dim * hp;
+    const uint8_t *w3 = p;
+    p += (size_t)L * hidden * dp;
+    const int8_t *wcls = reinterpret_cast<const int8_t *>(p);
+    // scales
+    const float *sp = sb.data();
+    const float *emb_scale = sp;
+    sp += vocab;
+    const float *gs[7];
+    for (int k = 0; k < 7; ++k) {
+        gs[k] = sp;
+        sp += (size_t)L * rows_in[k][0] * ngroups((int)rows_in[k][1]);
+    }
+    const float *wcls_scale = sp;
+    sp += vocab;
+    const float *sg_dim = had ? sp : nullptr;
+    const float *sg_q = had ? sp + dim : nullptr;
+    const float *sg_hidden = had ? sp + dim + q_dim : nullptr;
+    // norms
+    const float *rms_att = nb.data(), *rms_ffn = rms_att + (size_t)L * dim, *rms_final = rms_ffn + (size_t)L * dim;
+    const float *sub_att = subs ? rms_final + dim : nullptr;
+    const float *sub_ffn = subs ? sub_att + (size_t)L * q_dim : nullptr;
+
+    eif_hip_bitnet *m = nullptr;
+    int rc = eif_hip_bitnet_create(&m, &c);
+    if (rc) return rc;
+    for (int l = 0; l < L && rc == EIF_HIP_OK; ++l) {
+        eif_hip_bitnet_layer lw{};
+        lw.wq = wq + (size_t)l * q_dim * dp, lw.wk = wk + (size_t)l * kv_dim * dp, lw.wv = wv + (size_t)l * kv_dim * dp;
+        lw.wo = wo + (size_t)l * dim * qp, lw.w1 = w1 + (size_t)l * hidden * dp, lw.w3 = w3 + (size_t)l * hidden * dp;
+        lw.w2 = w2 + (size_t)l * dim * hp;
+        const float **g[7] = {&lw.gq, &lw.gk, &lw.gv, &lw.go, &lw.g1, &lw.g3, &lw.g2};
+        for (int k = 0; k < 7; ++k) *g[k] = gs[k] + (size_t)l * rows_in[k][0] * ngroups((int)rows_in[k][1]);
+        lw.rms_att = rms_att + (size_t)l * dim, lw.rms_ffn = rms_ffn + (size_t)l * dim;
+        lw.rms_sub_att = sub_att ? sub_att + (size_t)l * q_dim : nullptr;
+        lw.rms_sub_ffn = sub_ffn ? sub_ffn + (size_t)l * hidden : nullptr;
+        rc = eif_hip_bitnet_set_layer(m, l, &lw);
+    }
+    if (rc == EIF_HIP_OK) {
+        eif_hip_bitnet_globals gl{};
+        gl.emb = emb, gl.emb_scale = emb_scale, gl.rms_final = rms_final;
+        gl.signs_dim = sg_dim, gl.signs_q = sg_q, gl.signs_hidden = sg_hidden;
+        gl.wcls = wcls, gl.wcls_scale = wcls_scale;
+        rc = eif_hip_bitnet_set_globals(m, &gl);
+    }
+    if (rc) {
+        eif_hip_bitnet_destroy(m);
+        return rc;
+    }
+    *out = m;
+    return EIF_HIP_OK;
+}

@@ -163,7 +163,7 @@ def bitnet_model(key, cfg):
               "1": (h, d, cfg["g_13"]), "3": (h, d, cfg["g_13"]), "2": (d, h, cfg["g_2"])}
     for i, (name, (N, K, g)) in enumerate(shapes.items()):
         w["w" + name] = ternary_packed((*key, 20 + i), L * N, K)
-        ng = -(-K // g)
+        ng = -(-K // g) if g else 1   # g = 0: one scale per row
         w["g" + name] = (np.abs(rng(*key, 30 + i).standard_normal((L * N, ng))) * 0.02 + 0.005).astype(np.float32)
     for i, (name, n) in enumerate((("rms_att", d), ("rms_ffn", d), ("rms_sub_att", qd), ("rms_sub_ffn", h))):
         w[name] = (1.0 + 0.1 * rng(*key, 40 + i).standard_normal(L * n)).astype(np.float32)
@@ -173,3 +173,36 @@ def bitnet_model(key, cfg):
     w["wcls"] = rng(*key, 60).integers(-127, 128, size=(V, d), dtype=np.int8)
     w["wcls_scale"] = (np.abs(rng(*key, 61).standard_normal(V)) * 0.01 + 0.002).astype(np.float32)
     return w
+
+
+def write_svlm(path, cfg, w, group_bound, hadamard=True):
+    """Write a BitNet model (bitnet_model's arrays) as a file in the reference's SVLM layout, the one
+    tinyllm_load_quantized_model reads (src/eif_tinyllm.c:2442-2556, pointers as tinyllm_setup_quantized_pointers
+    sets them, :2690-2731; configuration words as src/eif_llm.c:321-342 reads them). cfg's groups must be the
+    ones the reader derives: eif_bitnet_group_size(input width, group_bound), or 0 (one scale per row) when that is
+    0 or the width itself."""
+    d, h, L = cfg["dim"], cfg["hidden"], cfg["n_layers"]
+    weights = b"".join(np.ascontiguousarray(w[k]).tobytes()
+                       for k in ("emb", "wq", "wk", "wv", "wo", "w1", "w2", "w3", "wcls"))
+    skeys = ["emb_scale", "gq", "gk", "gv", "go", "g1", "g3", "g2", "wcls_scale"]
+    if hadamard:
+        skeys += ["signs_dim", "signs_q", "signs_hidden"]
+    scales = b"".join(np.ascontiguousarray(w[k], dtype=np.float32).tobytes() for k in skeys)
+    norms = b"".join(np.ascontiguousarray(w[k], dtype=np.float32).tobytes()
+                     for k in ("rms_att", "rms_ffn", "rms_final", "rms_sub_att", "rms_sub_ffn"))
+    w_off = 48 + 128
+    s_off = w_off + len(weights)
+    r_off = s_off + len(scales)
+    hdr = np.zeros(12, np.uint32)
+    hdr[0], hdr[1] = 0x53564C4D, 1
+    hdr[3], hdr[4], hdr[5] = w_off, s_off, r_off
+    hdr[7], hdr[8], hdr[9] = len(weights), len(scales), len(norms)
+    ci = np.zeros(32, np.int32)
+    ci[:8] = [d, h, L, cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["vocab"], cfg["seq_len"]]
+    ci[12], ci[14], ci[15] = 3, group_bound, 1 if hadamard else 0
+    with open(path, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(ci.tobytes())
+        f.write(weights)
+        f.write(scales)
+        f.write(norms)

@@ -38,7 +38,7 @@ typedef struct eif_hip_bitnet_config {
     float sub_eps;                          /* sub-norm epsilon (1e-5 in the reference) */
     int wht_dim, wht_q, wht_hidden;         /* WHT blocks of the inputs of wq/wk/wv/w1/w3, wo, w2 (0: none) */
     float wht_norm_dim, wht_norm_q, wht_norm_hidden;   /* their scales, e.g. eif_hip_wht_norm(block) */
-    int g_q, g_o, g_13, g_2;                /* ternary groups of wq/wk/wv, wo, w1/w3, w2 */
+    int g_q, g_o, g_13, g_2;                /* ternary groups of wq/wk/wv, wo, w1/w3, w2 (0: one scale per row) */
 } eif_hip_bitnet_config;
 
 typedef struct eif_hip_bitnet_layer {       /* one layer, host pointers */
@@ -55,6 +55,13 @@ typedef struct eif_hip_bitnet_globals {    /* host pointers */
     const int8_t *wcls;                     /* [vocab, dim] */
     const float *wcls_scale;                /* [vocab] or NULL */
 } eif_hip_bitnet_globals;
+
+/* A BitNet-b1.58 model file in the reference's SVLM layout (what tinyllm_load_quantized_model reads,
+ * src/eif_tinyllm.c:2442-2556, laid out as tinyllm_setup_quantized_pointers expects, :2690-2731, configured as
+ * src/eif_llm.c:321-342 reads it: RoPE theta 100000, the file's group bound and Hadamard flag) -> a ready model,
+ * weights repacked into the GPU layout. seq_len <= 0 takes the file's (512 when it has none). Files of another
+ * layout (not BitNet, or neither group scales nor rotation) return EIF_HIP_E_ARG.                      */
+int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, int seq_len);
 
 /* Allocates the model (weights are set separately). Limits: head_dim 32, 64 or 128, n_heads a multiple of
  * n_kv_heads, seq_len <= 4096, dim / q_dim / hidden multiples of 32 with the WHT blocks dividing them.      */
@@ -89,6 +96,9 @@ int eif_hip_bitnet_position(eif_hip_bitnet *m, void *stream);   /* current posit
 /* Cached keys and values of one layer at positions [pos0, pos0 + n), as floats in the reference's cache layout
  * [position][kv_head * head_dim + i] (src/eif_tinyllm.c:414-418), copied to the host (synchronous).           */
 int eif_hip_bitnet_kv_cache(eif_hip_bitnet *m, int layer, int pos0, int n, float *k, float *v, void *stream);
+
+/* The model's configuration (e.g. of a model read from a file).                                          */
+int eif_hip_bitnet_get_config(const eif_hip_bitnet *m, eif_hip_bitnet_config *out);
 
 /* Bytes of weights, scales and norms resident on the device, and the KV bytes one step reads at position p. */
 size_t eif_hip_bitnet_weight_bytes(const eif_hip_bitnet *m);

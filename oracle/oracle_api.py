@@ -123,4 +123,5 @@ REF_TINYLLM_SIGS = {
     "ref_bitnet_create": (_vp, [_vp, _vp, _i]),
     "ref_bitnet_forward": (C.POINTER(_f), [_vp, _i, _i]),
     "ref_bitnet_destroy": (None, [_vp]),
+    "ref_svlm_create": (_vp, [C.c_char_p]),
 }

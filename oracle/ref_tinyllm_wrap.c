@@ -3,6 +3,8 @@
  * the in-memory construction of tests/test_seq_bounds.c:11-26) from the oracle's weight arrays and runs its decode
  * (tinyllm_forward, src/eif_tinyllm.c:1502-1506). Compiled together with the reference sources into oracle/_ref/.
  */
+#include <stdint.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -13,6 +15,7 @@ typedef struct {
     tinyllm_t llm;
     void *pool;
     float *ones;
+    void *wbuf;
 } ref_bitnet;
 
 /* bitnet_group: the reference's one group bound for all matrices (eif_bitnet_group_size per input width). */
@@ -70,5 +73,38 @@ void ref_bitnet_destroy(void *h)
 {
     ref_bitnet *r = (ref_bitnet *)h;
     if (!r) return;
-    free(r->pool), free(r->ones), free(r);
+    free(r->pool), free(r->ones), free(r->wbuf), free(r);
+}
+
+/* A BitNet model file in the SVLM layout read by the reference itself: the configuration words as its engine
+ * reads them (src/eif_llm.c:321-342), tinyllm_init, then tinyllm_load_quantized_model (src/eif_tinyllm.c:2442)
+ * into a weight buffer, as src/eif_llm.c:343-395 does. Returns a handle for ref_bitnet_forward / _destroy. */
+void *ref_svlm_create(const char *path)
+{
+    FILE *f = fopen(path, "rb");
+    if (!f) return NULL;
+    uint32_t hdr[12];
+    int32_t ci[32];
+    const int ok = fread(hdr, 4, 12, f) == 12 && fseek(f, 48, SEEK_SET) == 0 && fread(ci, 4, 32, f) == 32;
+    fclose(f);
+    if (!ok || hdr[0] != 0x53564C4Du) return NULL;
+    tinyllm_config_t cfg;
+    memset(&cfg, 0, sizeof(cfg));
+    cfg.dim = ci[0], cfg.hidden_dim = ci[1], cfg.n_layers = ci[2], cfg.n_heads = ci[3], cfg.n_kv_heads = ci[4];
+    cfg.head_dim = ci[5], cfg.vocab_size = ci[6], cfg.seq_len = ci[7] > 0 ? ci[7] : 512;
+    cfg.rope_theta = 100000.0f;
+    cfg.qtype = ci[12] == 3 ? TINYLLM_QTYPE_BITNET_158 : (tinyllm_qtype_t)ci[12];
+    cfg.bitnet_group = ci[14];
+    cfg.bitnet_hadamard = ci[15];
+    ref_bitnet *r = (ref_bitnet *)calloc(1, sizeof(ref_bitnet));
+    if (!r) return NULL;
+    const size_t sz = tinyllm_memory_size(&cfg), wsz = (size_t)hdr[7] + hdr[8] + hdr[9];
+    r->pool = malloc(sz);
+    r->wbuf = malloc(wsz);
+    if (!r->pool || !r->wbuf || tinyllm_init(&r->llm, &cfg, r->pool, sz) != 0 ||
+        tinyllm_load_quantized_model(&r->llm, path, r->wbuf, wsz) != 0) {
+        free(r->pool), free(r->wbuf), free(r);
+        return NULL;
+    }
+    return r;
 }

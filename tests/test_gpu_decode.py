@@ -41,9 +41,9 @@ class OracleRun:
         return lo
 
 
-def compare_steps(gpu, oracle, cfg, w, prompt, n_steps, graph, prefill=0):
+def compare_steps(gpu, oracle, cfg, w, prompt, n_steps, graph, prefill=0, oracle_cfg=None):
     m = gpu.BitnetModel(cfg, w)
-    orc = OracleRun(oracle, cfg, w)
+    orc = OracleRun(oracle, oracle_cfg or cfg, w)
     try:
         m.reset(prompt)
         if prefill:
@@ -97,6 +97,17 @@ def test_decode_head128_gqa(gpu, oracle):
     w = synth.bitnet_model((8,), cfg)
     prompt = list(np.random.default_rng(4).integers(0, cfg["vocab"], 64))
     compare_steps(gpu, oracle, cfg, w, prompt, 80, graph=False)
+
+
+def test_decode_row_scales(gpu, oracle):
+    # one scale per ternary row (group 0 on the GPU, one group spanning the input in the oracle)
+    cfg = make_golden.decode_config()
+    for k in ("g_q", "g_o", "g_13", "g_2"):
+        cfg[k] = 0
+    w = synth.bitnet_model((13,), cfg)
+    ocfg = dict(cfg, g_q=cfg["dim"], g_o=cfg["n_heads"] * cfg["head_dim"], g_13=cfg["dim"], g_2=cfg["hidden"])
+    prompt = list(np.random.default_rng(9).integers(0, cfg["vocab"], 6))
+    compare_steps(gpu, oracle, cfg, w, prompt, 16, graph=False, prefill=4, oracle_cfg=ocfg)
 
 
 def test_decode_graph_equals_eager(gpu, oracle):
@@ -205,3 +216,54 @@ def test_prefill_limits(gpu):
             m.prefill(1)                       # the prompt is consumed
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("bound,group", [(32, 32), (0, 0)])
+def test_svlm_file_equals_in_memory(gpu, tmp_path, bound, group):
+    """A model read from an SVLM file (eif_hip_bitnet_load_svlm) decodes bit for bit as the same arrays set in
+    memory with the configuration the reader derives (theta 100000, tinyllm's rotation blocks and groups)."""
+    cfg = make_golden.decode_config()
+    cfg["rope_theta"] = 100000.0
+    for k in ("g_q", "g_o", "g_13", "g_2"):
+        cfg[k] = group
+    for k, b in (("wht_norm_dim", "wht_dim"), ("wht_norm_q", "wht_q"), ("wht_norm_hidden", "wht_hidden")):
+        cfg[k] = gpu.wht_norm(cfg[b])
+    w = synth.bitnet_model((12, group), cfg)
+    path = str(tmp_path / "model.svlm")
+    synth.write_svlm(path, cfg, w, bound)
+    mf = gpu.BitnetModel.from_svlm(path)
+    mm = gpu.BitnetModel(cfg, w)
+    try:
+        for k in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "seq_len", "wht_dim",
+                  "wht_q", "wht_hidden", "g_q", "g_o", "g_13", "g_2"):
+            assert mf.cfg[k] == cfg[k], k
+        assert mf.weight_bytes() == mm.weight_bytes()
+        prompt = [3, 141, 59, 26]
+        out = []
+        for m in (mf, mm):
+            m.reset(prompt)
+            m.prefill(3)
+            m.steps(9, graph=True)
+            out.append((m.tokens(13), m.logits()))
+        assert np.array_equal(out[0][0], out[1][0])
+        assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    finally:
+        mf.close()
+        mm.close()
+
+
+def test_svlm_rejects(gpu, tmp_path):
+    cfg, w = tiny()
+    path = tmp_path / "m.svlm"
+    synth.write_svlm(str(path), cfg, w, 32)
+    raw = bytearray(path.read_bytes())
+    bad = tmp_path / "bad.svlm"
+    raw[48 + 12 * 4] = 1                      # qtype INT8: not a BitNet file
+    bad.write_bytes(bytes(raw))
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_svlm(str(bad))
+    bad.write_bytes(path.read_bytes()[:1000])  # truncated
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_svlm(str(bad))
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_svlm(str(tmp_path / "missing.svlm"))

@@ -1,0 +1,74 @@
+"""The SVLM model-file layout (bitllm.c_amd/synth.py write_svlm) against the reference's own reader.
+
+A file written by write_svlm and read by the reference itself (tinyllm_init + tinyllm_load_quantized_model,
+src/eif_tinyllm.c:2442-2556, configuration words as src/eif_llm.c:321-342, built from the reference sources
+into oracle/_ref/libref_scalar.so) decodes bit for bit as the reference's decode of the same arrays held in
+memory: the file carries the reference's layout. Grouped (bound 32) and per-row (bound 0, rotated) files. The
+GPU reader of the same files is checked in tests/test_gpu_decode.py.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+import synth  # noqa: E402
+import oracle_api  # noqa: E402
+import make_golden  # noqa: E402
+
+REF = os.path.join(ROOT, "oracle", "_ref", "libref_scalar.so")
+
+
+def tiny(group):
+    cfg = make_golden.decode_config()
+    cfg["rope_theta"] = 100000.0           # what an SVLM file configures
+    for k in ("g_q", "g_o", "g_13", "g_2"):
+        cfg[k] = group
+    return cfg, synth.bitnet_model((11, group), cfg)
+
+
+@pytest.mark.parametrize("bound,group", [(32, 32), (0, 0)])
+def test_svlm_file_read_by_reference(tmp_path, bound, group):
+    if not os.path.exists(REF):
+        pytest.skip("oracle/_ref/libref_scalar.so not built (no reference tree)")
+    ref = oracle_api.load_ref_tinyllm(REF)
+    cfg, w = tiny(group)
+    path = str(tmp_path / "model.svlm")
+    synth.write_svlm(path, cfg, w, bound)
+    hf = ref.ref_svlm_create(os.fsencode(path))
+    assert hf
+    c, ws = oracle_api.bitnet_structs(cfg, w)
+    hm = ref.ref_bitnet_create(C.byref(c), C.byref(ws), bound if bound else 1 << 30)
+    try:
+        tok = 17
+        for pos in range(12):
+            a = np.ctypeslib.as_array(ref.ref_bitnet_forward(hf, tok, pos), shape=(cfg["vocab"],)).copy()
+            b = np.ctypeslib.as_array(ref.ref_bitnet_forward(hm, tok, pos), shape=(cfg["vocab"],)).copy()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), pos
+            tok = int(np.argmax(a))
+    finally:
+        ref.ref_bitnet_destroy(hf)
+        ref.ref_bitnet_destroy(hm)
+
+
+def test_svlm_writer_layout(tmp_path):
+    """Header words and region sizes as the reader takes them."""
+    cfg, w = tiny(32)
+    path = str(tmp_path / "m.svlm")
+    synth.write_svlm(path, cfg, w, 32)
+    raw = open(path, "rb").read()
+    hdr = np.frombuffer(raw[:48], np.uint32)
+    ci = np.frombuffer(raw[48:176], np.int32)
+    assert hdr[0] == 0x53564C4D and ci[12] == 3 and ci[14] == 32 and ci[15] == 1
+    d, h, L, V = cfg["dim"], cfg["hidden"], cfg["n_layers"], cfg["vocab"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    wbytes = 2 * V * d + L * (qd * d // 4 + 2 * kvd * d // 4 + d * qd // 4 + 2 * h * d // 4 + d * h // 4)
+    assert hdr[7] == wbytes
+    sc = 2 * V + L * (qd * d + 2 * kvd * d + d * qd + 2 * h * d + d * h) // 32 + d + qd + h
+    assert hdr[8] == 4 * sc
+    assert hdr[9] == 4 * (2 * L * d + d + L * (qd + h))
+    assert hdr[5] + hdr[9] == len(raw)
