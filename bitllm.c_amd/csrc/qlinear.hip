@@ -216,6 +216,10 @@ __global__ __launch_bounds__(kGemmThreads) void qgemm_kernel(QArgs a)
             }
         }
     };
+    // The MFMA sums carry the weight codes' 2^SHIFT; the combine takes them unshifted against the group scale
+    // times 2^-SHIFT: fmaf((float)sum, s * 2^-SHIFT, F) == fmaf((float)(sum >> SHIFT), s, F) bit for bit, since both
+    // products are exact (|sum| < 2^24 and a power-of-two factor is exact for a normal scale).
+    constexpr float kUnshift = 1.0f / (float)(1 << GE::SHIFT);
     auto store_step = [&](int b, const v4i (&r)[PPT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
@@ -251,14 +255,15 @@ __global__ __launch_bounds__(kGemmThreads) void qgemm_kernel(QArgs a)
                     if constexpr (GROUPED) {
                         const int gi = 2 * st + grp;
                         if (gi < a.G) {
+                            const float cu = c[grp] * kUnshift;
 #pragma unroll
                             for (int v = 0; v < 4; ++v) {
-                                const int g_acc = cc[v] >> GE::SHIFT;
                                 if constexpr (ACC) {
                                     const int tok = m0 + 16 * tt + 4 * s + v;
-                                    if (row_ok && tok < a.M) a.acc[((size_t)tok * a.N + row) * a.G + gi] = g_acc;
+                                    if (row_ok && tok < a.M)
+                                        a.acc[((size_t)tok * a.N + row) * a.G + gi] = cc[v] >> GE::SHIFT;
                                 } else {
-                                    F[tt][v] = fmaf((float)g_acc, c[grp], F[tt][v]);
+                                    F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
                                 }
                             }
                         }
@@ -941,6 +946,7 @@ namespace {
 int g_gemm_min_tokens = 16;
 int g_gemv_ksplit = 0;   // waves per row tile of the GEMV, 0 = pick_ks_gemv()
 int g_gemv_rt = 0;       // row tiles per workgroup of the GEMV, 0 = chosen from the shape
+int g_gemv_prep_cols = 0;   // fewest columns per thread of the fused prep (4, 8, 16), 0 = chosen from the shape
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
 
@@ -1128,7 +1134,7 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
         // E columns per thread: the fewest that let at most 16 waves cover the padded row (short per-thread
         // chains), and a WHT block within one wave.
         for (int e = 4; e <= 16; e *= 2) {
-            if (64 * e < p.block) continue;
+            if (64 * e < p.block || e < g_gemv_prep_cols) continue;
             int k = ks;
             while (k < maxks && (64 * rt * k * e < kpad || !scales_fit(k))) ++k;
             if (64 * rt * k * e < kpad || !scales_fit(k)) continue;
@@ -1447,6 +1453,13 @@ int eif_hip_set_gemm_split(int k)
 {
     int old = g_gemm_split;
     if (k >= 0 && k <= 16) g_gemm_split = k;
+    return old;
+}
+
+int eif_hip_set_gemv_prep_cols(int e)
+{
+    const int old = g_gemv_prep_cols;
+    if (e == 0 || e == 4 || e == 8 || e == 16) g_gemv_prep_cols = e;
     return old;
 }
 

@@ -155,6 +155,12 @@ int eif_hip_set_gemv_ksplit(int k);
  * previous setting. A tuning knob: results do not depend on it.                                          */
 int eif_hip_set_gemv_row_tiles(int rt);
 
+/* Fewest columns per thread of the prep fused into the GEMV (4, 8 or 16; 0 = chosen from the shape, the
+ * default): more columns, fewer waves per workgroup. Returns the previous setting. A tuning knob: results do
+ * not depend on it (with an RMSNorm pre-op, as for the other shape knobs, its sum of squares is added in
+ * another order).                                                                                       */
+int eif_hip_set_gemv_prep_cols(int e);
+
 /* Splits along K of the GEMM (1..16; 0 = chosen from the shape, the default); returns the previous setting.
  * A split GEMM adds the per-split FP32 partials of grouped ternary in split order (deterministic, within
  * 1e-5 of the oracle; unsplit launches match it bit for bit); integer sums do not depend on it. Splits use a

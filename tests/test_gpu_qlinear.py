@@ -92,7 +92,8 @@ def test_ternary_grouped(gpu, oracle, N, K, g, M, path):
 
 @pytest.mark.parametrize("N,K,g", [(3072, 2560, 128), (1024, 6912, 96), (200, 2560, 128)])
 def test_gemv_shape_knobs(gpu, oracle, N, K, g):
-    """Row tiles per workgroup and waves per tile change the launch, never the result (y, acc, fused y)."""
+    """Row tiles per workgroup, waves per tile and prep columns per thread change the launch, never the result
+    (y, acc, fused y)."""
     import torch
     dev = torch.device("cuda:0")
     lib = gpu.load()
@@ -111,22 +112,25 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
             oacc = np.zeros((M, N, ng), np.int32)
             oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
             ref = None
-            for rt, ks in [(0, 0), (1, 0), (4, 0), (1, 2), (4, 2), (1, 16), (4, 4), (1, 1)]:
+            for rt, ks, e in [(0, 0, 0), (1, 0, 0), (4, 0, 0), (1, 2, 0), (4, 2, 0), (1, 16, 0), (4, 4, 0), (1, 1, 0),
+                              (0, 0, 8), (1, 0, 16), (4, 0, 8), (1, 4, 16)]:
                 lib.eif_hip_set_gemv_row_tiles(rt)
                 lib.eif_hip_set_gemv_ksplit(ks)
+                lib.eif_hip_set_gemv_prep_cols(e)
                 y = run_linear(gpu, qw, xq_d, xs_d, M, GEMV)
-                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (M, rt, ks)
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (M, rt, ks, e)
                 acc = run_acc(gpu, qw, xq_d, M, (M, N, ng), GEMV)
-                assert np.array_equal(acc, oacc), (M, rt, ks)
+                assert np.array_equal(acc, oacc), (M, rt, ks, e)
                 yf = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
                 qw.linear_f32(xd, yf, 128, norm)
                 yf = yf.cpu().numpy()
                 if ref is None:
                     ref = yf
-                assert np.array_equal(yf.view(np.uint32), ref.view(np.uint32)), (M, rt, ks)
+                assert np.array_equal(yf.view(np.uint32), ref.view(np.uint32)), (M, rt, ks, e)
     finally:
         lib.eif_hip_set_gemv_row_tiles(0)
         lib.eif_hip_set_gemv_ksplit(0)
+        lib.eif_hip_set_gemv_prep_cols(0)
         qw.close()
 
 
