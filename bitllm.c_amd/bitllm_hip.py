@@ -48,6 +48,7 @@ _SIGS = {
     "eif_hip_qlinear_prep": (_i, [_vp, C.POINTER(PrepSpec), _vp, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_prep_acc": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _vp]),
     "eif_hip_prep_spec_rows": (_i, [C.POINTER(PrepSpec), _i, _vp, _i, _vp, _i, _vp]),
+    "eif_hip_quant_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
     "eif_hip_bitnet_create": (_i, [C.POINTER(_vp), C.POINTER(BitnetConfig)]),
     "eif_hip_bitnet_set_layer": (_i, [_vp, _i, C.POINTER(BitnetLayer)]),
     "eif_hip_bitnet_set_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
@@ -219,6 +220,13 @@ def prep_spec_rows(spec, K, xq, xs, M, stream=None):
     """The prep of a spec on its own: M rows of K columns -> xq [M, ldq] int8 + xs [M] (device tensors)."""
     check(load().eif_hip_prep_spec_rows(C.byref(spec), K, ptr(xq), xq.stride(0), ptr(xs), M, stream_ptr(stream)),
           "eif_hip_prep_spec_rows")
+
+
+def quant_rows(x, bits, dst, scales, stream=None):
+    """FP32 rows x [rows, cols] (device) -> INT8 / INT4 row-scaled codes dst and scales (device)."""
+    rows, cols = x.shape
+    check(load().eif_hip_quant_rows(ptr(x), x.stride(0), rows, cols, bits, ptr(dst), ptr(scales), stream_ptr(stream)),
+          "eif_hip_quant_rows")
 
 
 class BitnetModel:

@@ -22,6 +22,8 @@
  *   orc_matmul_bitnet_int8              bit-exact vs compiled reference
  *   FP32-activation GEMVs, GEMM, softmax  float64 references with the reference tests' bounds
  *                                       (test_int8_gemv.c:10-44, test_q35_int4.c:24-33, test_gemm.c:9-34)
+ *   orc_quant_rows                      numpy float32 restatement, nibble order of test_q35_int4.c:20,
+ *                                       closed-form bounds (|x - q s| <= s / 2, the largest |x| at +-qmax)
  */
 #include <math.h>
 #include <stdint.h>
@@ -554,4 +556,41 @@ int orc_num_threads(void)
 #else
     return 1;
 #endif
+}
+
+
+/* Row-wise symmetric quantisation of FP32 rows to INT8 or INT4 with one scale per row: the reference's GGUF import,
+ * quant_rows (src/eif_qwen35_gguf.c:225-258) after its dequant_row. amax = max(1e-8, max |x|), s = amax / qmax
+ * (qmax 127 or 7), inv = 1 / s, q = nearbyintf(x * inv) clamped to [-128, 127] or [-8, 7]; INT4 packs columns
+ * (2i, 2i+1) into byte i as ((a + 8) << 4) | (b + 8), a zero column padding an odd count. */
+void orc_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8_t *dst, float *scales)
+{
+    const size_t rb = bits == 8 ? (size_t)cols : (size_t)(cols + 1) / 2;
+    const float qmax = bits == 8 ? 127.0f : 7.0f;
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * ldx;
+        float amax = 1e-8f;
+        for (int c = 0; c < cols; c++) {
+            const float a = fabsf(xr[c]);
+            if (a > amax) amax = a;
+        }
+        const float sc = amax / qmax, inv = 1.0f / sc;
+        scales[r] = sc;
+        uint8_t *o = dst + (size_t)r * rb;
+        if (bits == 8) {
+            for (int c = 0; c < cols; c++) {
+                int q = (int)nearbyintf(xr[c] * inv);
+                q = q > 127 ? 127 : (q < -128 ? -128 : q);
+                ((int8_t *)o)[c] = (int8_t)q;
+            }
+        } else {
+            for (int c = 0; c < cols; c += 2) {
+                int a = (int)nearbyintf(xr[c] * inv);
+                int b = c + 1 < cols ? (int)nearbyintf(xr[c + 1] * inv) : 0;
+                a = a > 7 ? 7 : (a < -8 ? -8 : a);
+                b = b > 7 ? 7 : (b < -8 ? -8 : b);
+                o[c / 2] = (uint8_t)(((a + 8) << 4) | ((b + 8) & 0x0F));
+            }
+        }
+    }
 }

@@ -37,6 +37,7 @@ size_t orc_interleave_weights_4rows(const uint8_t *src, uint8_t *dst, int rows, 
 void orc_matmul_bitnet_tmac_interleaved_f32(const uint8_t *il, const float *scales, const float *x, const float *bias, float *y, int rows, int cols);
 void orc_int8_rowscale_f32(float *y, const int8_t *w, const float *x, int cols, int rows, const float *scales);
 void orc_int4_gemv_f32(float *out, const uint8_t *w, const float *sc, const float *x, int rows, int cols);
+void orc_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8_t *dst, float *scales);
 void orc_gemm_f32_nt_ld(const float *A, int lda, const float *W, int ldw, const float *bias, float *C, int ldc, int M, int N, int K, int act, int accumulate);
 void orc_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale);
 int orc_num_threads(void);

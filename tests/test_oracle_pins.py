@@ -334,3 +334,53 @@ def test_gemm_softmax_vs_double(oracle):
     ref_sm = e / e.sum(1, keepdims=True)
     assert np.max(np.abs(S[:, :7] - ref_sm) / (ref_sm + 1e-30)) < 1e-5
     assert np.array_equal(S[:, 7:], S0[:, 7:])
+
+
+def _quant_rows_np(x, bits):
+    """The reference's quant_rows (src/eif_qwen35_gguf.c:225-258) in numpy float32 arithmetic."""
+    x = np.asarray(x, np.float32)
+    rows, cols = x.shape
+    qmax = np.float32(127.0 if bits == 8 else 7.0)
+    lo, hi = (-128, 127) if bits == 8 else (-8, 7)
+    amax = np.maximum(np.abs(x).max(axis=1), np.float32(1e-8)).astype(np.float32)
+    sc = (amax / qmax).astype(np.float32)
+    inv = (np.float32(1.0) / sc).astype(np.float32)
+    q = np.clip(np.rint((x * inv[:, None]).astype(np.float32)), lo, hi).astype(np.int32)
+    if bits == 8:
+        return q.astype(np.int8).view(np.uint8), sc
+    if cols % 2:
+        q = np.concatenate([q, np.zeros((rows, 1), np.int32)], axis=1)
+    packed = (((q[:, 0::2] + 8) << 4) | ((q[:, 1::2] + 8) & 0xF)).astype(np.uint8)
+    return packed, sc
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("rows,cols", [(7, 64), (5, 33), (3, 1), (2, 1024)])
+def test_quant_rows(oracle, bits, rows, cols):
+    r = np.random.default_rng(70 + bits + cols)
+    x = (r.standard_normal((rows, cols)) * 10.0 ** r.integers(-3, 3, (rows, 1))).astype(np.float32)
+    x[0, : min(4, cols)] = 0.0
+    if rows > 2:
+        x[2] = 0.0                                        # all-zero row: the 1e-8 floor, codes 0
+    if rows > 1 and cols > 3:
+        amax = np.abs(x[1]).max()
+        qmax = 127.0 if bits == 8 else 7.0
+        x[1, 1] = np.float32(amax / qmax * 2.5)           # an exact tie at 2.5 -> 2 (half to even)
+    rb = cols if bits == 8 else (cols + 1) // 2
+    dst = np.zeros((rows, rb), np.uint8)
+    sc = np.zeros(rows, np.float32)
+    oracle.orc_quant_rows(P(x), cols, rows, cols, bits, P(dst), P(sc))
+    want, wsc = _quant_rows_np(x, bits)
+    assert np.array_equal(dst, want) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+    # closed forms: decode (int4 nibble order of tests/test_q35_int4.c:20: even column in the high nibble)
+    if bits == 8:
+        q = dst.view(np.int8).astype(np.float64)
+    else:
+        q = np.stack([(dst >> 4).astype(np.int32) - 8, (dst & 0xF).astype(np.int32) - 8], axis=2).reshape(rows, -1)[:, :cols]
+    s64 = sc.astype(np.float64)[:, None]
+    err = np.abs(x.astype(np.float64) - q * s64)
+    assert (err <= s64 * (0.5 + 1e-5)).all()               # within half a step (no value is clamped)
+    big = np.abs(x).argmax(axis=1)
+    for i in range(rows):
+        if np.abs(x[i]).max() > 0:
+            assert abs(q[i, big[i]]) == (127 if bits == 8 else 7)
