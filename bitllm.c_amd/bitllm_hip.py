@@ -49,6 +49,8 @@ _SIGS = {
     "eif_hip_qlinear_prep_acc": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _vp]),
     "eif_hip_prep_spec_rows": (_i, [C.POINTER(PrepSpec), _i, _vp, _i, _vp, _i, _vp]),
     "eif_hip_quant_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),
+    "eif_gguf_ternary_rows": (_i, [_i, _vp, _i, _i, _vp, _vp]),
+    "eif_hip_qweight_from_gguf_ternary": (_i, [_vp, _i, _vp, _i, _i, _vp]),
     "eif_hip_bitnet_create": (_i, [C.POINTER(_vp), C.POINTER(BitnetConfig)]),
     "eif_hip_bitnet_set_layer": (_i, [_vp, _i, C.POINTER(BitnetLayer)]),
     "eif_hip_bitnet_set_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
@@ -177,6 +179,17 @@ class QWeight:
         check(load().eif_hip_qweight_info(h, C.byref(r), C.byref(c), C.byref(kp), C.byref(g), C.byref(b)),
               "eif_hip_qweight_info")
         self.kpad, self.bytes = kp.value, b.value
+
+    @classmethod
+    def wrap(cls, h):
+        """A QWeight around a handle made by another constructor of the library (it takes ownership)."""
+        self = cls.__new__(cls)
+        r, c, kp, g, b = C.c_int(), C.c_int(), C.c_int(), C.c_int(), C.c_size_t()
+        check(load().eif_hip_qweight_info(h, C.byref(r), C.byref(c), C.byref(kp), C.byref(g), C.byref(b)),
+              "eif_hip_qweight_info")
+        self.h, self.fmt, self.rows, self.cols, self.group = h, None, r.value, c.value, g.value
+        self.kpad, self.bytes = kp.value, b.value
+        return self
 
     def close(self):
         if self.h:

@@ -24,6 +24,8 @@
  *                                       (test_int8_gemv.c:10-44, test_q35_int4.c:24-33, test_gemm.c:9-34)
  *   orc_quant_rows                      numpy float32 restatement, nibble order of test_q35_int4.c:20,
  *                                       closed-form bounds (|x - q s| <= s / 2, the largest |x| at +-qmax)
+ *   orc_gguf_ternary_rows               numpy restatement: the codes byte for byte, every fp16 scale value
+ *                                       against numpy's binary16, the mean in block order
  */
 #include <math.h>
 #include <stdint.h>
@@ -592,5 +594,59 @@ void orc_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8
                 o[c / 2] = (uint8_t)(((a + 8) << 4) | ((b + 8) & 0x0F));
             }
         }
+    }
+}
+
+
+/* BitNet projection tensors of a GGUF file -> 2-bit ternary rows with one scale per row: the reference's
+ * load_projection_tensor (src/eif_tinyllm.c:3351-3400) for TL1/TL2 (types 34/35: blocks of an fp16 scale and 8
+ * code bytes, copied) and Q8_0 (type 8: blocks of an fp16 scale and 32 int8, coded by sign); scale = the sum of the
+ * block scales in block order over the block count; the fp16 conversion is the reference's (include/eif_gguf.h:
+ * 57-80). A TL row's copy stops at the row's end. */
+static float orc_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)(h & 0x8000)) << 16, exp = (h >> 10) & 0x1F, mant = h & 0x03FF;
+    if (exp == 0) {
+        if (mant == 0) return sign ? -0.0f : 0.0f;
+        while (!(mant & 0x0400)) { mant <<= 1; exp--; }
+        exp++;
+        mant &= ~0x0400u;
+    } else if (exp == 31) {
+        return mant == 0 ? (sign ? -INFINITY : INFINITY) : NAN;
+    }
+    exp = exp + (127 - 15);
+    uint32_t u = sign | (exp << 23) | (mant << 13);
+    float out;
+    memcpy(&out, &u, 4);
+    return out;
+}
+
+void orc_gguf_ternary_rows(int type, const uint8_t *src, int rows, int cols, uint8_t *codes, float *scales)
+{
+    const int blocks = (cols + 31) / 32;
+    const size_t rb = (size_t)(cols + 3) / 4, bb = type == 8 ? 34 : 10;
+    for (int r = 0; r < rows; r++) {
+        const uint8_t *rs = src + (size_t)r * blocks * bb;
+        uint8_t *rd = codes + (size_t)r * rb;
+        memset(rd, 0, rb);
+        float s_sum = 0.0f;
+        for (int b = 0; b < blocks; b++) {
+            const uint8_t *blk = rs + (size_t)b * bb;
+            uint16_t h;
+            memcpy(&h, blk, 2);
+            s_sum += orc_f16_to_f32(h);
+            if (type != 8) {
+                for (int i = 0; i < 8 && (size_t)b * 8 + i < rb; i++) rd[b * 8 + i] = blk[2 + i];
+            } else {
+                const int count = b == blocks - 1 ? cols - b * 32 : 32;
+                for (int i = 0; i < count; i++) {
+                    const int c = b * 32 + i;
+                    const int8_t v = (int8_t)blk[2 + i];
+                    const uint8_t code = v > 0 ? 1 : (v < 0 ? 2 : 0);
+                    rd[c / 4] |= (uint8_t)(code << ((c % 4) * 2));
+                }
+            }
+        }
+        scales[r] = blocks > 0 ? s_sum / blocks : 1.0f;
     }
 }

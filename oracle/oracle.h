@@ -38,6 +38,7 @@ void orc_matmul_bitnet_tmac_interleaved_f32(const uint8_t *il, const float *scal
 void orc_int8_rowscale_f32(float *y, const int8_t *w, const float *x, int cols, int rows, const float *scales);
 void orc_int4_gemv_f32(float *out, const uint8_t *w, const float *sc, const float *x, int rows, int cols);
 void orc_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8_t *dst, float *scales);
+void orc_gguf_ternary_rows(int type, const uint8_t *src, int rows, int cols, uint8_t *codes, float *scales);
 void orc_gemm_f32_nt_ld(const float *A, int lda, const float *W, int ldw, const float *bias, float *C, int ldc, int M, int N, int K, int act, int accumulate);
 void orc_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale);
 int orc_num_threads(void);

@@ -39,6 +39,7 @@ ORACLE_SIGS = {
     "orc_num_threads": (_i, []),
     "orc_round_f16": (_f, [_f]),
     "orc_quant_rows": (None, [_vp, _i, _i, _i, _i, _vp, _vp]),
+    "orc_gguf_ternary_rows": (None, [_i, _vp, _i, _i, _vp, _vp]),
     "orc_bitnet_forward": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }
 

@@ -355,3 +355,34 @@ def test_fused_prep_linear(gpu, oracle, fmt, N, K, g, M, block, signed):
         oacc = xq[:, :K].astype(np.int64) @ synth.unpack_int4(w, K).astype(np.int64).T
     assert np.array_equal(acc.cpu().numpy(), oacc)
     qw.close()
+
+
+@pytest.mark.parametrize("kind", [34, 35, 8])
+def test_gguf_ternary_weight(gpu, oracle, kind):
+    """GGUF TL1/TL2/Q8_0 projection rows -> 2-bit rows + row scales (eif_gguf_ternary_rows) == the oracle byte for
+    byte; the resident weight (eif_hip_qweight_from_gguf_ternary) gives the exact integer sums of those codes."""
+    import ctypes as C
+    import torch
+    from test_oracle_pins import _gguf_blocks
+    N, K = 300, 2560
+    r = np.random.default_rng(97 + kind)
+    raw, _ = _gguf_blocks(r, kind, N, K)
+    rb = K // 4
+    codes = np.zeros((N, rb), np.uint8)
+    sc = np.zeros(N, np.float32)
+    assert gpu.load().eif_gguf_ternary_rows(kind, P(raw), N, K, P(codes), P(sc)) == 0
+    oc = np.zeros((N, rb), np.uint8)
+    osc = np.zeros(N, np.float32)
+    oracle.orc_gguf_ternary_rows(kind, P(raw), N, K, P(oc), P(osc))
+    assert np.array_equal(codes, oc) and np.array_equal(sc.view(np.uint32), osc.view(np.uint32))
+    h = C.c_void_p()
+    gpu.check(gpu.load().eif_hip_qweight_from_gguf_ternary(C.byref(h), kind, P(raw), N, K, None),
+              "eif_hip_qweight_from_gguf_ternary")
+    qw = gpu.QWeight.wrap(h)
+    assert (qw.rows, qw.cols, qw.group) == (N, K, 0)
+    x = synth.activations((98, 3), 3, K)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    acc = run_acc(gpu, qw, xq_d, 3, (3, N), GEMV)
+    want = xq[:, :K].astype(np.int64) @ synth.unpack_ternary(oc, K).astype(np.int64).T
+    assert np.array_equal(acc, want)
+    qw.close()

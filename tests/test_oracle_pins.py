@@ -384,3 +384,62 @@ def test_quant_rows(oracle, bits, rows, cols):
     for i in range(rows):
         if np.abs(x[i]).max() > 0:
             assert abs(q[i, big[i]]) == (127 if bits == 8 else 7)
+
+
+def _gguf_blocks(r, kind, rows, cols):
+    """Synthetic GGUF tensor rows: 32-column blocks of a finite fp16 scale and TL codes (10 bytes) or Q8_0 values
+    (34 bytes)."""
+    blocks = (cols + 31) // 32
+    h = r.uniform(0.01, 2.0, (rows, blocks)).astype(np.float16).view(np.uint16)
+    if kind == 8:
+        body = r.integers(-128, 128, (rows, blocks, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+    else:
+        body = r.integers(0, 256, (rows, blocks, 8), dtype=np.int16).astype(np.uint8)
+    raw = np.concatenate([h.view(np.uint8).reshape(rows, blocks, 2), body], axis=2)
+    return np.ascontiguousarray(raw), h
+
+
+@pytest.mark.parametrize("kind", [34, 35, 8])
+@pytest.mark.parametrize("rows,cols", [(5, 256), (3, 100), (2, 32)])
+def test_gguf_ternary_rows(oracle, kind, rows, cols):
+    r = np.random.default_rng(95 + kind + cols)
+    raw, h = _gguf_blocks(r, kind, rows, cols)
+    rb = (cols + 3) // 4
+    codes = np.zeros((rows, rb), np.uint8)
+    sc = np.zeros(rows, np.float32)
+    oracle.orc_gguf_ternary_rows(kind, P(raw), rows, cols, P(codes), P(sc))
+    blocks = raw.shape[1]
+    want_sc = np.zeros(rows, np.float32)
+    for i in range(rows):
+        s = np.float32(0.0)
+        for b in range(blocks):
+            s = np.float32(s + h[i, b].view(np.float16).astype(np.float32))
+        want_sc[i] = np.float32(s / np.float32(blocks))
+    assert np.array_equal(sc.view(np.uint32), want_sc.view(np.uint32))
+    if kind == 8:
+        q = raw[:, :, 2:].view(np.int8).reshape(rows, -1)[:, :cols]
+        c = np.where(q > 0, 1, np.where(q < 0, 2, 0)).astype(np.uint8)
+        c = np.concatenate([c, np.zeros((rows, 4 * rb - cols), np.uint8)], axis=1).reshape(rows, rb, 4)
+        want = c[:, :, 0] | (c[:, :, 1] << 2) | (c[:, :, 2] << 4) | (c[:, :, 3] << 6)
+    else:
+        want = raw[:, :, 2:].reshape(rows, -1)[:, :rb]
+    assert np.array_equal(codes, want)
+    # the decoded codes of Q8_0 rows are the values' signs
+    if kind == 8:
+        dec = synth.unpack_ternary(codes, cols)
+        assert np.array_equal(dec, np.sign(q))
+
+
+def test_gguf_fp16_scales_every_value(oracle):
+    # one 32-column TL block per row, every fp16 bit pattern as its scale: the row scale is that value exactly
+    rows = 65536
+    raw = np.zeros((rows, 1, 10), np.uint8)
+    raw[:, 0, :2] = np.arange(rows, dtype=np.uint32).astype(np.uint16).view(np.uint8).reshape(rows, 2)
+    codes = np.zeros((rows, 8), np.uint8)
+    sc = np.zeros(rows, np.float32)
+    oracle.orc_gguf_ternary_rows(34, P(raw), rows, 32, P(codes), P(sc))
+    want = np.arange(rows, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    want = (np.float32(0.0) + want) / np.float32(1.0)   # the mean's sum starts at +0 (so -0 becomes +0)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(sc), nan)
+    assert np.array_equal(sc[~nan].view(np.uint32), want[~nan].view(np.uint32))
