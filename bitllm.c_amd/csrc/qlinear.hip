@@ -174,8 +174,14 @@ struct QArgs {
 // row-scaled: one int32 sum over K.
 constexpr int kGemmThreads = 256;
 
+// Waves per SIMD the register budget is cut for: four for the g128 ternary and INT formats (their MFMA sums
+// would otherwise sit in accumulation registers, at three waves), the compiler's choice for the rest.
+template <int FMT, int UD>
+constexpr int gemm_waves() { return FMT == kTern && UD == 3 ? 1 : 4; }
+
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
-__global__ __launch_bounds__(kGemmThreads) void qgemm_kernel(QArgs a)
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<FMT, UD>())))
+void qgemm_kernel(QArgs a)
 {
     using GE = Geo<FMT, UD>;
     constexpr int NW = GE::SB / 4;
@@ -197,22 +203,29 @@ __global__ __launch_bounds__(kGemmThreads) void qgemm_kernel(QArgs a)
     v4i ra[2][PPT];   // a clang vector type: an array of HIP's int4 structs would live in scratch
     uint32_t wb[2][NW];
     float sc[2][2];
-    const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
+    // 32-bit byte offsets from the uniform bases (the launcher keeps the batch's int8 rows and the weights below
+    // 4 GiB): the loads take the scalar-base form and a step adds st * SC (st * 4 * SB) to them.
+    const uint32_t wo = (uint32_t)row * (uint32_t)a.wld + (uint32_t)(s * GE::SB);
+    uint32_t xo[PPT];   // the thread's activation pieces at step 0, token rows clamped into the batch
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+        const int pc = threadIdx.x + i * kGemmThreads;
+        const int t = pc / PR, q = pc - t * PR;
+        const int tok = m0 + (t < TM ? t : TM - 1);
+        xo[i] = (uint32_t)(tok < a.M ? tok : a.M - 1) * (uint32_t)a.ldq + (uint32_t)(16 * q);
+    }
+    const uint32_t so = GROUPED ? (uint32_t)row_c * (uint32_t)a.G : 0u;
     auto load_step = [&](int st, v4i (&r)[PPT], uint32_t (&w)[NW], float (&c)[2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int pc = threadIdx.x + i * kGemmThreads;
-            const int t = pc / PR, q = pc - t * PR;
-            const int tok = m0 + (t < TM ? t : TM - 1);
-            r[i] = *reinterpret_cast<const v4i *>(a.xq + (size_t)(tok < a.M ? tok : a.M - 1) * a.ldq +
-                                                    (size_t)st * GE::SC + 16 * q);
-        }
-        load_words<NW>(wp + (size_t)st * 4 * GE::SB, w);
+        for (int i = 0; i < PPT; ++i) r[i] = *reinterpret_cast<const v4i *>(a.xq + (xo[i] + (uint32_t)(st * GE::SC)));
+        load_words<NW>(a.W + (wo + (uint32_t)(st * 4 * GE::SB)), w);
         if constexpr (GROUPED) {
+            // a group past the row's last one (a ragged final step) gets scale 0 and adds nothing: F + 0 * x == F
 #pragma unroll
             for (int grp = 0; grp < 2; ++grp) {
                 const int gi = 2 * st + grp;
-                c[grp] = a.scales[(size_t)row_c * a.G + (gi < a.G ? gi : a.G - 1)];
+                const float v = a.scales[so + (uint32_t)(gi < a.G ? gi : a.G - 1)];
+                c[grp] = gi < a.G ? v : 0.0f;
             }
         }
     };
@@ -254,18 +267,19 @@ __global__ __launch_bounds__(kGemmThreads) void qgemm_kernel(QArgs a)
                     v4i cc = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C[tt]);
                     if constexpr (GROUPED) {
                         const int gi = 2 * st + grp;
-                        if (gi < a.G) {
-                            const float cu = c[grp] * kUnshift;
+                        if constexpr (ACC) {
+                            if (gi < a.G) {
 #pragma unroll
-                            for (int v = 0; v < 4; ++v) {
-                                if constexpr (ACC) {
+                                for (int v = 0; v < 4; ++v) {
                                     const int tok = m0 + 16 * tt + 4 * s + v;
                                     if (row_ok && tok < a.M)
                                         a.acc[((size_t)tok * a.N + row) * a.G + gi] = cc[v] >> GE::SHIFT;
-                                } else {
-                                    F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
                                 }
                             }
+                        } else {
+                            const float cu = c[grp] * kUnshift;
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
                         }
                     } else {
                         C[tt] = cc;
@@ -1004,6 +1018,8 @@ int pick_split(QArgs &a, int tiles, hipStream_t st)
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
 int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
 {
+    // the kernel addresses the batch rows and the weights with 32-bit offsets
+    if ((size_t)a.M * a.ldq >= ((size_t)1 << 32) || (size_t)rows_pad * a.wld >= ((size_t)1 << 32)) return EIF_HIP_E_LIMIT;
     const int tm = eif_ceil_div(a.M, 16 * TT), tiles = rows_pad / 64 * tm;
     const int ks = pick_split<ACC>(a, tiles, st);
     dim3 grid(rows_pad / 64, tm, ks);
