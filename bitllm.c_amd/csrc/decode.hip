@@ -6,7 +6,8 @@
 // the GEMV with per-tile maxima (the argmax's first stage), and kernels of its own:
 //   attn_split_kernel   RoPE of q and k (:396-405, :476-507; angles from a table made once), fp16 KV append,
 //                       softmax attention (:555-650) of each query head over one chunk of the positions per
-//                       workgroup, one pass over the chunk; the head's last chunk to finish combines the shares
+//                       workgroup, one pass over the chunk, leaving the chunk's share; the O projection's
+//                       fused prep combines a head's shares (qlinear_prep_shares)
 //   sample_kernel       greedy argmax over the head's tile maxima (first maximum, src/eif_tinyllm.c:1519-1530)
 //                       or the next prompt token, stored in the sequence; position + 1; x = the next token's
 //                       INT8 embedding row * its scale (src/eif_tinyllm.c:902-916)
@@ -77,11 +78,13 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
 // the row groups are then combined: M = max_r m_r, out = sum_r e^(m_r - M) o_r / sum_r e^(m_r - M) l_r.
 // This is the softmax of the scores followed by the weighted sum of the values, with the sums taken in another
 // order.
-// PARTIAL: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized, out[HD] = M, out[HD + 1] = sum_r e^(m_r - M) l_r
-// (a chunk's share; the head's last chunk to finish combines the shares).
-template <int HD, int NT, bool PARTIAL = false>
+// PARTIAL: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized, out_ml[0] = M, out_ml[kAttnShares] =
+// sum_r e^(m_r - M) l_r (a chunk's share, combined by the next linear's prep).
+// pro(): called once the first batch's loads are issued, before q_l is read (the caller fills q_l, k_x and v_x
+// there and synchronizes the workgroup), so those loads overlap the caller's set-up.
+template <int HD, int NT, bool PARTIAL, class Pro>
 EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int n_cache, const float *k_x,
-                    const float *v_x, float inv_sqrt_hd, float *out)
+                    const float *v_x, float inv_sqrt_hd, float *out, float *out_ml, Pro &&pro)
 {
     constexpr int DPR = HD / 8, RG = NT / DPR, UNR = 8;
     constexpr int PARTS = NT / HD;   // threads per output dimension in the combine
@@ -91,6 +94,18 @@ EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int 
     __shared__ float po_l[PARTS][HD], pl_l[PARTS];
     const int t = threadIdx.x;
     const int sub = t % DPR, r0 = t / DPR;
+    uint4 kr[UNR], vr[UNR];
+    auto load_batch = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int tt = base + u * RG + r0;
+            const size_t off = (size_t)(tt < n_cache ? tt : 0) * HD + 8 * sub;
+            kr[u] = *reinterpret_cast<const uint4 *>(kcg + off);
+            vr[u] = *reinterpret_cast<const uint4 *>(vcg + off);
+        }
+    };
+    load_batch(0);
+    pro();
     float qv[8], o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) qv[i] = q_l[8 * sub + i], o[i] = 0.0f;
@@ -104,14 +119,7 @@ EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int 
         return d * inv_sqrt_hd;
     };
     for (int base = 0; base < n_cache; base += RG * UNR) {
-        uint4 kr[UNR], vr[UNR];
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int tt = base + u * RG + r0;
-            const size_t off = (size_t)(tt < n_cache ? tt : 0) * HD + 8 * sub;
-            kr[u] = *reinterpret_cast<const uint4 *>(kcg + off);
-            vr[u] = *reinterpret_cast<const uint4 *>(vcg + off);
-        }
+        if (base > 0) load_batch(base);
         float sv[UNR];
         float bm = -INFINITY;
 #pragma unroll
@@ -185,91 +193,72 @@ EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int 
         for (int q = 1; q < PARTS; ++q) os += po_l[q][t], ls += pl_l[q];
         if constexpr (PARTIAL) {
             out[t] = os;
-            if (t == 0) out[HD] = mx, out[HD + 1] = ls;
+            if (t == 0) out_ml[0] = mx, out_ml[kAttnShares] = ls;
         } else {
             out[t] = os / ls;
         }
     }
 }
 
-// Decode, split over the positions: workgroup (h, s) takes query head h (kv head g = h / kv_mul) over the cache
-// rows of chunk s, [s CH, min((s + 1) CH, pos)), CH = the rows one batch of attend<HD, 256> covers; chunk
-// pos / CH also takes row pos itself. Chunks past pos exit. Every workgroup rotates q_h (RoPE from the table);
-// the workgroup of the last chunk also rotates k_g, rounds k and v to fp16 and, for the first query head of
-// the kv head, appends them to the cache. Each writes its share (attend's partial form) to
-// part[(h * n_chunks + s) * (HD + 2)], then counts itself in cnt[h] (agent-scope release before the count);
-// the workgroup that completes the count (acquire after it) combines the head's shares,
-//   M = max_s M_s, out = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s,
-// and sets cnt[h] back to 0 for the next step. No workgroup waits on another.
+// Decode, split over the positions: workgroup (h, s) takes query head h (kv head g = h / kv_mul) over the
+// positions of chunk s, [s CH, (s + 1) CH), CH = the fewest whole UNITs (the rows one batch of attend<HD, 256>
+// covers) that cover positions 0 .. pos in kAttnShares chunks; cache rows below pos, and row pos itself in the
+// chunk holding it. A chunk past pos sets its share's maximum to -inf and exits. Every workgroup rotates q_h (RoPE
+// from the table); the workgroup of the chunk holding pos also rotates k_g, rounds k and v to fp16 and, for the
+// first query head of the kv head, appends them to the cache. Each writes its share (attend's partial form):
+// outputs sh_o[h][s][HD], maximum sh_ml[h][s], sum sh_ml[h][kAttnShares + s]; the O projection combines them,
+//   M = max_s M_s, out = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s.
 // Cache layout: [kv_head][seq_len][HD] fp16 per layer.
 template <int HD>
 constexpr int attn_chunk() { return (256 / (HD / 8)) * 8; }
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __half *kc, __half *vc, const int *state,
-                                                         const float2 *rope, float *part, int *cnt, float *out,
-                                                         int n_chunks, int n_heads, int n_kv, int seq_len,
-                                                         float inv_sqrt_hd)
+                                                         const float2 *rope, float *sh_o, float *sh_ml, int n_heads,
+                                                         int n_kv, int seq_len, float inv_sqrt_hd)
 {
-    constexpr int HALF = HD / 2, CH = attn_chunk<HD>();
+    constexpr int HALF = HD / 2, UNIT = attn_chunk<HD>();
     __shared__ float q_l[HD], k_l[HD], v_l[HD];
-    __shared__ int last_l;
     const int h = blockIdx.x, sc = blockIdx.y, kv_mul = n_heads / n_kv, g = h / kv_mul;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
-    const int pos = state[0];
-    const int c0 = sc * CH;
-    if (c0 > pos) return;   // uniform over the workgroup
-    const bool last = pos < c0 + CH;
     const int t = threadIdx.x;
-    if (t < HALF) {
-        const float2 cs = rope[(size_t)pos * HALF + t];
-        const float c = cs.x, sn = cs.y;
-        const float *qh = qkv + h * HD;
-        const float a = qh[t], b = qh[t + HALF];
-        q_l[t] = a * c - b * sn;
-        q_l[t + HALF] = b * c + a * sn;
-        if (last) {
-            const float *kh = qkv + q_dim + g * HD, *vh = qkv + q_dim + kv_dim + g * HD;
-            const float ka = kh[t], kb = kh[t + HALF];
-            const __half k0 = __float2half(ka * c - kb * sn), k1 = __float2half(kb * c + ka * sn);
-            const __half v0 = __float2half(vh[t]), v1 = __float2half(vh[t + HALF]);
-            k_l[t] = __half2float(k0), k_l[t + HALF] = __half2float(k1);
-            v_l[t] = __half2float(v0), v_l[t + HALF] = __half2float(v1);
-            if (h % kv_mul == 0) {
-                __half *kw = kc + ((size_t)g * seq_len + pos) * HD, *vw = vc + ((size_t)g * seq_len + pos) * HD;
-                kw[t] = k0, kw[t + HALF] = k1;
-                vw[t] = v0, vw[t + HALF] = v1;
+    const int pos = state[0];
+    const int ch = UNIT * ((pos + UNIT * kAttnShares) / (UNIT * kAttnShares));
+    const int c0 = sc * ch;
+    float *ml = sh_ml + (size_t)h * 2 * kAttnShares + sc;
+    if (c0 > pos) {   // uniform over the workgroup
+        if (t == 0) ml[0] = -INFINITY;
+        return;
+    }
+    const bool last = pos < c0 + ch;
+    auto rotate = [&]() {
+        if (t < HALF) {
+            const float2 cs = rope[(size_t)pos * HALF + t];
+            const float c = cs.x, sn = cs.y;
+            const float *qh = qkv + h * HD;
+            const float a = qh[t], b = qh[t + HALF];
+            q_l[t] = a * c - b * sn;
+            q_l[t + HALF] = b * c + a * sn;
+            if (last) {
+                const float *kh = qkv + q_dim + g * HD, *vh = qkv + q_dim + kv_dim + g * HD;
+                const float ka = kh[t], kb = kh[t + HALF];
+                const __half k0 = __float2half(ka * c - kb * sn), k1 = __float2half(kb * c + ka * sn);
+                const __half v0 = __float2half(vh[t]), v1 = __float2half(vh[t + HALF]);
+                k_l[t] = __half2float(k0), k_l[t + HALF] = __half2float(k1);
+                v_l[t] = __half2float(v0), v_l[t + HALF] = __half2float(v1);
+                if (h % kv_mul == 0) {
+                    __half *kw = kc + ((size_t)g * seq_len + pos) * HD, *vw = vc + ((size_t)g * seq_len + pos) * HD;
+                    kw[t] = k0, kw[t + HALF] = k1;
+                    vw[t] = v0, vw[t + HALF] = v1;
+                }
             }
         }
-    }
-    __syncthreads();
+        __syncthreads();
+    };
     const size_t base = ((size_t)g * seq_len + c0) * HD;
-    const int rows = (last ? pos : c0 + CH) - c0;
-    float *ph = part + (size_t)h * n_chunks * (HD + 2);
+    const int rows = (last ? pos : c0 + ch) - c0;
     attend<HD, 256, true>(q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr, inv_sqrt_hd,
-                          ph + (size_t)sc * (HD + 2));
-    __syncthreads();   // the workgroup's share is written
-    const int ns = pos / CH + 1;
-    if (t == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        last_l = atomicAdd(&cnt[h], 1) == ns - 1;
-    }
-    __syncthreads();
-    if (!last_l) return;   // uniform
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (t < HD) {
-        float mx = -INFINITY;
-        for (int s2 = 0; s2 < ns; ++s2) mx = fmaxf(mx, ph[(size_t)s2 * (HD + 2) + HD]);
-        float os = 0.0f, ls = 0.0f;
-        for (int s2 = 0; s2 < ns; ++s2) {
-            const float *pp = ph + (size_t)s2 * (HD + 2);
-            const float w = expf(pp[HD] - mx);
-            os = fmaf(w, pp[t], os);
-            ls = fmaf(w, pp[HD + 1], ls);
-        }
-        out[h * HD + t] = os / ls;
-    }
-    if (t == 0) cnt[h] = 0;
+                          sh_o + ((size_t)h * kAttnShares + sc) * HD, ml, rotate);
 }
 
 // Prefill, step 1: token i of a batch at position pos0 + i (one workgroup per token). RoPE of every query head
@@ -310,10 +299,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int
 {
     __shared__ float q_l[HD];
     const int h = blockIdx.x, i = blockIdx.y, g = h / (n_heads / n_kv);
-    if ((int)threadIdx.x < HD) q_l[threadIdx.x] = qkv[(size_t)i * ldqkv + h * HD + threadIdx.x];
-    __syncthreads();
-    attend<HD, 256>(q_l, kc + (size_t)g * seq_len * HD, vc + (size_t)g * seq_len * HD, pos0 + i + 1, nullptr,
-                    nullptr, inv_sqrt_hd, out + (size_t)i * ldo + h * HD);
+    auto load_q = [&]() {
+        if ((int)threadIdx.x < HD) q_l[threadIdx.x] = qkv[(size_t)i * ldqkv + h * HD + threadIdx.x];
+        __syncthreads();
+    };
+    attend<HD, 256, false>(q_l, kc + (size_t)g * seq_len * HD, vc + (size_t)g * seq_len * HD, pos0 + i + 1, nullptr,
+                           nullptr, inv_sqrt_hd, out + (size_t)i * ldo + h * HD, nullptr, load_q);
 }
 
 // Prefill: the embedding rows of prompt tokens pos0 .. pos0 + n - 1 (one workgroup per token).
@@ -420,13 +411,12 @@ struct eif_hip_bitnet {
     float *rms_final = nullptr, *signs_dim = nullptr, *signs_q = nullptr, *signs_hidden = nullptr;
     int8_t *emb = nullptr;
     float *emb_scale = nullptr;
-    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *hb = nullptr, *logits = nullptr;
+    float *x = nullptr, *qkv = nullptr, *hb = nullptr, *logits = nullptr;
     __half *kc = nullptr, *vc = nullptr;
     int *state = nullptr, *prompt = nullptr, *seq = nullptr;
     float2 *rope = nullptr;          // RoPE (cos, sin) [seq_len][head_dim / 2]
-    float *apart = nullptr;          // attention chunk shares [n_heads][n_chunks][head_dim + 2]
-    int *acnt = nullptr;             // per head, the chunks done this step (0 between steps)
-    int n_chunks = 0;
+    float *sh_o = nullptr;           // attention shares: outputs [n_heads][kAttnShares][head_dim]
+    float *sh_ml = nullptr;          // and their maxima, then sums [n_heads][2 kAttnShares]
     int8_t *hq = nullptr;            // the head's prepped input row [head_kpad] and its scale
     float *hs = nullptr;
     float *amax_v = nullptr;         // the head's per-tile maxima [head_tiles]
@@ -462,14 +452,16 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
         auto attn = c.head_dim == 128 ? attn_split_kernel<128>
                     : (c.head_dim == 64 ? attn_split_kernel<64> : attn_split_kernel<32>);
-        attn<<<dim3(c.n_heads, m->n_chunks), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
-                                                           m->rope, m->apart, m->acnt, m->xb, m->n_chunks, c.n_heads,
-                                                           c.n_kv_heads, c.seq_len, inv_sqrt_hd);
+        attn<<<dim3(c.n_heads, kAttnShares), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
+                                                           m->rope, m->sh_o, m->sh_ml, c.n_heads, c.n_kv_heads,
+                                                           c.seq_len, inv_sqrt_hd);
         EIF_HIP_LAUNCHED();
         sp = eif_hip_prep_spec{};
-        sp.x = m->xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l], sp.eps = c.sub_eps;
+        sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l], sp.eps = c.sub_eps;
         sp.signs = m->signs_q, sp.wht_block = c.wht_q, sp.wht_norm = c.wht_norm_q;
-        if ((rc = eif_hip_qlinear_prep(m->wo[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += O xb
+        // x += O attention (the shares combined in the prep)
+        if ((rc = eif::qlinear_prep_shares(m->wo[l], &sp, m->sh_o, m->sh_ml, c.head_dim, m->x, m->x, c.dim, st)))
+            return rc;
         sp = eif_hip_prep_spec{};
         sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_ffn[l], sp.eps = c.rms_eps;
         sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
@@ -648,7 +640,6 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
     m->rms_att.assign(c.n_layers, nullptr), m->rms_ffn.assign(c.n_layers, nullptr);
     m->rms_sub_att.assign(c.n_layers, nullptr), m->rms_sub_ffn.assign(c.n_layers, nullptr);
     if (hipMalloc(&m->x, sizeof(float) * c.dim) != hipSuccess ||
-        hipMalloc(&m->xb, sizeof(float) * m->q_dim) != hipSuccess ||
         hipMalloc(&m->qkv, sizeof(float) * (m->q_dim + 2 * m->kv_dim)) != hipSuccess ||
         hipMalloc(&m->hb, sizeof(float) * 2 * c.hidden) != hipSuccess ||
         hipMalloc(&m->logits, sizeof(float) * c.vocab) != hipSuccess ||
@@ -660,12 +651,13 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
         eif_hip_bitnet_destroy(m);
         return EIF_HIP_E_NOMEM;
     }
-    const int ch = c.head_dim == 128 ? attn_chunk<128>() : (c.head_dim == 64 ? attn_chunk<64>() : attn_chunk<32>());
-    m->n_chunks = (c.seq_len + ch - 1) / ch;
+    // the shares start at zero: a share a step does not reach keeps finite values, weighed by 0
+    const size_t n_sh_o = (size_t)c.n_heads * kAttnShares * c.head_dim, n_sh_ml = (size_t)c.n_heads * 2 * kAttnShares;
     if (hipMalloc(&m->rope, sizeof(float2) * c.seq_len * (c.head_dim / 2)) != hipSuccess ||
-        hipMalloc(&m->apart, sizeof(float) * c.n_heads * m->n_chunks * (c.head_dim + 2)) != hipSuccess ||
-        hipMalloc(&m->acnt, sizeof(int) * c.n_heads) != hipSuccess ||
-        hipMemset(m->acnt, 0, sizeof(int) * c.n_heads) != hipSuccess) {
+        hipMalloc(&m->sh_o, sizeof(float) * n_sh_o) != hipSuccess ||
+        hipMalloc(&m->sh_ml, sizeof(float) * n_sh_ml) != hipSuccess ||
+        hipMemset(m->sh_o, 0, sizeof(float) * n_sh_o) != hipSuccess ||
+        hipMemset(m->sh_ml, 0, sizeof(float) * n_sh_ml) != hipSuccess) {
         eif_hip_bitnet_destroy(m);
         return EIF_HIP_E_NOMEM;
     }
@@ -886,10 +878,10 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
         for (float *p : *v)
             if (p) (void)hipFree(p);
     for (void *p : {(void *)m->rms_final, (void *)m->signs_dim, (void *)m->signs_q, (void *)m->signs_hidden,
-                    (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->xb, (void *)m->qkv, (void *)m->hb,
+                    (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->qkv, (void *)m->hb,
                     (void *)m->logits, (void *)m->kc, (void *)m->vc, (void *)m->state, (void *)m->prompt,
                     (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_v, (void *)m->amax_i,
-                    (void *)m->rope, (void *)m->apart, (void *)m->acnt})
+                    (void *)m->rope, (void *)m->sh_o, (void *)m->sh_ml})
         if (p) (void)hipFree(p);
     delete m;
 }

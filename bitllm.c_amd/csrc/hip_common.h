@@ -43,6 +43,10 @@ EIF_DEV float eif_wave_sum(float v)
     return v;
 }
 
+// Decode attention: the positions of a head are split into at most kAttnShares chunks, each leaving a share
+// (unnormalized output, running maximum, sum) that the next linear's prep combines.
+constexpr int kAttnShares = 8;
+
 // Internal launchers shared between translation units (defined in the .hip files).
 namespace eif {
 int launch_prep_rows(const float *x, int ldx, const float *signs, int M, int K, int wht_block, float norm,
@@ -54,6 +58,12 @@ int launch_quant_rows(const float *x, int ldx, int M, int K, int8_t *xq, int ldq
 int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *xq, int ldq, const float *xs,
                    const float *bias, float *y, int ldy, int M, int path, hipStream_t st);
 int qweight_row_tiles(const eif_hip_qweight *w);
+// The fused-prep linear of one token row (M = 1) whose input row is combined from attention shares in the prep:
+// column c = h hd + d is sum_s e^(M_s - M) O_s[d] / sum_s e^(M_s - M) L_s over the shares s of head h, M = max_s M_s,
+// with sh_o [K / hd][kAttnShares][hd] the outputs O_s and sh_ml [K / hd][2 kAttnShares] the maxima M_s, then the
+// sums L_s (a share with M_s = -inf weighs 0). spec->x and spec->ldx are ignored; ternary weights only.
+int qlinear_prep_shares(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *sh_o,
+                        const float *sh_ml, int hd, const float *bias, float *y, int ldy, hipStream_t st);
 int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y, float *amax_v,
                    int *amax_i, hipStream_t st);
 

@@ -405,6 +405,9 @@ struct PrepArgs {
     const float *x2;      // EIF_HIP_PRE_SWIGLU_RMS: the up-projection rows [M, ldx] (x holds the gate)
     const float *nw;      // RMSNorm weight [K], NULL = 1
     float eps;            // RMSNorm epsilon
+    const float *sh_o;    // attention shares in place of x (one row): [K / sh_hd][kAttnShares][sh_hd] outputs,
+    const float *sh_ml;   // [K / sh_hd][2 kAttnShares] maxima then sums; NULL: x holds the rows
+    int sh_hd;
 };
 
 // v <- v of lane (l ^ LX): DPP only for LX <= 8 (quad_perm, row_half_mirror, row_mirror compositions).
@@ -509,6 +512,50 @@ EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E], 
     load4<E>((p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : xr) + ic, nw);
 }
 
+// The attention shares of thread t's columns [E t, E t + E) (head h = E t / sh_hd, dims from E t % sh_hd): every
+// share's outputs and the head's maxima and sums, loaded unconditionally like prep_load (signs and the norm
+// weight too, from the outputs where absent).
+template <int E>
+struct Shares {
+    float o[kAttnShares][E];
+    float ml[2 * kAttnShares];
+};
+
+template <int E>
+EIF_DEV void prep_load_sh(const PrepArgs &p, Shares<E> &sh, float (&sg)[E], float (&nw)[E])
+{
+    const int i0 = E * threadIdx.x;
+    const int ic = i0 < p.K ? i0 : 0;
+    const int h = ic / p.sh_hd, d = ic - h * p.sh_hd;
+    load4<2 * kAttnShares>(p.sh_ml + (size_t)h * 2 * kAttnShares, sh.ml);
+    const float *o = p.sh_o + (size_t)h * kAttnShares * p.sh_hd + d;
+#pragma unroll
+    for (int s = 0; s < kAttnShares; ++s) load4<E>(o + s * p.sh_hd, sh.o[s]);
+    load4<E>((p.signs ? p.signs : p.sh_o) + ic, sg);
+    load4<E>((p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : p.sh_o) + ic, nw);
+}
+
+// v = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s, M = max_s M_s (share 0 always holds rows, so M is finite).
+template <int E>
+EIF_DEV void sh_combine(const Shares<E> &sh, float (&v)[E])
+{
+    float mx = sh.ml[0];
+#pragma unroll
+    for (int s = 1; s < kAttnShares; ++s) mx = fmaxf(mx, sh.ml[s]);
+    float ls = 0.0f, o[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kAttnShares; ++s) {
+        const float w = expf(sh.ml[s] - mx);
+        ls = fmaf(w, sh.ml[kAttnShares + s], ls);
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = fmaf(w, sh.o[s][e], o[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = o[e] / ls;
+}
+
 // Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
 // LB = log2 of the WHT block when it is fixed at compile time (0: no rotation), -1: block read from p.block.
 template <int E, int LB>
@@ -610,8 +657,8 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
 // RT row tiles of 16 rows per workgroup; wave w works on tile w % RT and on steps w / RT, w / RT + ks, ... of
 // it (ks = waves / RT). SPW: steps per wave held in registers at once; the first SPW are loaded unconditionally
 // (a wave with fewer steps loads its last step again and skips the copies), later chunks only when a row has
-// more steps.
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT>
+// more steps. SH: one token row combined from attention shares (PrepArgs::sh_o) in the prep.
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, bool SH = false>
 __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 {
     using GE = Geo<FMT, UD>;
@@ -658,7 +705,10 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         }
     };
     float xs_v = 0.0f;
-    if constexpr (E > 0) {
+    [[maybe_unused]] Shares<SH ? EV : 1> shv;
+    if constexpr (SH) {
+        prep_load_sh<E>(p, shv, sg, nwv);
+    } else if constexpr (E > 0) {
         prep_load<E>(p, 0, v, sg, v2, nwv);
     } else {
         pc0 = *piece_at(0);
@@ -713,7 +763,12 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     }
 
     // 3. activations -> LDS
-    if constexpr (E > 0) {
+    if constexpr (SH) {
+        sh_combine<E>(shv, v);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v2[e] = 0.0f;
+        prep_finish<E, LB>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
+    } else if constexpr (E > 0) {
         prep_finish<E, LB>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
         for (int m = 1; m < a.M; ++m) {
             prep_load<E>(p, m, v, sg, v2, nwv);
@@ -1092,9 +1147,25 @@ int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipSt
     return EIF_HIP_OK;
 }
 
+// The shares-combining form (one row, ternary weights, E = 4 or 8, one row tile per workgroup, one step per
+// wave held at once).
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
+int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
+{
+    if constexpr (FMT == kTern && !ACC && (E == 4 || E == 8) && RT == 1) {
+        const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
+        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, true><<<rows_pad / 16, 64 * ks, lds, st>>>(a, p);
+        EIF_HIP_LAUNCHED();
+        return EIF_HIP_OK;
+    } else {
+        return EIF_HIP_E_ARG;
+    }
+}
+
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
 int launch_gemv_e(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
+    if (p.sh_ml) return launch_gemv_sh<FMT, UD, GROUPED, ACC, E, LB, RT>(a, p, rows_pad, ks, st);
     constexpr int SMAX = Geo<FMT, UD>::SB >= 32 ? 4 : 8;   // 8-dword steps: half the registers per chunk
     const int steps = eif_ceil_div(a.nsteps, ks);
     if constexpr (ACC || !gemv_tuned<FMT, UD, GROUPED>()) {
@@ -1151,6 +1222,7 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
         // chains), and a WHT block within one wave.
         for (int e = 4; e <= 16; e *= 2) {
             if (64 * e < p.block || e < g_gemv_prep_cols) continue;
+            if (p.sh_ml && (e > 8 || p.sh_hd % e != 0)) continue;
             int k = ks;
             while (k < maxks && (64 * rt * k * e < kpad || !scales_fit(k))) ++k;
             if (64 * rt * k * e < kpad || !scales_fit(k)) continue;
@@ -1177,7 +1249,7 @@ int launch_gemv(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
     p.ldl = a.nsteps * Geo<FMT, UD>::SC + 16;
     int rt = 1;
     if constexpr (gemv_tuned<FMT, UD, GROUPED>())
-        rt = g_gemv_rt > 0 ? g_gemv_rt : (rows_pad / 16 >= 768 && (GROUPED || p.x || rows_pad / 16 < kBigTiles) ? 4 : 1);
+        if (!p.sh_ml) rt = g_gemv_rt > 0 ? g_gemv_rt : (rows_pad / 16 >= 768 && (GROUPED || p.x || rows_pad / 16 < kBigTiles) ? 4 : 1);
     if (rt > 1) {
         const int rc = launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, rt, st);
         if (rc == EIF_HIP_OK || rc == EIF_HIP_E_DEVICE) return rc;
@@ -1346,6 +1418,27 @@ int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const fl
     a.amax_v = amax_v;
     a.amax_i = amax_i;
     rc = gemv_rowscaled(w, a, st);
+    return rc == 1 ? EIF_HIP_E_LIMIT : rc;
+}
+
+int qlinear_prep_shares(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *sh_o,
+                        const float *sh_ml, int hd, const float *bias, float *y, int ldy, hipStream_t st)
+{
+    if (!w || !spec || !sh_o || !sh_ml || w->fmt != kTern || hd < 4 || w->cols % hd != 0 ||
+        ((uintptr_t)sh_o & 15) || ((uintptr_t)sh_ml & 15) || spec->pre == EIF_HIP_PRE_SWIGLU_RMS)
+        return EIF_HIP_E_ARG;
+    eif_hip_prep_spec sp = *spec;
+    sp.x = sh_o, sp.ldx = w->cols;   // the row's bounds checks (the kernel reads the shares instead)
+    PrepArgs p;
+    int rc = make_prep_spec(w, &sp, 1, &p);
+    if (rc) return rc;
+    if (!y || ldy < w->rows) return EIF_HIP_E_ARG;
+    p.sh_o = sh_o, p.sh_ml = sh_ml, p.sh_hd = hd;
+    QArgs a = make_args(w, nullptr, 0, 1);
+    a.bias = bias;
+    a.y = y;
+    a.ldy = ldy;
+    rc = dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, st);
     return rc == 1 ? EIF_HIP_E_LIMIT : rc;
 }
 

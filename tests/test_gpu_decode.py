@@ -99,6 +99,23 @@ def test_decode_head128_gqa(gpu, oracle):
     compare_steps(gpu, oracle, cfg, w, prompt, 80, graph=False)
 
 
+def test_decode_long_context_shares(gpu, oracle):
+    # head_dim 128: attention chunks of 128 positions up to position 1023 (eight shares at 1016..1023), then of
+    # 256 (position 1024 alone in the fifth chunk); graph replays across the change of chunk length
+    cfg = synth.bitnet_config(512, 768, 2, 8, 2, 128, 1000, 1280, 128, 96, 128, 128, 128)
+    w = synth.bitnet_model((21,), cfg)
+    prompt = list(np.random.default_rng(22).integers(0, cfg["vocab"], 1040))
+    compare_steps(gpu, oracle, cfg, w, prompt, 1030, graph=True, prefill=1016)
+
+
+def test_decode_shares_head64(gpu, oracle):
+    # head_dim 64: chunks of 256 positions, the second chunk starting at position 256
+    cfg = synth.bitnet_config(256, 512, 2, 4, 2, 64, 500, 320, 64, 64, 64, 64, 128)
+    w = synth.bitnet_model((23,), cfg)
+    prompt = list(np.random.default_rng(24).integers(0, cfg["vocab"], 270))
+    compare_steps(gpu, oracle, cfg, w, prompt, 262, graph=False, prefill=250)
+
+
 def test_decode_row_scales(gpu, oracle):
     # one scale per ternary row (group 0 on the GPU, one group spanning the input in the oracle)
     cfg = make_golden.decode_config()
