@@ -4,9 +4,9 @@
  * Replaces the token loop of the reference's tinyllm engine for the BitNet path: tinyllm_forward /
  * tinyllm_forward_embedding_ex (src/eif_tinyllm.c:371-857, :1502-1506) and its greedy sampler
  * tinyllm_sample_greedy (src/eif_tinyllm.c:1519-1530). One token step is 5 launches per layer plus 3:
- *   per layer: [RMSNorm + WHT + INT8] QKV GEMV | RoPE + fp16 KV append + attention over chunks of the
- *              positions, the chunks combined by the last of them |
- *              [sub-RMSNorm + WHT + INT8] O GEMV + residual | [RMSNorm + WHT + INT8] gate/up GEMV |
+ *   per layer: [RMSNorm + WHT + INT8] QKV GEMV | RoPE + fp16 KV append + attention over up to eight chunks of
+ *              the positions per head, one share each |
+ *              [shares combined + sub-RMSNorm + WHT + INT8] O GEMV + residual | [RMSNorm + WHT + INT8] gate/up GEMV |
  *              [SiLU(gate) * up + sub-RMSNorm + WHT + INT8] down GEMV + residual
  *   RMSNorm + INT8 prep | INT8 head GEMV with per-tile maxima | argmax (greedy) or the next prompt token,
  *   position + 1, the next token's embedding row (INT8 table x per-token scale)
