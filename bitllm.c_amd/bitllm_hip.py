@@ -58,6 +58,13 @@ _SIGS = {
     "eif_hip_bitnet_steps": (_i, [_vp, _i, _i, _vp]),
     "eif_hip_bitnet_prefill": (_i, [_vp, _i, _vp]),
     "eif_hip_bitnet_load_svlm": (_i, [_vp, C.c_char_p, _i]),
+    "eif_qwen35_parse": (_i, [_vp, _sz, _vp]),
+    "eif_hip_qwen35_load": (_i, [_vp, C.c_char_p, _vp]),
+    "eif_hip_qwen35_destroy": (None, [_vp]),
+    "eif_hip_qwen35_get_layout": (_vp, [_vp]),
+    "eif_hip_qwen35_linear": (_vp, [_vp, _i, _i]),
+    "eif_hip_qwen35_head": (_vp, [_vp]),
+    "eif_hip_qwen35_vector": (_vp, [_vp, _sz]),
     "eif_hip_bitnet_get_config": (_i, [_vp, _vp]),
     "eif_hip_bitnet_tokens": (_i, [_vp, _vp, _i, _vp]),
     "eif_hip_bitnet_logits": (_i, [_vp, _vp, _vp]),
@@ -191,10 +198,17 @@ class QWeight:
         self.kpad, self.bytes = kp.value, b.value
         return self
 
+    @classmethod
+    def view(cls, h, owner):
+        """A QWeight around a handle that `owner` keeps (and destroys); holds a reference to the owner."""
+        self = cls.wrap(h)
+        self._owner = owner
+        return self
+
     def close(self):
-        if self.h:
+        if self.h and getattr(self, "_owner", None) is None:
             load().eif_hip_qweight_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:
@@ -340,6 +354,71 @@ class BitnetModel:
     def close(self):
         if self.h:
             load().eif_hip_bitnet_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- Qwen3.5 model files (include/eif_hip_qwen35.h) ----
+Q35_DN_QKV, Q35_DN_Z, Q35_DN_OUT, Q35_DN_B, Q35_DN_A, Q35_FA_Q, Q35_FA_K, Q35_FA_V, Q35_FA_O, Q35_FF_GATE, \
+    Q35_FF_UP, Q35_FF_DOWN = range(12)
+Q35_KINDS = 12
+Q35_FP32, Q35_INT4, Q35_TERN2, Q35_TERN3, Q35_INT8 = range(5)
+
+
+class Q35Tensor(C.Structure):
+    _fields_ = [("codes", C.c_size_t), ("scales", C.c_size_t), ("rows", C.c_int), ("cols", C.c_int),
+                ("qtype", C.c_int), ("group", C.c_int)]
+
+
+class Q35Layout(C.Structure):
+    _fields_ = [("config", C.c_int32 * 32), ("layer_types", C.c_uint8 * 24), ("n_layers", C.c_int),
+                ("embed", Q35Tensor), ("lin", (Q35Tensor * Q35_KINDS) * 24),
+                ("rms_att", C.c_size_t * 24), ("rms_ffn", C.c_size_t * 24), ("rms_final", C.c_size_t),
+                ("sub_att", C.c_size_t * 24), ("sub_ffn", C.c_size_t * 24),
+                ("conv", C.c_size_t * 24), ("dt_bias", C.c_size_t * 24), ("a_log", C.c_size_t * 24),
+                ("delta_norm", C.c_size_t * 24), ("q_norm", C.c_size_t * 24), ("k_norm", C.c_size_t * 24),
+                ("signs_dim", C.c_size_t), ("signs_hid", C.c_size_t), ("hadamard_block", C.c_int),
+                ("weights_end", C.c_size_t), ("scales_end", C.c_size_t), ("norms_end", C.c_size_t)]
+
+
+def qwen35_parse(image):
+    """The layout of a QWN5 image (bytes) as eif_qwen35_parse walks it (host code, no GPU)."""
+    buf = (C.c_uint8 * len(image)).from_buffer_copy(image)
+    lay = Q35Layout()
+    check(load().eif_qwen35_parse(C.cast(buf, _vp), len(image), C.byref(lay)), "eif_qwen35_parse")
+    return lay
+
+
+class Qwen35Model:
+    """A QWN5 file's quantized linears and tied head resident on the GPU (eif_hip_qwen35_load)."""
+
+    def __init__(self, path, stream=None):
+        h = C.c_void_p()
+        check(load().eif_hip_qwen35_load(C.byref(h), os.fsencode(path), stream_ptr(stream)), "eif_hip_qwen35_load")
+        self.h = h
+        self.layout = Q35Layout.from_address(load().eif_hip_qwen35_get_layout(h))
+
+    def linear(self, layer, kind):
+        """The resident weight (a QWeight view) or None (absent or FP32)."""
+        w = load().eif_hip_qwen35_linear(self.h, layer, kind)
+        return QWeight.view(w, self) if w else None
+
+    def head(self):
+        w = load().eif_hip_qwen35_head(self.h)
+        return QWeight.view(w, self) if w else None
+
+    def vector(self, offset):
+        """Device address of an FP32 vector of the layout (0 if absent)."""
+        return load().eif_hip_qwen35_vector(self.h, offset) or 0
+
+    def close(self):
+        if self.h:
+            load().eif_hip_qwen35_destroy(self.h)
             self.h = None
 
     def __del__(self):

@@ -206,3 +206,187 @@ def write_svlm(path, cfg, w, group_bound, hadamard=True):
         f.write(weights)
         f.write(scales)
         f.write(norms)
+
+
+# ---- Qwen3.5 (QWN5) model files ----
+Q35_FP32, Q35_INT4, Q35_TERN2, Q35_TERN3 = 0, 1, 2, 3
+Q35_EMBED_INT8, Q35_EMBED_INT4, Q35_EMBED_2BIT, Q35_EMBED_DENSE, Q35_EMBED_FP32 = 0, 1, 2, 3, 4
+
+
+def qwen35_config(dim, hidden, layer_types, n_heads, n_kv_heads, head_dim, vocab, lin_k_heads, lin_k_dim,
+                  lin_v_heads, lin_v_dim, conv_k=4, seq_len=64, quant_lm=Q35_TERN2, quant_embed=Q35_EMBED_INT8,
+                  group=0, hadamard=0, plain=0):
+    """A Qwen3.5 hybrid configuration (qwen35_config_t, include/eif_qwen35.h:56-110): layer_types is a list of
+    0 (DeltaNet) / 1 (full attention)."""
+    lt = list(layer_types)
+    return dict(dim=dim, hidden=hidden, layer_types=lt, n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=head_dim,
+                vocab=vocab, lin_k_heads=lin_k_heads, lin_k_dim=lin_k_dim, lin_v_heads=lin_v_heads,
+                lin_v_dim=lin_v_dim, conv_k=conv_k, seq_len=seq_len, quant_lm=quant_lm, quant_embed=quant_embed,
+                group=group, hadamard=hadamard, plain=plain)
+
+
+def pack_ternary_dense(v):
+    """int8 values in {-1,0,1}, shape [..., K] -> uint8 [..., (K+4)//5]: five base-3 digits per byte, the first
+    column least significant, digit 1 = +1, 2 = -1 (the reference's dense LUT, src/eif_qwen35.c:78-92)."""
+    v = np.asarray(v)
+    K = v.shape[-1]
+    Kp = (K + 4) // 5 * 5
+    d = np.zeros(v.shape[:-1] + (Kp,), np.int32)
+    d[..., :K] = np.where(v > 0, 1, np.where(v < 0, 2, 0))
+    d = d.reshape(v.shape[:-1] + (Kp // 5, 5))
+    return (d[..., 0] + 3 * d[..., 1] + 9 * d[..., 2] + 27 * d[..., 3] + 81 * d[..., 4]).astype(np.uint8)
+
+
+def _q35_matrix(r, rows, cols, qt):
+    """Random rows of one storage type: (bytes, values) with values the ternary / int4 ints or FP32 floats."""
+    if qt == Q35_FP32:
+        v = r.standard_normal((rows, cols)).astype(np.float32)
+        return v.tobytes(), v
+    if qt == Q35_INT4:
+        v = r.integers(-8, 8, size=(rows, cols), dtype=np.int8)
+        return pack_int4(v).tobytes(), v
+    if qt == 4:   # int8 embedding
+        v = r.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+        return v.tobytes(), v
+    v = r.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    return (pack_ternary(v) if qt == Q35_TERN2 else pack_ternary_dense(v)).tobytes(), v
+
+
+def qwen35_image(cfg, key, sub_norms=True, region_pad=0):
+    """A QWN5 image in the layout qwen35_load walks (src/eif_qwen35.c:1223-1430), random contents: returns
+    (image bytes, arrays) where arrays maps a name to (byte offset, values, scales or None, scales' byte offset or
+    0). Names: "embed";
+    "L{l}.{kind}" for kinds qkv, z, out, pb, pa (DeltaNet), q, k, v, o (attention), gate, up, down; FP32 vectors
+    "L{l}.rms_att", "L{l}.rms_ffn", "rms_final", "L{l}.conv", "L{l}.dt", "L{l}.alog", "L{l}.dnorm", "L{l}.qnorm",
+    "L{l}.knorm", "L{l}.sub_att", "L{l}.sub_ffn", "signs_dim", "signs_hid". region_pad bytes go before each region
+    (an odd count puts every array off its natural alignment)."""
+    r = rng(*key, 40)
+    d, h, lt, V = cfg["dim"], cfg["hidden"], cfg["layer_types"], cfg["vocab"]
+    L = len(lt)
+    nh, nkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    nk, kd, nv, vd, ck = cfg["lin_k_heads"], cfg["lin_k_dim"], cfg["lin_v_heads"], cfg["lin_v_dim"], cfg["conv_k"]
+    qlm, qe, g, had = cfg["quant_lm"], cfg["quant_embed"], cfg["group"], cfg["hadamard"]
+    key_dim, val_dim = nk * kd, nv * vd
+    conv_dim, q_dim, kv_dim = 2 * key_dim + val_dim, nh * hd, nkv * hd
+    small = Q35_FP32 if g > 0 else qlm
+    dn = [l for l in range(L) if lt[l] == 0]
+    fa = [l for l in range(L) if lt[l] == 1]
+    arrays = {}
+    regions = {"w": bytearray(), "s": bytearray(), "n": bytearray()}
+    pending = []   # (region, name, field, position in region)
+
+    def put(region, name, data, field=0):
+        pending.append((region, name, field, len(regions[region])))
+        regions[region] += data
+
+    def scales_of(rows, cols, grouped):
+        n = rows * (cols // g) if grouped else rows
+        return (np.abs(r.standard_normal(n)) * 0.02 + 1e-3).astype(np.float32)
+
+    emb_qt = {Q35_EMBED_INT8: 4, Q35_EMBED_INT4: Q35_INT4, Q35_EMBED_2BIT: Q35_TERN2,
+              Q35_EMBED_DENSE: Q35_TERN3, Q35_EMBED_FP32: Q35_FP32}[qe]
+    b, v = _q35_matrix(r, V, d, emb_qt)
+    arrays["embed"] = [0, v, None, 0]
+    put("w", "embed", b)
+    shapes = {"qkv": (conv_dim, d), "z": (val_dim, d), "out": (d, val_dim), "pb": (nv, d), "pa": (nv, d),
+              "q": (2 * q_dim, d), "k": (kv_dim, d), "v": (kv_dim, d), "o": (d, q_dim),
+              "gate": (h, d), "up": (h, d), "down": (d, h)}
+
+    def mats(kinds, layers, qt=None, slots=None):
+        for kind in kinds:
+            rows, cols = shapes[kind]
+            for i in range(slots if slots is not None else len(layers)):
+                b, v = _q35_matrix(r, rows, cols, qt if qt is not None else qlm)
+                if i < len(layers):
+                    arrays[f"L{layers[i]}.{kind}"] = [0, v, None, 0]
+                    put("w", f"L{layers[i]}.{kind}", b)
+                else:
+                    regions["w"] += b     # an unused FFN slot
+    mats(("qkv", "z", "out"), dn)
+    mats(("pb", "pa"), dn, qt=small)
+    mats(("q", "k", "v", "o"), fa)
+    mats(("gate", "up", "down"), list(range(L)), slots=24)
+    for name, n in (("conv", conv_dim * ck), ("dt", nv), ("alog", nv)):
+        for l in dn:
+            v = r.standard_normal(n).astype(np.float32)
+            arrays[f"L{l}.{name}"] = [0, v, None, 0]
+            put("w", f"L{l}.{name}", v.tobytes())
+    # scales
+    ge = qe == Q35_EMBED_2BIT and g > 0
+    s = scales_of(V, d, ge)
+    arrays["embed"][2] = s
+    put("s", "embed", s.tobytes(), 3)
+    grouped = g > 0
+    for l in dn:
+        for kind in ("qkv", "z", "out"):
+            s = scales_of(*shapes[kind], grouped)
+            arrays[f"L{l}.{kind}"][2] = s
+            put("s", f"L{l}.{kind}", s.tobytes(), 3)
+        if not grouped:
+            for kind in ("pb", "pa"):
+                s = scales_of(nv, d, False)
+                arrays[f"L{l}.{kind}"][2] = s
+                put("s", f"L{l}.{kind}", s.tobytes(), 3)
+    for l in fa:
+        for kind in ("q", "k", "v", "o"):
+            s = scales_of(*shapes[kind], grouped)
+            arrays[f"L{l}.{kind}"][2] = s
+            put("s", f"L{l}.{kind}", s.tobytes(), 3)
+    for slot in range(24):
+        for kind in ("gate", "up", "down"):
+            s = scales_of(*shapes[kind], grouped)
+            if slot < L:
+                arrays[f"L{slot}.{kind}"][2] = s
+                put("s", f"L{slot}.{kind}", s.tobytes(), 3)
+            else:
+                regions["s"] += s.tobytes()
+
+    def vec(name, n, signs=False):
+        v = (np.where(r.random(n) < 0.5, -1.0, 1.0) if signs else 1.0 + 0.1 * r.standard_normal(n)).astype(np.float32)
+        if name is not None:
+            arrays[name] = [0, v, None, 0]
+            put("n", name, v.tobytes())
+        else:
+            regions["n"] += v.tobytes()
+    for which in ("rms_att", "rms_ffn"):
+        for slot in range(24):
+            vec(f"L{slot}.{which}" if slot < L else None, d)
+    vec("rms_final", d)
+    for l in range(L):
+        if lt[l] == 0:
+            vec(f"L{l}.dnorm", vd)
+        else:
+            vec(f"L{l}.qnorm", hd)
+            vec(f"L{l}.knorm", hd)
+    if had:
+        vec("signs_dim", d, True)
+        vec("signs_hid", h, True)
+    if sub_norms:
+        for l in range(L):
+            if lt[l] == 1:
+                vec(f"L{l}.sub_att", q_dim)
+            vec(f"L{l}.sub_ffn", h)
+    # place: header, config, layer types, then the weights, scales and norms regions
+    head = 48 + 128 + L
+    offs = {}
+    pos = head
+    for key_ in ("w", "s", "n"):
+        pos += region_pad
+        offs[key_] = pos
+        pos += len(regions[key_])
+    img = bytearray(pos)
+    hdr = np.zeros(12, np.uint32)
+    hdr[0], hdr[1], hdr[2] = 0x51574E35, 1, 48
+    hdr[3], hdr[4], hdr[5] = offs["w"], offs["s"], offs["n"]
+    hdr[7], hdr[8], hdr[9] = len(regions["w"]), len(regions["s"]), len(regions["n"])
+    ci = np.zeros(32, np.int32)
+    ci[:15] = [d, h, L, nh, nkv, hd, V, cfg["seq_len"], len(dn), len(fa), nk, kd, nv, vd, ck]
+    ci[22], ci[23], ci[25], ci[26], ci[27], ci[28] = 1, qlm, qe, cfg["plain"], g, had
+    img[:48] = hdr.tobytes()
+    img[48:176] = ci.tobytes()
+    img[176:176 + L] = bytes(lt)
+    for key_ in ("w", "s", "n"):
+        img[offs[key_]:offs[key_] + len(regions[key_])] = regions[key_]
+    for region, name, field, at in pending:
+        arrays[name][field] = offs[region] + at
+    return bytes(img), {k: tuple(v) for k, v in arrays.items()}

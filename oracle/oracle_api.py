@@ -64,6 +64,8 @@ REF_SIGS = {
     "tinyllm_matmul_int8_rowscale": (None, [_vp, _vp, _vp, _i, _i, _vp]),
     "ref_q35_int4_gemv": (None, [_vp, _vp, _vp, _vp, _i, _i]),
     "ref_q35_int8_gemv": (None, [_vp, _vp, _vp, _vp, _i, _i]),
+    "ref_q35_layout": (_i, [C.c_char_p, _vp, _i, _vp]),
+    "ref_q35_dense_gemv": (None, [_vp, _vp, _vp, _vp, _i, _i]),
     "eif_gemm_f32_nt_ld": (None, [_vp, _i, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i]),
     "eif_softmax_rows_f32": (None, [_vp, _i, _i, _i, _f]),
 }
