@@ -116,6 +116,15 @@ def test_decode_shares_head64(gpu, oracle):
     compare_steps(gpu, oracle, cfg, w, prompt, 262, graph=False, prefill=250)
 
 
+def test_decode_big_vocab_head(gpu, oracle):
+    # a 70000-token INT8 head (4375 row tiles): the vocabulary-sized head path (one prep launch, then the GEMV
+    # with per-tile maxima over 4375 tiles) against the oracle
+    cfg = synth.bitnet_config(128, 256, 1, 4, 2, 32, 70000, 32, 32, 32, 128, 128, 256)
+    w = synth.bitnet_model((25,), cfg)
+    prompt = [11, 69999, 123]
+    compare_steps(gpu, oracle, cfg, w, prompt, 10, graph=False)
+
+
 def test_decode_row_scales(gpu, oracle):
     # one scale per ternary row (group 0 on the GPU, one group spanning the input in the oracle)
     cfg = make_golden.decode_config()
