@@ -1055,15 +1055,29 @@ int device_cus()
 
 int g_gemm_split = 0;   // splits along K of the GEMM, 0 = chosen from the shape
 
-// Splits along K: enough workgroups for two per CU when the tiles alone are fewer than one per CU, at least
-// three steps per split, at most 16; 1 for the parity outputs and when no workspace can be had (first use of
-// a stream inside a graph capture).
+// Splits along K (at most 16, at least three steps per split). Fewer tiles than CUs: the split with the fewest
+// rounds of workgroups per unit of work, ceil(tiles s / CUs) / s, the smallest of equal ones. One round or
+// more: 2 when a long K (24 steps or more) leaves the last round under 70% full (e.g. 320 tiles on 256 CUs).
+// 1 for the parity outputs and when no workspace can be had (first use of a stream inside a graph capture).
 template <bool ACC>
 int pick_split(QArgs &a, int tiles, hipStream_t st)
 {
     if (ACC) return 1;
     int ks = g_gemm_split;
-    if (ks == 0) ks = tiles < device_cus() ? eif_ceil_div(2 * device_cus(), tiles) : 1;
+    if (ks == 0) {
+        const int C = device_cus(), smax = std::min(16, std::max(1, a.nsteps / 3));
+        if (tiles < C) {
+            ks = 1;
+            double best = 1.0;
+            for (int s2 = 2; s2 <= smax; ++s2) {
+                const double r = (double)eif_ceil_div(tiles * s2, C) / s2;
+                if (r < best - 1e-9) best = r, ks = s2;
+            }
+        } else {
+            const int rounds = eif_ceil_div(tiles, C);
+            ks = a.nsteps >= 24 && (double)tiles < 0.7 * rounds * C ? 2 : 1;
+        }
+    }
     ks = std::min(ks, std::min(16, std::max(1, a.nsteps / 3)));
     if (ks <= 1) return 1;
     a.part = split_ws(st, (size_t)ks * a.M * a.N * sizeof(float));
