@@ -291,20 +291,138 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float *qkv, int ldqkv,
     }
 }
 
-// Prefill, step 2: query head h of token i (workgroup (h, i)) over cache rows 0 .. pos0 + i (causal).
+// Prefill, step 2: causal attention of the batch on fp32 MFMAs (v_mfma_f32_16x16x4f32: lane l supplies A[l % 16][l / 16]
+// and B[l / 16][l % 16], and holds D[4 (l / 16) + i][l % 16] in register i). Workgroup (x, y) takes batch tokens
+// [16 y, 16 y + 16) and up to four query heads of kv head g = x / P (P = ceil(kv_mul / 4)), one wave per head. Per
+// 16-key tile: S = Q K^T over the head's dims (lane group q holds dims [q HD/4, (q + 1) HD/4), the same order for Q
+// and K), s = S / sqrt(HD) with keys past the query's position at -inf; per query row the online softmax of the
+// decode (max m, sum l, the outputs rescaled by e^(m - m')); then O += P V with P passed through LDS and the tile's
+// values staged in LDS once for the workgroup (dims x keys, zero past the batch's last key). out = O / l.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int ldqkv, const __half *kc,
-                                                           const __half *vc, float *out, int ldo, int pos0,
+                                                           const __half *vc, float *out, int ldo, int pos0, int n,
                                                            int n_heads, int n_kv, int seq_len, float inv_sqrt_hd)
 {
-    __shared__ float q_l[HD];
-    const int h = blockIdx.x, i = blockIdx.y, g = h / (n_heads / n_kv);
-    auto load_q = [&]() {
-        if ((int)threadIdx.x < HD) q_l[threadIdx.x] = qkv[(size_t)i * ldqkv + h * HD + threadIdx.x];
-        __syncthreads();
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    constexpr int DQ = HD / 4, NT = HD / 16, VP = 20;
+    __shared__ __align__(16) float v_l[2][HD][VP];
+    __shared__ __align__(16) float p_l[4][16][VP];
+    const int kv_mul = n_heads / n_kv, parts = (kv_mul + 3) / 4;
+    const int g = blockIdx.x / parts, part = blockIdx.x - g * parts;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const bool active = part * 4 + w < kv_mul;   // uniform over the wave
+    const int h = g * kv_mul + (active ? part * 4 + w : 0);
+    const int i0 = blockIdx.y * 16, r = lane & 15, q = lane >> 4;
+    const __half *kg = kc + (size_t)g * seq_len * HD, *vg = vc + (size_t)g * seq_len * HD;
+    const int n_keys = pos0 + min(i0 + 16, n);   // keys the block's queries may see
+    const int n_tiles = (n_keys + 15) / 16;
+
+    float qv[DQ];   // query row r (batch token i0 + r), dims [DQ q, DQ q + DQ)
+    {
+        const float *qp = qkv + (size_t)min(i0 + r, n - 1) * ldqkv + h * HD + DQ * q;
+#pragma unroll
+        for (int j = 0; j < DQ; j += 4) {
+            const float4 f = *reinterpret_cast<const float4 *>(qp + j);
+            qv[j] = f.x, qv[j + 1] = f.y, qv[j + 2] = f.z, qv[j + 3] = f.w;
+        }
+    }
+    v4f O[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) O[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_r[4], l_r[4];   // rows 4 q + i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m_r[i] = -INFINITY, l_r[i] = 0.0f;
+
+    // Tile kt + 1's keys and values are loaded into registers while tile kt computes (the last tile loads
+    // itself again); the values go to LDS at the top of the next iteration.
+    constexpr int VI = 2 * HD / 64;   // staging pieces per thread at most (8 values each, 64-thread workgroups)
+    uint4 vraw[VI], kraw[DQ / 8];
+    auto fetch = [&](int kt) {
+        const int k0 = 16 * kt;
+#pragma unroll
+        for (int u = 0; u < VI; ++u) {
+            const int idx = t + u * (int)blockDim.x;
+            const int key = min(idx, 2 * HD - 1) & 15, d0 = (min(idx, 2 * HD - 1) >> 4) * 8;
+            vraw[u] = *reinterpret_cast<const uint4 *>(vg + (size_t)min(k0 + key, n_keys - 1) * HD + d0);
+        }
+        const __half *kp = kg + (size_t)min(k0 + r, n_keys - 1) * HD + DQ * q;
+#pragma unroll
+        for (int j = 0; j < DQ / 8; ++j) kraw[j] = *reinterpret_cast<const uint4 *>(kp + 8 * j);
     };
-    attend<HD, 256, false>(q_l, kc + (size_t)g * seq_len * HD, vc + (size_t)g * seq_len * HD, pos0 + i + 1, nullptr,
-                           nullptr, inv_sqrt_hd, out + (size_t)i * ldo + h * HD, nullptr, load_q);
+    fetch(0);
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        const int k0 = 16 * kt;
+        float(*vb)[VP] = v_l[kt & 1];
+#pragma unroll
+        for (int u = 0; u < VI; ++u) {   // 8 values of one key per piece, zero past the batch's last key
+            const int idx = t + u * (int)blockDim.x;
+            if (idx < 2 * HD) {
+                const int key = idx & 15, d0 = (idx >> 4) * 8;
+                float vv[8];
+                half8_to_float(vraw[u], vv);
+                const bool ok = k0 + key < n_keys;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vb[d0 + e][key] = ok ? vv[e] : 0.0f;
+            }
+        }
+        float kv[DQ];   // key row k0 + r (clamped; keys past n_keys are masked), dims [DQ q, DQ q + DQ)
+#pragma unroll
+        for (int j = 0; j < DQ / 8; ++j) {
+            float f8[8];
+            half8_to_float(kraw[j], f8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kv[8 * j + e] = f8[e];
+        }
+        fetch(min(kt + 1, n_tiles - 1));
+        __syncthreads();   // the tile's values staged; the other buffer's readers (tile kt - 1) are done
+        if (active) {
+            v4f S = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < DQ; ++j) S = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[j], kv[j], S, 0, 0, 0);
+            const int kpos = k0 + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {   // S[i] = score of query row 4 q + i and key k0 + r
+                const int qpos = pos0 + i0 + 4 * q + i;
+                const float sv = kpos <= qpos && kpos < n_keys ? S[i] * inv_sqrt_hd : -INFINITY;
+                float mx = fmaxf(sv, xlane<1>(sv));   // the row's 16 keys: DPP butterflies inside the lane row
+                mx = fmaxf(mx, xlane<2>(mx));
+                mx = fmaxf(mx, xlane<4>(mx));
+                mx = fmaxf(mx, xlane<8>(mx));
+                const float mn = fmaxf(m_r[i], mx);   // finite: key 0 is in every row's first tile
+                const float sc = expf(m_r[i] - mn), pw = expf(sv - mn);
+                float ps = pw + xlane<1>(pw);
+                ps = ps + xlane<2>(ps);
+                ps = ps + xlane<4>(ps);
+                ps = ps + xlane<8>(ps);
+                l_r[i] = l_r[i] * sc + ps;
+                m_r[i] = mn;
+                p_l[w][4 * q + i][r] = pw;
+#pragma unroll
+                for (int tt = 0; tt < NT; ++tt) O[tt][i] *= sc;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const float4 pa = *reinterpret_cast<const float4 *>(&p_l[w][r][4 * q]);   // P[r][4 q .. 4 q + 3]
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) {
+                const float4 vv = *reinterpret_cast<const float4 *>(&vb[16 * tt + r][4 * q]);   // V[4 q + j][16 tt + r]
+                O[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.x, vv.x, O[tt], 0, 0, 0);
+                O[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.y, vv.y, O[tt], 0, 0, 0);
+                O[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.z, vv.z, O[tt], 0, 0, 0);
+                O[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.w, vv.w, O[tt], 0, 0, 0);
+            }
+        }
+    }
+    if (!active) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qi = i0 + 4 * q + i;
+        if (qi >= n) continue;
+        float *op = out + (size_t)qi * ldo + h * HD + r;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) op[16 * tt] = O[tt][i] / l_r[i];
+    }
 }
 
 // Prefill: the embedding rows of prompt tokens pos0 .. pos0 + n - 1 (one workgroup per token).
@@ -562,8 +680,10 @@ int enqueue_prefill(eif_hip_bitnet *m, int pos0, int n, hipStream_t st)
         EIF_HIP_LAUNCHED();
         auto attn = c.head_dim == 128 ? attn_prefill_kernel<128>
                     : (c.head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<32>);
-        attn<<<dim3(c.n_heads, n), 256, 0, st>>>(m->p_qkv, ldqkv, m->kc + cache_l, m->vc + cache_l, m->p_xb,
-                                                 m->q_dim, pos0, c.n_heads, c.n_kv_heads, c.seq_len, inv_sqrt_hd);
+        const int kv_mul = c.n_heads / c.n_kv_heads, parts = (kv_mul + 3) / 4;
+        attn<<<dim3(c.n_kv_heads * parts, (n + 15) / 16), 64 * std::min(kv_mul, 4), 0, st>>>(
+            m->p_qkv, ldqkv, m->kc + cache_l, m->vc + cache_l, m->p_xb, m->q_dim, pos0, n, c.n_heads, c.n_kv_heads,
+            c.seq_len, inv_sqrt_hd);
         EIF_HIP_LAUNCHED();
         sp = eif_hip_prep_spec{};
         sp.x = m->p_xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l];

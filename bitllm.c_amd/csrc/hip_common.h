@@ -47,6 +47,27 @@ EIF_DEV float eif_wave_sum(float v)
 // (unnormalized output, running maximum, sum) that the next linear's prep combines.
 constexpr int kAttnShares = 8;
 
+// v <- v of lane (l ^ LX): DPP only for LX <= 8 (quad_perm, row_half_mirror, row_mirror compositions).
+template <int LX>
+EIF_DEV float xlane(float v)
+{
+    int i = __float_as_int(v);
+    if constexpr (LX == 1) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0xB1, 0xF, 0xF, false);            // quad_perm [1,0,3,2]
+    } else if constexpr (LX == 2) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0x4E, 0xF, 0xF, false);            // quad_perm [2,3,0,1]
+    } else if constexpr (LX == 4) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);           // row_half_mirror: l ^ 7
+        i = __builtin_amdgcn_update_dpp(0, i, 0x1B, 0xF, 0xF, false);            // quad_perm [3,2,1,0]: ^ 3
+    } else if constexpr (LX == 8) {
+        i = __builtin_amdgcn_update_dpp(0, i, 0x140, 0xF, 0xF, false);           // row_mirror: l ^ 15
+        i = __builtin_amdgcn_update_dpp(0, i, 0x141, 0xF, 0xF, false);           // row_half_mirror: ^ 7
+    } else {
+        return __shfl_xor(v, LX, 64);
+    }
+    return __int_as_float(i);
+}
+
 // Internal launchers shared between translation units (defined in the .hip files).
 namespace eif {
 int launch_prep_rows(const float *x, int ldx, const float *signs, int M, int K, int wht_block, float norm,
