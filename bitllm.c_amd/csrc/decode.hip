@@ -293,14 +293,20 @@ __global__ __launch_bounds__(256) void rope_append_kernel(float *qkv, int ldqkv,
 
 // Prefill, step 2: causal attention of the batch on fp32 MFMAs (v_mfma_f32_16x16x4f32: lane l supplies A[l % 16][l / 16]
 // and B[l / 16][l % 16], and holds D[4 (l / 16) + i][l % 16] in register i). Workgroup (x, y) takes batch tokens
-// [16 y, 16 y + 16) and up to four query heads of kv head g = x / P (P = ceil(kv_mul / 4)), one wave per head. Per
-// 16-key tile: S = Q K^T over the head's dims (lane group q holds dims [q HD/4, (q + 1) HD/4), the same order for Q
-// and K), s = S / sqrt(HD) with keys past the query's position at -inf; per query row the online softmax of the
-// decode (max m, sum l, the outputs rescaled by e^(m - m')); then O += P V with P passed through LDS and the tile's
-// values staged in LDS once for the workgroup (dims x keys, zero past the batch's last key). out = O / l.
+// [16 b, 16 b + 16) (b = y / s_call) and up to four query heads of kv head g = x / P (P = ceil(kv_mul / 4)), one
+// wave per head, over key tiles [kPrefillTiles s, kPrefillTiles (s + 1)) (s = y % s_call) of the block's causal
+// range. Per 16-key tile: S = Q K^T over the head's dims (lane group q holds dims [q HD/4, (q + 1) HD/4), the same
+// order for Q and K), s = S / sqrt(HD) with keys past the query's position at -inf; per query row the online
+// softmax of the decode (max m, sum l, the outputs rescaled by e^(m - m')); then O += P V with P passed through LDS
+// and the tile's values staged in LDS once for the workgroup (dims x keys, zero past the batch's last key). A block
+// whose range is one workgroup's writes out = O / l; a longer one writes each workgroup's share (O, m, l) to
+// po / pml for attn_prefill_combine_kernel.
+constexpr int kPrefillTiles = 8;
+
 template <int HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int ldqkv, const __half *kc,
-                                                           const __half *vc, float *out, int ldo, int pos0, int n,
+                                                           const __half *vc, float *out, int ldo, float *po,
+                                                           float *pml, int s_call, int s_cap, int pos0, int n,
                                                            int n_heads, int n_kv, int seq_len, float inv_sqrt_hd)
 {
     typedef float v4f __attribute__((ext_vector_type(4)));
@@ -312,10 +318,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const bool active = part * 4 + w < kv_mul;   // uniform over the wave
     const int h = g * kv_mul + (active ? part * 4 + w : 0);
-    const int i0 = blockIdx.y * 16, r = lane & 15, q = lane >> 4;
+    const int b = blockIdx.y / s_call, sp = blockIdx.y - b * s_call;
+    const int i0 = b * 16, r = lane & 15, q = lane >> 4;
     const __half *kg = kc + (size_t)g * seq_len * HD, *vg = vc + (size_t)g * seq_len * HD;
     const int n_keys = pos0 + min(i0 + 16, n);   // keys the block's queries may see
-    const int n_tiles = (n_keys + 15) / 16;
+    const int all_tiles = (n_keys + 15) / 16;
+    const int t_begin = sp * kPrefillTiles, n_tiles = min(t_begin + kPrefillTiles, all_tiles);
+    if (t_begin >= n_tiles) return;   // uniform over the workgroup
+    const bool split = all_tiles > kPrefillTiles;
 
     float qv[DQ];   // query row r (batch token i0 + r), dims [DQ q, DQ q + DQ)
     {
@@ -349,8 +359,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int
 #pragma unroll
         for (int j = 0; j < DQ / 8; ++j) kraw[j] = *reinterpret_cast<const uint4 *>(kp + 8 * j);
     };
-    fetch(0);
-    for (int kt = 0; kt < n_tiles; ++kt) {
+    fetch(t_begin);
+    for (int kt = t_begin; kt < n_tiles; ++kt) {
         const int k0 = 16 * kt;
         float(*vb)[VP] = v_l[kt & 1];
 #pragma unroll
@@ -388,8 +398,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int
                 mx = fmaxf(mx, xlane<2>(mx));
                 mx = fmaxf(mx, xlane<4>(mx));
                 mx = fmaxf(mx, xlane<8>(mx));
-                const float mn = fmaxf(m_r[i], mx);   // finite: key 0 is in every row's first tile
-                const float sc = expf(m_r[i] - mn), pw = expf(sv - mn);
+                // mn = -inf only while a share's keys all lie past the query (a split range); the row then
+                // keeps m = -inf, l = 0, O = 0, which weighs 0 in the combine
+                const float mn = fmaxf(m_r[i], mx);
+                const bool none = mn == -INFINITY;
+                const float sc = none ? 1.0f : expf(m_r[i] - mn), pw = none ? 0.0f : expf(sv - mn);
                 float ps = pw + xlane<1>(pw);
                 ps = ps + xlane<2>(ps);
                 ps = ps + xlane<4>(ps);
@@ -419,10 +432,43 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *qkv, int
     for (int i = 0; i < 4; ++i) {
         const int qi = i0 + 4 * q + i;
         if (qi >= n) continue;
-        float *op = out + (size_t)qi * ldo + h * HD + r;
+        if (split) {   // share (b, sp) of query row 4 q + i: [b][s][head][row]
+            const size_t e = (((size_t)b * s_cap + sp) * n_heads + h) * 16 + 4 * q + i;
+            float *op = po + e * HD + r;
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) op[16 * tt] = O[tt][i] / l_r[i];
+            for (int tt = 0; tt < NT; ++tt) op[16 * tt] = O[tt][i];
+            if (r == 0) pml[2 * e] = m_r[i], pml[2 * e + 1] = l_r[i];
+        } else {
+            float *op = out + (size_t)qi * ldo + h * HD + r;
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) op[16 * tt] = O[tt][i] / l_r[i];
+        }
     }
+}
+
+// Prefill, step 3 (blocks whose causal range was split): out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s over the
+// block's shares, M = max_s m_s (a share with m_s = -inf weighs 0). Workgroup (token i, head h), HD threads.
+template <int HD>
+__global__ __launch_bounds__(128) void attn_prefill_combine_kernel(const float *po, const float *pml, float *out,
+                                                                   int ldo, int s_cap, int pos0, int n, int n_heads)
+{
+    const int i = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+    const int b = i / 16, row = i - 16 * b;
+    const int all_tiles = (pos0 + min(16 * b + 16, n) + 15) / 16;
+    if (all_tiles <= kPrefillTiles) return;   // written by the attention kernel
+    const int ns = (all_tiles + kPrefillTiles - 1) / kPrefillTiles;
+    const size_t e0 = ((size_t)b * s_cap * n_heads + h) * 16 + row, es = (size_t)n_heads * 16;
+    float mx = -INFINITY;
+    for (int s2 = 0; s2 < ns; ++s2) mx = fmaxf(mx, pml[2 * (e0 + s2 * es)]);
+    float os = 0.0f, ls = 0.0f;
+    for (int s2 = 0; s2 < ns; ++s2) {
+        const size_t e = e0 + s2 * es;
+        const float ms = pml[2 * e];
+        const float wgt = ms == -INFINITY ? 0.0f : expf(ms - mx);
+        os = fmaf(wgt, po[e * HD + d], os);
+        ls = fmaf(wgt, pml[2 * e + 1], ls);
+    }
+    out[(size_t)i * ldo + h * HD + d] = os / ls;
 }
 
 // Prefill: the embedding rows of prompt tokens pos0 .. pos0 + n - 1 (one workgroup per token).
@@ -546,6 +592,8 @@ struct eif_hip_bitnet {
     // residual x, attention output, qkv, gate|up, a linear's output, int8 rows and their scales
     int pf_cap = 0;
     float *p_x = nullptr, *p_xb = nullptr, *p_qkv = nullptr, *p_h = nullptr, *p_y = nullptr, *p_xs = nullptr;
+    float *p_po = nullptr, *p_pml = nullptr;   // attention shares of split blocks [block][share][head][16][HD | 2]
+    int pf_scap = 0;                           // shares per block the buffers hold
     int8_t *p_xq = nullptr;
     size_t weight_bytes = 0;
     hipGraph_t graph = nullptr;
@@ -619,10 +667,11 @@ int kpad_of(const eif_hip_qweight *w)
 
 void free_prefill(eif_hip_bitnet *m)
 {
-    for (void *p : {(void *)m->p_x, (void *)m->p_xb, (void *)m->p_qkv, (void *)m->p_h, (void *)m->p_y,
+    for (void *p : {(void *)m->p_po, (void *)m->p_pml, (void *)m->p_x, (void *)m->p_xb, (void *)m->p_qkv, (void *)m->p_h, (void *)m->p_y,
                     (void *)m->p_xs, (void *)m->p_xq})
         if (p) (void)hipFree(p);
-    m->p_x = m->p_xb = m->p_qkv = m->p_h = m->p_y = m->p_xs = nullptr;
+    m->p_x = m->p_xb = m->p_qkv = m->p_h = m->p_y = m->p_xs = m->p_po = m->p_pml = nullptr;
+    m->pf_scap = 0;
     m->p_xq = nullptr;
     m->pf_cap = 0;
 }
@@ -645,6 +694,15 @@ int ensure_prefill(eif_hip_bitnet *m, int n)
         free_prefill(m);
         return EIF_HIP_E_NOMEM;
     }
+    // attention shares: up to ceil(ceil(seq_len / 16) / kPrefillTiles) per 16-token block
+    const int scap = ((c.seq_len + 15) / 16 + kPrefillTiles - 1) / kPrefillTiles;
+    const size_t ne = (size_t)((n + 15) / 16) * scap * c.n_heads * 16;
+    if (scap > 1 && (hipMalloc(&m->p_po, sizeof(float) * ne * c.head_dim) != hipSuccess ||
+                     hipMalloc(&m->p_pml, sizeof(float) * ne * 2) != hipSuccess)) {
+        free_prefill(m);
+        return EIF_HIP_E_NOMEM;
+    }
+    m->pf_scap = scap;
     m->pf_cap = n;
     return EIF_HIP_OK;
 }
@@ -681,9 +739,17 @@ int enqueue_prefill(eif_hip_bitnet *m, int pos0, int n, hipStream_t st)
         auto attn = c.head_dim == 128 ? attn_prefill_kernel<128>
                     : (c.head_dim == 64 ? attn_prefill_kernel<64> : attn_prefill_kernel<32>);
         const int kv_mul = c.n_heads / c.n_kv_heads, parts = (kv_mul + 3) / 4;
-        attn<<<dim3(c.n_kv_heads * parts, (n + 15) / 16), 64 * std::min(kv_mul, 4), 0, st>>>(
-            m->p_qkv, ldqkv, m->kc + cache_l, m->vc + cache_l, m->p_xb, m->q_dim, pos0, n, c.n_heads, c.n_kv_heads,
-            c.seq_len, inv_sqrt_hd);
+        const int s_call = ((pos0 + n + 15) / 16 + kPrefillTiles - 1) / kPrefillTiles;   // shares of the longest block
+        attn<<<dim3(c.n_kv_heads * parts, (n + 15) / 16 * s_call), 64 * std::min(kv_mul, 4), 0, st>>>(
+            m->p_qkv, ldqkv, m->kc + cache_l, m->vc + cache_l, m->p_xb, m->q_dim, m->p_po, m->p_pml, s_call,
+            m->pf_scap, pos0, n, c.n_heads, c.n_kv_heads, c.seq_len, inv_sqrt_hd);
+        EIF_HIP_LAUNCHED();
+        if (s_call > 1) {
+            auto comb = c.head_dim == 128 ? attn_prefill_combine_kernel<128>
+                        : (c.head_dim == 64 ? attn_prefill_combine_kernel<64> : attn_prefill_combine_kernel<32>);
+            comb<<<dim3(n, c.n_heads), c.head_dim, 0, st>>>(m->p_po, m->p_pml, m->p_xb, m->q_dim, m->pf_scap, pos0, n,
+                                                            c.n_heads);
+        }
         EIF_HIP_LAUNCHED();
         sp = eif_hip_prep_spec{};
         sp.x = m->p_xb, sp.ldx = m->q_dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l];

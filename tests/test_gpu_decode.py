@@ -220,6 +220,17 @@ def test_prefill_head128_gqa(gpu, oracle):
     check_prefill(gpu, oracle, cfg, w, prompt, [64, 6])
 
 
+def test_prefill_long_split(gpu, oracle):
+    # causal ranges longer than one attention workgroup's (8 tiles of 16 keys) are split and combined: 200 tokens
+    # in one batch, then as two batches of 100 (the second starting mid-tile, where a share may hold no key a
+    # query sees)
+    cfg = synth.bitnet_config(512, 768, 2, 8, 2, 128, 1000, 300, 128, 96, 128, 128, 128)
+    w = synth.bitnet_model((26,), cfg)
+    prompt = list(np.random.default_rng(27).integers(0, cfg["vocab"], 201))
+    check_prefill(gpu, oracle, cfg, w, prompt, [200])
+    check_prefill(gpu, oracle, cfg, w, prompt, [100, 100])
+
+
 def test_prefill_then_greedy(gpu, oracle):
     cfg, w = tiny()
     prompt = list(np.random.default_rng(7).integers(0, cfg["vocab"], 12))
