@@ -398,7 +398,7 @@ def decode_workload(args, torch, bh, synth, np):
            "frac_hbm": round(per_tok * ntok / sec / 1e9 / HBM_PEAK_GBS, 4),
            "launches_per_token": 5 * cfg["n_layers"] + 3, "timing": "HIP graph of one token step, replayed; HIP events",
            "prefill": {"tokens": npr - 1, "ms": round(pre_sec * 1e3, 3), "tok_per_s": round((npr - 1) / pre_sec, 1),
-                       "path": "prep + int8-MFMA GEMM per linear over the batch, causal attention per (head, token)"},
+                       "path": "prep + int8-MFMA GEMM per linear over the batch, causal attention on fp32 MFMAs per (kv head, 16-token block)"},
            "weights_generated_s": round(gen_s, 1), "greedy_tail": [int(t) for t in toks[-8:]]}
     m.close()
     if not args.no_cpu:

@@ -708,8 +708,8 @@ int ensure_prefill(eif_hip_bitnet *m, int n)
 }
 
 // The prompt tokens at positions pos0 .. pos0 + n - 1 as one batch: every linear as prep + MFMA GEMM over the
-// n rows, RoPE + KV append for the batch, causal attention per (head, token), the residual adds; then the head
-// and the sampler for the last token, as its decode step would run them.
+// n rows, RoPE + KV append for the batch, causal attention per 16-token block (shares of long ranges combined),
+// the residual adds; then the head and the sampler for the last token, as its decode step would run them.
 int enqueue_prefill(eif_hip_bitnet *m, int pos0, int n, hipStream_t st)
 {
     const eif_hip_bitnet_config &c = m->c;

@@ -81,8 +81,8 @@ int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream);
 
 /* Runs the next n prompt tokens (positions p .. p + n - 1, all within the prompt) as one batch: every linear
  * through the prep + int8-MFMA GEMM of the n rows (the prefill of tinyllm_forward_batch_embeddings,
- * src/eif_tinyllm.c:930-1500), RoPE and KV append for the batch, causal attention per (head, token). The
- * state afterwards is that of n token steps: the KV cache holds the n positions, the logits are the last
+ * src/eif_tinyllm.c:930-1500), RoPE and KV append for the batch, causal attention on fp32 MFMAs per
+ * 16-token block. The state afterwards is that of n token steps: the KV cache holds the n positions, the logits are the last
  * token's, and the current token is the prompt's next or, at the prompt's end, the argmax. Batch buffers
  * for n tokens are allocated on the first call with that n (not during graph capture).               */
 int eif_hip_bitnet_prefill(eif_hip_bitnet *m, int n, void *stream);
