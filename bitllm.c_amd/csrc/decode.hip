@@ -69,20 +69,18 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
 }
 
 // Softmax attention of one query (q_l, HD floats in LDS) over cache rows 0 .. n_cache - 1 (fp16 [HD] rows at
-// kcg / vcg) and, when k_x is not NULL, one more row (k_x, v_x in LDS) after them; out[0 .. HD) = the result.
-// NT threads. A thread holds 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG
+// kcg / vcg) and, when k_x is not NULL, one more row (k_x, v_x in LDS) after them, as a share of the query's
+// attention (below). NT threads. A thread holds 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG
 // row groups; row group r takes rows r, r + RG, r + 2 RG, ... in batches of UNR rows whose keys and values are
 // loaded together, and keeps a running softmax over them (max m, sum l, the weighted value sums o of its dims):
 //   s_t = (q . k_t) / sqrt(HD), m' = max(m, s_t), l = l e^(m - m') + sum e^(s_t - m'),
 //   o = o e^(m - m') + sum e^(s_t - m') v_t;
-// the row groups are then combined: M = max_r m_r, out = sum_r e^(m_r - M) o_r / sum_r e^(m_r - M) l_r.
-// This is the softmax of the scores followed by the weighted sum of the values, with the sums taken in another
-// order.
-// PARTIAL: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized, out_ml[0] = M, out_ml[kAttnShares] =
-// sum_r e^(m_r - M) l_r (a chunk's share, combined by the next linear's prep).
+// the row groups are then combined, M = max_r m_r: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized,
+// out_ml[0] = M, out_ml[kAttnShares] = sum_r e^(m_r - M) l_r (a chunk's share, combined by the next linear's prep
+// into out / l: the softmax of the scores followed by the weighted sum of the values, the sums in another order).
 // pro(): called once the first batch's loads are issued, before q_l is read (the caller fills q_l, k_x and v_x
 // there and synchronizes the workgroup), so those loads overlap the caller's set-up.
-template <int HD, int NT, bool PARTIAL, class Pro>
+template <int HD, int NT, class Pro>
 EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int n_cache, const float *k_x,
                     const float *v_x, float inv_sqrt_hd, float *out, float *out_ml, Pro &&pro)
 {
@@ -191,12 +189,8 @@ EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int 
         float os = po_l[0][t], ls = pl_l[0];
 #pragma unroll
         for (int q = 1; q < PARTS; ++q) os += po_l[q][t], ls += pl_l[q];
-        if constexpr (PARTIAL) {
-            out[t] = os;
-            if (t == 0) out_ml[0] = mx, out_ml[kAttnShares] = ls;
-        } else {
-            out[t] = os / ls;
-        }
+        out[t] = os;
+        if (t == 0) out_ml[0] = mx, out_ml[kAttnShares] = ls;
     }
 }
 
@@ -257,7 +251,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __hal
     };
     const size_t base = ((size_t)g * seq_len + c0) * HD;
     const int rows = (last ? pos : c0 + ch) - c0;
-    attend<HD, 256, true>(q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr, inv_sqrt_hd,
+    attend<HD, 256>(q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr, inv_sqrt_hd,
                           sh_o + ((size_t)h * kAttnShares + sc) * HD, ml, rotate);
 }
 
