@@ -1,8 +1,8 @@
-// svlm.cpp -- a BitNet-b1.58 model file in the reference's SVLM layout -> the GPU decoder (eif_hip_decode.h).
+// svlm.cpp -- a BitNet-b1.58 model file in the reference's SVLM or TTML layout -> the GPU decoder (eif_hip_decode.h).
 //
 // The file is what tinyllm_load_quantized_model reads (src/eif_tinyllm.c:2442-2556) with the pointer layout of
-// tinyllm_setup_quantized_pointers for BitNet (:2690-2731) and the configuration that the reference's engine
-// reads from it (src/eif_llm.c:321-342):
+// tinyllm_setup_quantized_pointers for BitNet (:2663-2731) and the configuration that the reference's engine
+// reads from it (src/eif_llm.c:321-351). SVLM:
 //   header   12 x u32: [0] 'SVLM', [3] weights offset, [4] scales offset, [5] norms offset, [7] weights bytes,
 //            [8] scales bytes, [9] norms bytes (the other words: version and the vision encoder, unused here)
 //   config   32 x i32 at byte 48: dim, hidden, layers, heads, kv heads, head_dim (0: dim / heads), vocab,
@@ -15,6 +15,15 @@
 //            with the Hadamard flag, the signs of the dim, q_dim and hidden inputs
 //   norms    attention [layers][dim], FFN [layers][dim], final [dim], then the sub-norms [layers][q_dim] and
 //            [layers][hidden] (absent: weight 1)
+// TTML / TLLM (tinyllm_save_quantized_model, src/eif_tinyllm.c:2305-2400): a 36-byte header (magic, version,
+// config, weights, scales and norms sizes) and tinyllm_config_t (dim, hidden, layers, heads, kv heads, vocab,
+// seq_len, qtype, head_dim, rope_interleaved, rope_theta (0: 5e6 above 120000 tokens of vocabulary, 1e5 above
+// 60000, else 1e4, src/eif_tinyllm.c:399), kv_type; the BitNet group fields are not read), then the regions in
+// that order; one scale per row, no rotation.
+// One scale per row without rotation (every TTML file, SVLM with bound 0 and no flag): scales are the embedding's
+// [vocab]; per layer the attention rows' at q 0, k wk, v wv, o wo within a stride of 4 dim + 2 kv_dim (k at
+// dim, v at 2 dim, o at 2 dim + kv_dim), or of q_dim + 2 kv_dim + dim packed when head_dim is set apart from
+// dim / heads (src/eif_tinyllm.c:383-385, :420-422); per layer w1, w3, w2 (:713-787); the head's [vocab].
 // The model's other choices are tinyllm's: rotation blocks eif_hadamard_block_size(width) with the reference
 // build's 1/sqrt(block) (eif_hip_wht_norm), RMSNorm epsilon 1e-6 above 120000 tokens of vocabulary else 1e-5,
 // sub-norm epsilon 1e-5 (src/eif_tinyllm.c:395-410, :660-670, :790-795).
@@ -28,7 +37,7 @@
 
 namespace {
 
-constexpr uint32_t kSvlmMagic = 0x53564C4Du;
+constexpr uint32_t kSvlmMagic = 0x53564C4Du, kTtmlMagic = 0x54544D4Cu, kTllmMagic = 0x544C4C4Du;
 
 struct File {
     FILE *f = nullptr;
@@ -52,18 +61,52 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
     File file;
     file.f = std::fopen(path, "rb");
     if (!file.f) return EIF_HIP_E_ARG;
-    uint32_t hdr[12];
-    int32_t ci[32];
-    if (!read_at(file.f, 0, hdr, sizeof(hdr)) || hdr[0] != kSvlmMagic || !read_at(file.f, 48, ci, sizeof(ci)))
+    uint32_t magic = 0;
+    if (!read_at(file.f, 0, &magic, 4)) return EIF_HIP_E_ARG;
+    int dim, hidden, L, nh, nkv, hd, vocab, file_seq, bound, had;
+    float theta;
+    long w_off, s_off, n_off;
+    size_t w_size, s_size, n_size;
+    if (magic == kSvlmMagic) {
+        uint32_t hdr[12];
+        int32_t ci[32];
+        if (!read_at(file.f, 0, hdr, sizeof(hdr)) || !read_at(file.f, 48, ci, sizeof(ci))) return EIF_HIP_E_ARG;
+        dim = ci[0], hidden = ci[1], L = ci[2], nh = ci[3], nkv = ci[4], vocab = ci[6];
+        hd = ci[5] > 0 ? ci[5] : (nh > 0 ? dim / nh : 0);
+        file_seq = ci[7] > 0 ? ci[7] : 512;
+        bound = ci[14], had = ci[15];
+        theta = 100000.0f;
+        if (ci[12] != 3) return EIF_HIP_E_ARG;
+        w_off = hdr[3], s_off = hdr[4], n_off = hdr[5], w_size = hdr[7], s_size = hdr[8], n_size = hdr[9];
+    } else if (magic == kTtmlMagic || magic == kTllmMagic) {
+        uint32_t hdr[9];
+        int32_t ci[12];
+        if (!read_at(file.f, 0, hdr, sizeof(hdr)) || hdr[2] < sizeof(ci) || !read_at(file.f, 36, ci, sizeof(ci)))
+            return EIF_HIP_E_ARG;
+        dim = ci[0], hidden = ci[1], L = ci[2], nh = ci[3], nkv = ci[4], vocab = ci[5];
+        file_seq = ci[6];
+        hd = ci[8] > 0 ? ci[8] : (nh > 0 ? dim / nh : 0);
+        std::memcpy(&theta, &ci[10], 4);
+        if (!(theta > 0.0f)) theta = vocab > 120000 ? 5000000.0f : (vocab > 60000 ? 100000.0f : 10000.0f);
+        bound = 0, had = 0;
+        if (ci[7] != 3 || ci[9] != 0) return EIF_HIP_E_ARG;   // BitNet only; the decoder rotates half-split pairs
+        w_off = 36 + (long)hdr[2], w_size = hdr[3];
+        s_off = w_off + (long)hdr[3], s_size = hdr[4];
+        n_off = s_off + (long)hdr[4], n_size = hdr[5];
+    } else {
         return EIF_HIP_E_ARG;
-    const int dim = ci[0], hidden = ci[1], L = ci[2], nh = ci[3], nkv = ci[4], vocab = ci[6];
-    const int hd = ci[5] > 0 ? ci[5] : (nh > 0 ? dim / nh : 0);
-    const int bound = ci[14], had = ci[15];
-    if (ci[12] != 3 || dim <= 0 || hidden <= 0 || L <= 0 || nh <= 0 || nkv <= 0 || vocab <= 0 || hd <= 0 ||
-        bound < 0 || (bound == 0 && !had))   // per-row files without the flag use the row-scale layout
+    }
+    if (dim <= 0 || hidden <= 0 || L <= 0 || nh <= 0 || nkv <= 0 || vocab <= 0 || hd <= 0 || bound < 0 ||
+        file_seq <= 0)
         return EIF_HIP_E_ARG;
+    const bool rowwise = bound == 0 && !had;   // the per-row scale layout
     const int q_dim = nh * hd, kv_dim = nkv * hd;
-    const int file_seq = ci[7] > 0 ? ci[7] : 512;
+    const bool explicit_hd = hd != dim / nh;
+    const size_t att_stride = explicit_hd ? (size_t)q_dim + 2 * kv_dim + dim : (size_t)4 * dim + 2 * kv_dim;
+    const size_t att_off[4] = {0, explicit_hd ? (size_t)q_dim : (size_t)dim,
+                               explicit_hd ? (size_t)q_dim + kv_dim : (size_t)2 * dim,
+                               explicit_hd ? (size_t)q_dim + 2 * kv_dim : (size_t)2 * dim + kv_dim};
+    const size_t ffn_stride = (size_t)2 * hidden + dim;
     // group of a kind with input width `in` (0 = one scale per row, as the file stores g = in)
     auto group_of = [&](int in) {
         const int g = bound > 0 ? eif_bitnet_group_size(in, bound) : 0;
@@ -82,11 +125,15 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
                                   {(size_t)hidden, (size_t)dim}, {(size_t)hidden, (size_t)dim},
                                   {(size_t)dim, (size_t)hidden}};   // q, k, v, o, w1, w3, w2 (the scales' order)
     size_t s_count = 2 * (size_t)vocab;
-    for (const auto &ri : rows_in) s_count += (size_t)L * ri[0] * ngroups((int)ri[1]);
-    if (had) s_count += (size_t)dim + q_dim + hidden;
+    if (rowwise) {
+        s_count += (size_t)L * (att_stride + ffn_stride);
+    } else {
+        for (const auto &ri : rows_in) s_count += (size_t)L * ri[0] * ngroups((int)ri[1]);
+        if (had) s_count += (size_t)dim + q_dim + hidden;
+    }
     const size_t n_std = (size_t)L * dim * 2 + dim, n_sub = (size_t)L * (q_dim + hidden);
-    if (hdr[7] < w_bytes || hdr[8] < s_count * sizeof(float) || hdr[9] < n_std * sizeof(float)) return EIF_HIP_E_ARG;
-    const bool subs = hdr[9] >= (n_std + n_sub) * sizeof(float);
+    if (w_size < w_bytes || s_size < s_count * sizeof(float) || n_size < n_std * sizeof(float)) return EIF_HIP_E_ARG;
+    const bool subs = n_size >= (n_std + n_sub) * sizeof(float);
     std::vector<uint8_t> wb;
     std::vector<float> sb, nb;
     try {
@@ -96,15 +143,14 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
     } catch (...) {
         return EIF_HIP_E_NOMEM;
     }
-    if (!read_at(file.f, (long)hdr[3], wb.data(), wb.size()) ||
-        !read_at(file.f, (long)hdr[4], sb.data(), sb.size() * sizeof(float)) ||
-        !read_at(file.f, (long)hdr[5], nb.data(), nb.size() * sizeof(float)))
+    if (!read_at(file.f, w_off, wb.data(), wb.size()) || !read_at(file.f, s_off, sb.data(), sb.size() * sizeof(float)) ||
+        !read_at(file.f, n_off, nb.data(), nb.size() * sizeof(float)))
         return EIF_HIP_E_ARG;
 
     eif_hip_bitnet_config c{};
     c.dim = dim, c.hidden = hidden, c.n_layers = L, c.n_heads = nh, c.n_kv_heads = nkv, c.head_dim = hd;
     c.vocab = vocab, c.seq_len = seq_len > 0 ? seq_len : file_seq;
-    c.rope_theta = 100000.0f;
+    c.rope_theta = theta;
     c.rms_eps = vocab > 120000 ? 1e-6f : 1e-5f;
     c.sub_eps = 1e-5f;
     if (had) {
@@ -138,10 +184,17 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
     const float *sp = sb.data();
     const float *emb_scale = sp;
     sp += vocab;
-    const float *gs[7];
-    for (int k = 0; k < 7; ++k) {
-        gs[k] = sp;
-        sp += (size_t)L * rows_in[k][0] * ngroups((int)rows_in[k][1]);
+    const float *gs[7];   // q, k, v, o, w1, w3, w2: grouped, the kind's first layer; per-row, the layer strides'
+    if (rowwise) {
+        for (int k = 0; k < 4; ++k) gs[k] = sp + att_off[k];
+        sp += (size_t)L * att_stride;
+        gs[4] = sp, gs[5] = sp + hidden, gs[6] = sp + 2 * (size_t)hidden;
+        sp += (size_t)L * ffn_stride;
+    } else {
+        for (int k = 0; k < 7; ++k) {
+            gs[k] = sp;
+            sp += (size_t)L * rows_in[k][0] * ngroups((int)rows_in[k][1]);
+        }
     }
     const float *wcls_scale = sp;
     sp += vocab;
@@ -162,7 +215,9 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
         lw.wo = wo + (size_t)l * dim * qp, lw.w1 = w1 + (size_t)l * hidden * dp, lw.w3 = w3 + (size_t)l * hidden * dp;
         lw.w2 = w2 + (size_t)l * dim * hp;
         const float **g[7] = {&lw.gq, &lw.gk, &lw.gv, &lw.go, &lw.g1, &lw.g3, &lw.g2};
-        for (int k = 0; k < 7; ++k) *g[k] = gs[k] + (size_t)l * rows_in[k][0] * ngroups((int)rows_in[k][1]);
+        for (int k = 0; k < 7; ++k)
+            *g[k] = gs[k] + (size_t)l * (rowwise ? (k < 4 ? att_stride : ffn_stride)
+                                                 : rows_in[k][0] * ngroups((int)rows_in[k][1]));
         lw.rms_att = rms_att + (size_t)l * dim, lw.rms_ffn = rms_ffn + (size_t)l * dim;
         lw.rms_sub_att = sub_att ? sub_att + (size_t)l * q_dim : nullptr;
         lw.rms_sub_ffn = sub_ffn ? sub_ffn + (size_t)l * hidden : nullptr;

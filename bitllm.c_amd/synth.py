@@ -390,3 +390,41 @@ def qwen35_image(cfg, key, sub_norms=True, region_pad=0):
     for region, name, field, at in pending:
         arrays[name][field] = offs[region] + at
     return bytes(img), {k: tuple(v) for k, v in arrays.items()}
+
+
+def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C):
+    """Write a BitNet model with one scale per row (bitnet_model's arrays with every group 0) as a TTML / TLLM file:
+    the 36-byte header and the tinyllm_config_t that tinyllm_save_quantized_model writes (src/eif_tinyllm.c:2305-2313,
+    :2319-2400; read back by src/eif_llm.c:341-351 up to the BitNet group fields), then the weights in SVLM's order
+    and the per-row scale layout of tinyllm_setup_quantized_pointers (src/eif_tinyllm.c:2694-2702) as the decode
+    indexes it (src/eif_tinyllm.c:383-385, :420-422, :713-787): embedding scales [vocab]; per layer the attention
+    scales at q 0, k wk, v wv, o wo within a stride (q_dim + 2 kv_dim + dim when head_dim is set apart from dim /
+    n_heads, else 4 dim + 2 kv_dim with k at dim, v at 2 dim, o at 2 dim + kv_dim); per layer w1, w3, w2; head
+    scales [vocab]. Norms: attention, FFN, final, then the sub-norms."""
+    d, h, L, V = cfg["dim"], cfg["hidden"], cfg["n_layers"], cfg["vocab"]
+    nh, nkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    qd, kvd = nh * hd, nkv * hd
+    assert all(cfg[k] == 0 for k in ("g_q", "g_o", "g_13", "g_2"))
+    weights = b"".join(np.ascontiguousarray(w[k]).tobytes()
+                       for k in ("emb", "wq", "wk", "wv", "wo", "w1", "w2", "w3", "wcls"))
+    explicit = hd != d // nh
+    stride = qd + 2 * kvd + d if explicit else 4 * d + 2 * kvd
+    offs = (0, qd, qd + kvd, qd + 2 * kvd) if explicit else (0, d, 2 * d, 2 * d + kvd)
+    att = np.zeros((L, stride), np.float32)
+    for name, off, rows in (("gq", offs[0], qd), ("gk", offs[1], kvd), ("gv", offs[2], kvd), ("go", offs[3], d)):
+        att[:, off:off + rows] = w[name].reshape(L, rows)
+    ffn = np.concatenate([w["g1"].reshape(L, h), w["g3"].reshape(L, h), w["g2"].reshape(L, d)], axis=1)
+    scales = b"".join(np.ascontiguousarray(a, dtype=np.float32).tobytes()
+                      for a in (w["emb_scale"], att, ffn, w["wcls_scale"]))
+    norms = b"".join(np.ascontiguousarray(w[k], dtype=np.float32).tobytes()
+                     for k in ("rms_att", "rms_ffn", "rms_final", "rms_sub_att", "rms_sub_ffn"))
+    theta = cfg["rope_theta"] if rope_theta is None else rope_theta
+    config = (np.array([d, h, L, nh, nkv, V, cfg["seq_len"], 3, hd, 0], np.int32).tobytes() +
+              np.array([theta], np.float32).tobytes() + np.array([0, 0, 0], np.int32).tobytes())
+    hdr = np.array([magic, 2, len(config), len(weights), len(scales), len(norms), 0, 0, 0], np.uint32)
+    with open(path, "wb") as f:
+        f.write(hdr.tobytes())
+        f.write(config)
+        f.write(weights)
+        f.write(scales)
+        f.write(norms)

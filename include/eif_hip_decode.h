@@ -56,11 +56,13 @@ typedef struct eif_hip_bitnet_globals {    /* host pointers */
     const float *wcls_scale;                /* [vocab] or NULL */
 } eif_hip_bitnet_globals;
 
-/* A BitNet-b1.58 model file in the reference's SVLM layout (what tinyllm_load_quantized_model reads,
- * src/eif_tinyllm.c:2442-2556, laid out as tinyllm_setup_quantized_pointers expects, :2690-2731, configured as
- * src/eif_llm.c:321-342 reads it: RoPE theta 100000, the file's group bound and Hadamard flag) -> a ready model,
- * weights repacked into the GPU layout. seq_len <= 0 takes the file's (512 when it has none). Files of another
- * layout (not BitNet, or neither group scales nor rotation) return EIF_HIP_E_ARG.                      */
+/* A BitNet-b1.58 model file in the reference's SVLM or TTML/TLLM layout (what tinyllm_load_quantized_model
+ * reads, src/eif_tinyllm.c:2442-2556, laid out as tinyllm_setup_quantized_pointers expects, :2663-2731,
+ * configured as src/eif_llm.c:321-351 reads it: SVLM with RoPE theta 100000, the file's group bound and
+ * Hadamard flag; TTML with the file's theta, or tinyllm's default by vocabulary when it is 0, and one scale per
+ * row) -> a ready model, weights repacked into the GPU layout. seq_len <= 0 takes the file's (512 when an SVLM
+ * file has none). Files of another kind (not BitNet, or TTML with RoPE on interleaved pairs) return
+ * EIF_HIP_E_ARG.                                                                                        */
 int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, int seq_len);
 
 /* Allocates the model (weights are set separately). Limits: head_dim 32, 64 or 128, n_heads a multiple of

@@ -128,4 +128,5 @@ REF_TINYLLM_SIGS = {
     "ref_bitnet_forward": (C.POINTER(_f), [_vp, _i, _i]),
     "ref_bitnet_destroy": (None, [_vp]),
     "ref_svlm_create": (_vp, [C.c_char_p]),
+    "ref_ttml_create": (_vp, [C.c_char_p]),
 }

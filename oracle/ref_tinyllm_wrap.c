@@ -108,3 +108,37 @@ void *ref_svlm_create(const char *path)
     }
     return r;
 }
+
+/* A BitNet model from a TTML / TLLM file, configured as the reference's engine reads that format
+ * (src/eif_llm.c:341-351: tinyllm_config_t after the 36-byte header, up to the BitNet group fields) and loaded by
+ * its own tinyllm_load_quantized_model. */
+void *ref_ttml_create(const char *path)
+{
+    FILE *f = fopen(path, "rb");
+    if (!f) return NULL;
+    uint32_t magic = 0;
+    tinyllm_config_t cfg;
+    memset(&cfg, 0, sizeof(cfg));
+    const int ok = fread(&magic, 4, 1, f) == 1 && fseek(f, 36, SEEK_SET) == 0 &&
+                   fread(&cfg, offsetof(tinyllm_config_t, bitnet_group), 1, f) == 1;
+    if (!ok || (magic != 0x54544D4Cu && magic != 0x544C4C4Du)) {
+        fclose(f);
+        return NULL;
+    }
+    uint32_t hdr[9];
+    fseek(f, 0, SEEK_SET);
+    const int ok2 = fread(hdr, 4, 9, f) == 9;
+    fclose(f);
+    if (!ok2) return NULL;
+    ref_bitnet *r = (ref_bitnet *)calloc(1, sizeof(ref_bitnet));
+    if (!r) return NULL;
+    const size_t sz = tinyllm_memory_size(&cfg), wsz = (size_t)hdr[3] + hdr[4] + hdr[5];
+    r->pool = malloc(sz);
+    r->wbuf = malloc(wsz);
+    if (!r->pool || !r->wbuf || tinyllm_init(&r->llm, &cfg, r->pool, sz) != 0 ||
+        tinyllm_load_quantized_model(&r->llm, path, r->wbuf, wsz) != 0) {
+        free(r->pool), free(r->wbuf), free(r);
+        return NULL;
+    }
+    return r;
+}

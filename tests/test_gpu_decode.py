@@ -289,6 +289,35 @@ def test_svlm_file_equals_in_memory(gpu, tmp_path, bound, group):
         mm.close()
 
 
+@pytest.mark.parametrize("head_dim", [32, 64])
+def test_ttml_file_equals_in_memory(gpu, tmp_path, head_dim):
+    """A TTML file (one scale per row, no rotation; head_dim 64 is set apart from dim / heads, which packs the
+    per-layer attention scales) read by eif_hip_bitnet_load_svlm decodes bit for bit as the same arrays set in
+    memory, with the RoPE theta the file carries."""
+    cfg = synth.bitnet_config(128, 256, 2, 4, 2, head_dim, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    w = synth.bitnet_model((14, head_dim), cfg)
+    path = str(tmp_path / "model.ttml")
+    synth.write_ttml(path, cfg, w)
+    mf = gpu.BitnetModel.from_svlm(path)
+    mm = gpu.BitnetModel(cfg, w)
+    try:
+        for k in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "seq_len", "wht_dim",
+                  "wht_q", "wht_hidden", "g_q", "g_o", "g_13", "g_2"):
+            assert mf.cfg[k] == cfg[k], k
+        prompt = [3, 141, 59, 26]
+        out = []
+        for m in (mf, mm):
+            m.reset(prompt)
+            m.prefill(3)
+            m.steps(9, graph=True)
+            out.append((m.tokens(13), m.logits()))
+        assert np.array_equal(out[0][0], out[1][0])
+        assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    finally:
+        mf.close()
+        mm.close()
+
+
 def test_svlm_rejects(gpu, tmp_path):
     cfg, w = tiny()
     path = tmp_path / "m.svlm"
@@ -304,3 +333,20 @@ def test_svlm_rejects(gpu, tmp_path):
         gpu.BitnetModel.from_svlm(str(bad))
     with pytest.raises(gpu.HipError):
         gpu.BitnetModel.from_svlm(str(tmp_path / "missing.svlm"))
+
+
+def test_ttml_rejects(gpu, tmp_path):
+    cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    w = synth.bitnet_model((14, 32), cfg)
+    path = tmp_path / "m.ttml"
+    synth.write_ttml(str(path), cfg, w)
+    for word, value in ((7, 1), (9, 1)):      # qtype INT8; RoPE on interleaved pairs (the decoder's are half-split)
+        raw = bytearray(path.read_bytes())
+        raw[36 + 4 * word] = value
+        bad = tmp_path / "bad.ttml"
+        bad.write_bytes(bytes(raw))
+        with pytest.raises(gpu.HipError):
+            gpu.BitnetModel.from_svlm(str(bad))
+    bad.write_bytes(path.read_bytes()[:2000])  # truncated
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_svlm(str(bad))

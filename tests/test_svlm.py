@@ -72,3 +72,61 @@ def test_svlm_writer_layout(tmp_path):
     assert hdr[8] == 4 * sc
     assert hdr[9] == 4 * (2 * L * d + d + L * (qd + h))
     assert hdr[5] + hdr[9] == len(raw)
+
+
+def ttml_config(head_dim):
+    # one scale per row, no rotation (what a TTML file holds); head_dim 32 = dim / heads, 64 set apart from it
+    cfg = synth.bitnet_config(128, 256, 2, 4, 2, head_dim, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    return cfg, synth.bitnet_model((14, head_dim), cfg)
+
+
+@pytest.mark.parametrize("head_dim", [32, 64])
+def test_ttml_file_read_by_reference(oracle, tmp_path, head_dim):
+    """A TTML file from write_ttml read by the reference itself (its TTML configuration and loader) decodes as the
+    oracle's FP32 decode of the same arrays, to 1e-5 of the logits' magnitude (the reference's per-row GEMV sums in
+    another order than the oracle's one-group form), with the same greedy tokens: every scale and weight sits
+    where the reference looks for it (q, k, v, o at the per-layer offsets, w1, w3, w2, the head)."""
+    if not os.path.exists(REF):
+        pytest.skip("oracle/_ref/libref_scalar.so not built (no reference tree)")
+    ref = oracle_api.load_ref_tinyllm(REF)
+    cfg, w = ttml_config(head_dim)
+    path = str(tmp_path / "model.ttml")
+    synth.write_ttml(path, cfg, w)
+    h = ref.ref_ttml_create(os.fsencode(path))
+    assert h
+    ocfg = dict(cfg, g_q=cfg["dim"], g_o=cfg["n_heads"] * cfg["head_dim"], g_13=cfg["dim"], g_2=cfg["hidden"])
+    c, ws = oracle_api.bitnet_structs(ocfg, w)
+    kv = cfg["n_kv_heads"] * cfg["head_dim"]
+    kc = np.zeros((cfg["n_layers"], cfg["seq_len"], kv), np.float32)
+    vc = np.zeros_like(kc)
+    try:
+        tok = 17
+        for pos in range(12):
+            a = np.ctypeslib.as_array(ref.ref_bitnet_forward(h, tok, pos), shape=(cfg["vocab"],)).copy()
+            lo = np.zeros(cfg["vocab"], np.float32)
+            assert oracle.orc_bitnet_forward(C.byref(c), C.byref(ws), kc.ctypes.data_as(C.c_void_p),
+                                             vc.ctypes.data_as(C.c_void_p), tok, pos, oracle_api.ORC_LIN_F32,
+                                             lo.ctypes.data_as(C.c_void_p)) == 0
+            assert np.abs(a - lo).max() <= 1e-5 * np.abs(lo).max(), pos
+            assert int(np.argmax(a)) == int(np.argmax(lo)), pos
+            tok = int(np.argmax(a))
+    finally:
+        ref.ref_bitnet_destroy(h)
+
+
+def test_ttml_writer_layout(tmp_path):
+    """Header words, configuration words and region sizes as the reader takes them."""
+    cfg, w = ttml_config(32)
+    path = str(tmp_path / "m.ttml")
+    synth.write_ttml(path, cfg, w)
+    raw = open(path, "rb").read()
+    hdr = np.frombuffer(raw[:36], np.uint32)
+    ci = np.frombuffer(raw[36:36 + 48], np.int32)
+    assert hdr[0] == 0x54544D4C and hdr[1] == 2 and hdr[2] == 56
+    assert list(ci[:10]) == [128, 256, 2, 4, 2, 300, 32, 3, 32, 0]
+    assert np.frombuffer(raw[76:80], np.float32)[0] == 10000.0
+    d, h, L, V, kvd = 128, 256, 2, 300, 64
+    assert hdr[3] == 2 * V * d + L * (d * d // 4 * 2 + 2 * kvd * d // 4 + 2 * h * d // 4 + d * h // 4)
+    assert hdr[4] == 4 * (2 * V + L * (4 * d + 2 * kvd + 2 * h + d))
+    assert hdr[5] == 4 * (2 * L * d + d + L * (d + h))
+    assert 36 + hdr[2] + hdr[3] + hdr[4] + hdr[5] == len(raw)
