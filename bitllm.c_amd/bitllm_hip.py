@@ -43,8 +43,21 @@ class BitnetGlobals(C.Structure):
                                     "wcls_scale")]
 
 
+class GgufInfo(C.Structure):
+    """eif_gguf_bitnet_info (include/eif_hip_gguf.h)."""
+    _fields_ = [("arch", C.c_char * 64), ("version", C.c_uint32), ("alignment", C.c_uint32)] + \
+               [(n, _i) for n in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "seq_len")] + \
+               [("rope_theta", _f)] + [(n, _i) for n in ("rope_interleaved", "proj_type", "emb_type", "head_type")]
+
+
 # name: (restype, argtypes) for every exported symbol this module binds.
 _SIGS = {
+    "eif_gguf_bitnet_open": (_i, [C.POINTER(_vp), C.c_char_p]),
+    "eif_gguf_bitnet_close": (None, [_vp]),
+    "eif_gguf_bitnet_get_info": (_i, [_vp, C.POINTER(GgufInfo)]),
+    "eif_gguf_bitnet_get_layer": (_i, [_vp, _i, C.POINTER(BitnetLayer)]),
+    "eif_gguf_bitnet_get_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
+    "eif_hip_bitnet_load_gguf": (_i, [_vp, C.c_char_p, _i]),
     "eif_hip_qlinear_prep": (_i, [_vp, C.POINTER(PrepSpec), _vp, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_prep_acc": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _vp]),
     "eif_hip_prep_spec_rows": (_i, [C.POINTER(PrepSpec), _i, _vp, _i, _vp, _i, _vp]),
@@ -307,6 +320,19 @@ class BitnetModel:
         self.cfg = {k: getattr(self.c, k) for k, _ in BitnetConfig._fields_}
         return self
 
+    @classmethod
+    def from_gguf(cls, path, seq_len=0):
+        """A model read from a BitNet GGUF file (eif_hip_bitnet_load_gguf)."""
+        lib = load()
+        h = C.c_void_p()
+        check(lib.eif_hip_bitnet_load_gguf(C.byref(h), os.fsencode(path), seq_len), "eif_hip_bitnet_load_gguf")
+        self = cls.__new__(cls)
+        self.h = h
+        self.c = BitnetConfig()
+        check(lib.eif_hip_bitnet_get_config(h, C.byref(self.c)), "eif_hip_bitnet_get_config")
+        self.cfg = {k: getattr(self.c, k) for k, _ in BitnetConfig._fields_}
+        return self
+
     def reset(self, prompt, stream=None):
         import numpy as np
         p = np.ascontiguousarray(prompt, dtype=np.int32)
@@ -361,6 +387,82 @@ class BitnetModel:
             self.close()
         except Exception:
             pass
+
+
+class GgufBitnet:
+    """A BitNet GGUF file read and converted on the host (eif_gguf_bitnet_open; no GPU): its configuration and
+    the reference-format arrays, one scale per row, rows as the file holds them."""
+
+    def __init__(self, path):
+        lib = load()
+        h = C.c_void_p()
+        check(lib.eif_gguf_bitnet_open(C.byref(h), os.fsencode(path)), "eif_gguf_bitnet_open")
+        self.h = h
+        self.info = GgufInfo()
+        check(lib.eif_gguf_bitnet_get_info(h, C.byref(self.info)), "eif_gguf_bitnet_get_info")
+
+    def layer(self, l):
+        """Copies of layer l's arrays: w* uint8 [rows, cols / 4], g* float32 [rows], rms_att / rms_ffn [dim]."""
+        import numpy as np
+        lw = BitnetLayer()
+        check(load().eif_gguf_bitnet_get_layer(self.h, l, C.byref(lw)), "eif_gguf_bitnet_get_layer")
+        i = self.info
+        qd, kvd = i.n_heads * i.head_dim, i.n_kv_heads * i.head_dim
+        shapes = {"q": (qd, i.dim), "k": (kvd, i.dim), "v": (kvd, i.dim), "o": (i.dim, qd), "1": (i.hidden, i.dim),
+                  "3": (i.hidden, i.dim), "2": (i.dim, i.hidden)}
+        out = {}
+        for k, (rows, cols) in shapes.items():
+            out["w" + k] = _host_array(getattr(lw, "w" + k), np.uint8, (rows, (cols + 3) // 4))
+            out["g" + k] = _host_array(getattr(lw, "g" + k), np.float32, (rows,))
+        out["rms_att"] = _host_array(lw.rms_att, np.float32, (i.dim,))
+        out["rms_ffn"] = _host_array(lw.rms_ffn, np.float32, (i.dim,))
+        return out
+
+    def globals(self):
+        import numpy as np
+        g = BitnetGlobals()
+        check(load().eif_gguf_bitnet_get_globals(self.h, C.byref(g)), "eif_gguf_bitnet_get_globals")
+        i = self.info
+        return {"emb": _host_array(g.emb, np.int8, (i.vocab, i.dim)),
+                "emb_scale": _host_array(g.emb_scale, np.float32, (i.vocab,)),
+                "rms_final": _host_array(g.rms_final, np.float32, (i.dim,)),
+                "wcls": _host_array(g.wcls, np.int8, (i.vocab, i.dim)),
+                "wcls_scale": _host_array(g.wcls_scale, np.float32, (i.vocab,))}
+
+    def model(self, seq_len=0):
+        """(cfg, w) for BitnetModel(cfg, w): the converted arrays with the decoder configuration
+        eif_hip_bitnet_load_gguf gives them (rows as the file holds them, sub-norms 1)."""
+        import numpy as np
+        i = self.info
+        qd = i.n_heads * i.head_dim
+        cfg = dict(dim=i.dim, hidden=i.hidden, n_layers=i.n_layers, n_heads=i.n_heads, n_kv_heads=i.n_kv_heads,
+                   head_dim=i.head_dim, vocab=i.vocab, seq_len=seq_len if seq_len > 0 else i.seq_len,
+                   rope_theta=i.rope_theta, rms_eps=1e-6 if i.vocab > 120000 else 1e-5, sub_eps=1e-5, wht_dim=0,
+                   wht_q=0, wht_hidden=0, wht_norm_dim=0.0, wht_norm_q=0.0, wht_norm_hidden=0.0, g_q=0, g_o=0,
+                   g_13=0, g_2=0)
+        layers = [self.layer(l) for l in range(i.n_layers)]
+        w = {k: np.concatenate([lay[k] for lay in layers]) for k in layers[0]}
+        w["rms_sub_att"] = np.ones(i.n_layers * qd, np.float32)
+        w["rms_sub_ffn"] = np.ones(i.n_layers * i.hidden, np.float32)
+        w.update(self.globals())
+        return cfg, w
+
+    def close(self):
+        if self.h:
+            load().eif_gguf_bitnet_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _host_array(ptr, dtype, shape):
+    import numpy as np
+    n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+    return np.frombuffer(C.string_at(ptr, n), dtype=dtype).reshape(shape).copy()
 
 
 # ---- Qwen3.5 model files (include/eif_hip_qwen35.h) ----

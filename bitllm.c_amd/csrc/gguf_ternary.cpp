@@ -3,7 +3,9 @@
 //
 // The conversion of the reference's GGUF loader, load_projection_tensor (src/eif_tinyllm.c:3351-3400):
 //   TL1 / TL2 (types 34, 35): 32-column blocks of 10 bytes, an fp16 scale then 8 bytes of 2-bit codes in the
-//     reference's own packing, copied as they are; row scale = sum of the block scales in block order / blocks
+//     reference's own packing, copied as they are; row scale = sum of the block scales in block order times
+//     1 / blocks (the reference's s_sum / blocks as its -ffast-math build computes it: blocks is loop-invariant,
+//     so the division becomes a multiply by the reciprocal)
 //   Q8_0 (type 8): 32-column blocks of 34 bytes, an fp16 scale then 32 int8 values; code +1 / -1 / 0 by the
 //     value's sign; row scale as above
 // The reference copies a TL row's last block whole, past the row's end when cols is not a multiple of 32; here
@@ -13,35 +15,9 @@
 #include <vector>
 
 #include "../../include/eif_hip.h"
+#include "host_formats.h"
 
-namespace {
-
-float half_to_float(uint16_t h)   // IEEE binary16 -> binary32, exact
-{
-    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t exp = (h >> 10) & 0x1Fu, mant = h & 0x3FFu, bits;
-    if (exp == 0) {
-        if (mant == 0) {
-            bits = sign;
-        } else {   // subnormal: normalise
-            int e = -1;
-            do {
-                mant <<= 1;
-                ++e;
-            } while (!(mant & 0x400u));
-            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | ((mant & 0x3FFu) << 13);
-        }
-    } else if (exp == 31) {
-        bits = sign | 0x7F800000u | (mant << 13);
-    } else {
-        bits = sign | ((exp + 112u) << 23) | (mant << 13);
-    }
-    float f;
-    std::memcpy(&f, &bits, 4);
-    return f;
-}
-
-}  // namespace
+using eif::half_to_float;
 
 extern "C" int eif_gguf_ternary_rows(int gguf_type, const void *src, int rows, int cols, uint8_t *codes,
                                      float *scales)
@@ -74,7 +50,7 @@ extern "C" int eif_gguf_ternary_rows(int gguf_type, const void *src, int rows, i
                 }
             }
         }
-        scales[r] = blocks > 0 ? sum / (float)blocks : 1.0f;
+        scales[r] = blocks > 0 ? sum * (1.0f / (float)blocks) : 1.0f;
     }
     return EIF_HIP_OK;
 }

@@ -19,7 +19,8 @@
 // config, weights, scales and norms sizes) and tinyllm_config_t (dim, hidden, layers, heads, kv heads, vocab,
 // seq_len, qtype, head_dim, rope_interleaved, rope_theta (0: 5e6 above 120000 tokens of vocabulary, 1e5 above
 // 60000, else 1e4, src/eif_tinyllm.c:399), kv_type; the BitNet group fields are not read), then the regions in
-// that order; one scale per row, no rotation.
+// that order; one scale per row, no rotation. With rope_interleaved set the rows of wq and wk are reordered
+// within each head for the decoder's half-split pairs (eif::rope_rows_to_half_split).
 // One scale per row without rotation (every TTML file, SVLM with bound 0 and no flag): scales are the embedding's
 // [vocab]; per layer the attention rows' at q 0, k wk, v wv, o wo within a stride of 4 dim + 2 kv_dim (k at
 // dim, v at 2 dim, o at 2 dim + kv_dim), or of q_dim + 2 kv_dim + dim packed when head_dim is set apart from
@@ -33,6 +34,7 @@
 
 #include "../../include/eif_hip.h"
 #include "../../include/eif_hip_decode.h"
+#include "host_formats.h"
 #include "../../include/eif_quantize_bitnet.h"
 
 namespace {
@@ -64,6 +66,7 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
     uint32_t magic = 0;
     if (!read_at(file.f, 0, &magic, 4)) return EIF_HIP_E_ARG;
     int dim, hidden, L, nh, nkv, hd, vocab, file_seq, bound, had;
+    bool interleaved = false;   // RoPE on interleaved pairs (TTML's rope_interleaved)
     float theta;
     long w_off, s_off, n_off;
     size_t w_size, s_size, n_size;
@@ -88,8 +91,8 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
         hd = ci[8] > 0 ? ci[8] : (nh > 0 ? dim / nh : 0);
         std::memcpy(&theta, &ci[10], 4);
         if (!(theta > 0.0f)) theta = vocab > 120000 ? 5000000.0f : (vocab > 60000 ? 100000.0f : 10000.0f);
-        bound = 0, had = 0;
-        if (ci[7] != 3 || ci[9] != 0) return EIF_HIP_E_ARG;   // BitNet only; the decoder rotates half-split pairs
+        bound = 0, had = 0, interleaved = ci[9] != 0;
+        if (ci[7] != 3) return EIF_HIP_E_ARG;   // BitNet only
         w_off = 36 + (long)hdr[2], w_size = hdr[3];
         s_off = w_off + (long)hdr[3], s_size = hdr[4];
         n_off = s_off + (long)hdr[4], n_size = hdr[5];
@@ -198,6 +201,14 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
     }
     const float *wcls_scale = sp;
     sp += vocab;
+    if (interleaved) {   // the decoder rotates half-split pairs: reorder the rows of wq and wk (one scale per row)
+        for (int l = 0; l < L; ++l) {
+            eif::rope_rows_to_half_split(wb.data() + (wq - wb.data()) + (size_t)l * q_dim * dp, dp,
+                                         sb.data() + (gs[0] - sb.data()) + (size_t)l * att_stride, nh, hd);
+            eif::rope_rows_to_half_split(wb.data() + (wk - wb.data()) + (size_t)l * kv_dim * dp, dp,
+                                         sb.data() + (gs[1] - sb.data()) + (size_t)l * att_stride, nkv, hd);
+        }
+    }
     const float *sg_dim = had ? sp : nullptr;
     const float *sg_q = had ? sp + dim : nullptr;
     const float *sg_hidden = had ? sp + dim + q_dim : nullptr;

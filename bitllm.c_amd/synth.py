@@ -392,7 +392,7 @@ def qwen35_image(cfg, key, sub_norms=True, region_pad=0):
     return bytes(img), {k: tuple(v) for k, v in arrays.items()}
 
 
-def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C):
+def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C, interleaved=0):
     """Write a BitNet model with one scale per row (bitnet_model's arrays with every group 0) as a TTML / TLLM file:
     the 36-byte header and the tinyllm_config_t that tinyllm_save_quantized_model writes (src/eif_tinyllm.c:2305-2313,
     :2319-2400; read back by src/eif_llm.c:341-351 up to the BitNet group fields), then the weights in SVLM's order
@@ -400,7 +400,7 @@ def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C):
     indexes it (src/eif_tinyllm.c:383-385, :420-422, :713-787): embedding scales [vocab]; per layer the attention
     scales at q 0, k wk, v wv, o wo within a stride (q_dim + 2 kv_dim + dim when head_dim is set apart from dim /
     n_heads, else 4 dim + 2 kv_dim with k at dim, v at 2 dim, o at 2 dim + kv_dim); per layer w1, w3, w2; head
-    scales [vocab]. Norms: attention, FFN, final, then the sub-norms."""
+    scales [vocab]. Norms: attention, FFN, final, then the sub-norms. interleaved: the rope_interleaved word."""
     d, h, L, V = cfg["dim"], cfg["hidden"], cfg["n_layers"], cfg["vocab"]
     nh, nkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
     qd, kvd = nh * hd, nkv * hd
@@ -419,7 +419,7 @@ def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C):
     norms = b"".join(np.ascontiguousarray(w[k], dtype=np.float32).tobytes()
                      for k in ("rms_att", "rms_ffn", "rms_final", "rms_sub_att", "rms_sub_ffn"))
     theta = cfg["rope_theta"] if rope_theta is None else rope_theta
-    config = (np.array([d, h, L, nh, nkv, V, cfg["seq_len"], 3, hd, 0], np.int32).tobytes() +
+    config = (np.array([d, h, L, nh, nkv, V, cfg["seq_len"], 3, hd, interleaved], np.int32).tobytes() +
               np.array([theta], np.float32).tobytes() + np.array([0, 0, 0], np.int32).tobytes())
     hdr = np.array([magic, 2, len(config), len(weights), len(scales), len(norms), 0, 0, 0], np.uint32)
     with open(path, "wb") as f:
@@ -428,3 +428,151 @@ def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C):
         f.write(weights)
         f.write(scales)
         f.write(norms)
+
+
+# ---- GGUF containers (the reference's GGUF causal-model reader, src/eif_tinyllm.c:2843-3009, :3529-3838) ----
+GGUF_F32, GGUF_F16, GGUF_Q8_0, GGUF_TL1, GGUF_TL2 = 0, 1, 8, 34, 35
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32V, GGUF_BOOL, GGUF_STR, GGUF_ARR, GGUF_U64, \
+    GGUF_I64, GGUF_F64 = range(13)
+_GGUF_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+
+
+def gguf_image(kv, tensors, alignment=32, version=3):
+    """A GGUF container: 'GGUF', version, tensor count, metadata count; the metadata [(key, value type, value)]
+    (an array's value: (element type, [elements])); the tensor table [(name, ggml type, dims with the row length
+    first, raw bytes)] with offsets from the data start, each tensor at a multiple of alignment; the data start
+    at the header's end rounded up to alignment."""
+    import struct
+
+    def string(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    def value(t, v):
+        if t in _GGUF_FMT:
+            return struct.pack(_GGUF_FMT[t], v)
+        if t == GGUF_STR:
+            return string(v)
+        et, items = v
+        return struct.pack("<IQ", et, len(items)) + b"".join(value(et, x) for x in items)
+
+    head = [b"GGUF", struct.pack("<IQQ", version, len(tensors), len(kv))]
+    for k, t, v in kv:
+        head += [string(k), struct.pack("<I", t), value(t, v)]
+    data, off = [], 0
+    for name, ty, dims, raw in tensors:
+        pad = -off % alignment
+        data.append(b"\0" * pad)
+        off += pad
+        head += [string(name), struct.pack("<I", len(dims)), struct.pack(f"<{len(dims)}Q", *dims),
+                 struct.pack("<IQ", ty, off)]
+        data.append(bytes(raw))
+        off += len(raw)
+    h = b"".join(head)
+    return h + b"\0" * (-len(h) % alignment) + b"".join(data)
+
+
+def _fp16_scales(r, n):
+    return (np.abs(r.standard_normal(n)) * 0.02 + 0.004).astype(np.float16)
+
+
+def gguf_ternary_tensor(r, rows, cols, ty):
+    """A BitNet projection as a GGUF tensor: (raw bytes, ternary values [rows, cols], fp16 block scales [rows,
+    cols / 32]). TL1 / TL2: per 32-column
+    block an fp16 scale then the block's 8 bytes of 2-bit codes (the reference's packing, copied by its loader,
+    src/eif_tinyllm.c:3366-3379); Q8_0: an fp16 scale then 32 int8 values, taken by sign (:3380-3402)."""
+    assert cols % 32 == 0
+    nb = cols // 32
+    sc = _fp16_scales(r, rows * nb).reshape(rows, nb)
+    if ty in (GGUF_TL1, GGUF_TL2):
+        v = r.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+        codes = pack_ternary(v).reshape(rows, nb, 8)
+        blk = np.concatenate([sc.view(np.uint8).reshape(rows, nb, 2), codes], axis=2)
+        return blk.tobytes(), v, sc
+    q = r.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+    q[r.uniform(size=q.shape) < 0.2] = 0
+    blk = np.concatenate([sc.view(np.uint8).reshape(rows, nb, 2), q.view(np.uint8).reshape(rows, nb, 32)], axis=2)
+    return blk.tobytes(), np.sign(q).astype(np.int8), sc
+
+
+def gguf_dense_tensor(r, rows, cols, ty):
+    """An embedding / output matrix as a GGUF tensor of type F32, F16 or Q8_0 (raw bytes)."""
+    x = (r.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    x[r.uniform(size=rows) < 0.05] *= 0.0          # some all-zero rows (scale 1)
+    if ty == GGUF_F32:
+        return x.tobytes()
+    if ty == GGUF_F16:
+        return x.astype(np.float16).tobytes()
+    assert cols % 32 == 0
+    nb = cols // 32
+    sc = _fp16_scales(r, rows * nb).reshape(rows, nb)
+    q = r.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+    return np.concatenate([sc.view(np.uint8).reshape(rows, nb, 2), q.view(np.uint8).reshape(rows, nb, 32)],
+                          axis=2).tobytes()
+
+
+def bitnet_gguf(cfg, key, arch="bitnet", proj_types=(GGUF_TL1,), emb_type=GGUF_F16, head_type=None,
+                norm_type=GGUF_F32, alignment=32, rope_theta=None, key_length=False, int_type=GGUF_U32,
+                permute=None, nested=False, kv_edit=None, drop=(), extra_tensors=()):
+    """A BitNet model as a GGUF file image: the metadata the reference reads (<arch>.embedding_length, ...,
+    tokenizer.ggml.tokens) among keys of every value type that it skips, then per layer attn_norm, attn_q/k/v,
+    attn_output, ffn_norm, ffn_gate/up/down, then token_embd, output_norm and, unless head_type is None (tied),
+    output. Projection types cycle through proj_types (the first, blk.0.attn_q, decides BitNet). permute(kind, rows)
+    -> a row order, applied to the q / k tensors (block scales move with their rows): the same draws as another
+    file with its rows reordered. kv_edit(metadata list) -> metadata list; drop: tensor names left out; extra_tensors:
+    more (name, type, dims, raw) at the end. Returns
+    (image, {'L<l>.<kind>': ternary values as written, 'L<l>.<kind>.scales': their fp16 block scales})."""
+    d, h, L, V = cfg["dim"], cfg["hidden"], cfg["n_layers"], cfg["vocab"]
+    nh, nkv, hd = cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    qd, kvd = nh * hd, nkv * hd
+    a = arch + "."
+    kv = [("general.name", GGUF_STR, "synthetic"), ("general.architecture", GGUF_STR, arch),
+          ("general.alignment", GGUF_U32, alignment), ("general.file_type", GGUF_U32, 1),
+          (a + "embedding_length", int_type, d), ("misc.u8", GGUF_U8, 7), ("misc.i16", GGUF_I16, -3),
+          (a + "feed_forward_length", int_type, h), (a + "block_count", int_type, L),
+          ("misc.bool", GGUF_BOOL, True), ("misc.f64", GGUF_F64, 2.5), ("misc.i64", GGUF_I64, -9),
+          (a + "attention.head_count", int_type, nh), (a + "attention.head_count_kv", int_type, nkv),
+          (a + "context_length", int_type, cfg["seq_len"]),
+          (a + "rope.freq_base", GGUF_F32V, cfg["rope_theta"] if rope_theta is None else rope_theta),
+          ("misc.arr_i32", GGUF_ARR, (GGUF_I32, [1, -2, 3])),
+          ("tokenizer.ggml.model", GGUF_STR, "gpt2"),
+          ("tokenizer.ggml.tokens", GGUF_ARR, (GGUF_STR, [f"t{i}" for i in range(V)])),
+          ("tokenizer.ggml.scores", GGUF_ARR, (GGUF_F32V, [0.0] * 4))]
+    if key_length:
+        kv.append((a + "attention.key_length", int_type, hd))
+    if nested:      # an array of arrays (the reference's metadata walk cannot skip one, src/eif_tinyllm.c:3595-3606)
+        kv.insert(3, ("misc.arr_arr", GGUF_ARR, (GGUF_ARR, [(GGUF_U16, [1, 2]), (GGUF_STR, ["x", "yz"])])))
+    if kv_edit is not None:
+        kv = kv_edit(kv)
+    r = rng(*key, 70)
+    tensors, vals = [], {}
+    shapes = (("attn_q", qd, d), ("attn_k", kvd, d), ("attn_v", kvd, d), ("attn_output", d, qd),
+              ("ffn_gate", h, d), ("ffn_up", h, d), ("ffn_down", d, h))
+    i = 0
+    for l in range(L):
+        tensors.append((f"blk.{l}.attn_norm.weight", GGUF_F32, (d,), _norm_bytes(r, d, norm_type)))
+        for kind, rows, cols in shapes:
+            ty = proj_types[i % len(proj_types)]
+            i += 1
+            raw, v, sc = gguf_ternary_tensor(r, rows, cols, ty)
+            if permute is not None and kind in ("attn_q", "attn_k"):
+                order = permute(kind, rows)            # new row i = written row order[i]
+                raw = np.frombuffer(raw, np.uint8).reshape(rows, -1)[order].tobytes()
+                v, sc = v[order], sc[order]
+            vals[f"L{l}.{kind}"] = v
+            vals[f"L{l}.{kind}.scales"] = sc
+            tensors.append((f"blk.{l}.{kind}.weight", ty, (cols, rows), raw))
+            if kind == "attn_v":
+                tensors.append((f"blk.{l}.ffn_norm.weight", GGUF_F32, (d,), _norm_bytes(r, d, norm_type)))
+    for nm, ty in (("token_embd.weight", emb_type), ("output.weight", head_type)):
+        if ty is not None:
+            tensors.append((nm, ty, (d, V), gguf_dense_tensor(r, V, d, ty)))
+    tensors.append(("output_norm.weight", GGUF_F32, (d,), _norm_bytes(r, d, norm_type)))
+    tensors = [(n, (norm_type if n.endswith("norm.weight") else t), dims, raw) for n, t, dims, raw in tensors
+               if n not in drop] + list(extra_tensors)
+    return gguf_image(kv, tensors, alignment=alignment), vals
+
+
+def _norm_bytes(r, n, ty):
+    x = (1.0 + 0.1 * r.standard_normal(n)).astype(np.float32)
+    return x.astype(np.float16).tobytes() if ty == GGUF_F16 else x.tobytes()

@@ -150,7 +150,8 @@ int eif_hip_quant_rows(const float *x, int ldx, int rows, int cols, int bits, ui
 /* BitNet projection tensors of a GGUF file -> the reference's 2-bit ternary rows with one scale per row, as the
  * reference's GGUF loader converts them (load_projection_tensor, src/eif_tinyllm.c:3351-3400): TL1 / TL2
  * (gguf_type 34 / 35: 32-column blocks of an fp16 scale and 8 bytes of codes, copied) or Q8_0 (gguf_type 8:
- * blocks of an fp16 scale and 32 int8 values, coded by sign); scale = the mean of the row's block scales. Host
+ * blocks of an fp16 scale and 32 int8 values, coded by sign); scale = the row's block scales summed in order, times
+ * 1 / blocks (the reference's mean as its -ffast-math build computes it). Host
  * memory in and out: codes [rows, (cols + 3) / 4], scales [rows]. (The reference copies a TL row's last block past
  * the row's end when cols % 32 != 0; this stops at the row's end.)                                      */
 int eif_gguf_ternary_rows(int gguf_type, const void *src, int rows, int cols, uint8_t *codes, float *scales);

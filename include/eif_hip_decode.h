@@ -61,8 +61,9 @@ typedef struct eif_hip_bitnet_globals {    /* host pointers */
  * configured as src/eif_llm.c:321-351 reads it: SVLM with RoPE theta 100000, the file's group bound and
  * Hadamard flag; TTML with the file's theta, or tinyllm's default by vocabulary when it is 0, and one scale per
  * row) -> a ready model, weights repacked into the GPU layout. seq_len <= 0 takes the file's (512 when an SVLM
- * file has none). Files of another kind (not BitNet, or TTML with RoPE on interleaved pairs) return
- * EIF_HIP_E_ARG.                                                                                        */
+ * file has none). A TTML file with rope_interleaved set has the rows of wq and wk reordered within each head for
+ * the decoder's half-split pairs (as eif_hip_bitnet_load_gguf, eif_hip_gguf.h). Files that are not BitNet
+ * return EIF_HIP_E_ARG.                                                                                  */
 int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, int seq_len);
 
 /* Allocates the model (weights are set separately). Limits: head_dim 32, 64 or 128, n_heads a multiple of

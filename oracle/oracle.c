@@ -25,7 +25,8 @@
  *   orc_quant_rows                      numpy float32 restatement, nibble order of test_q35_int4.c:20,
  *                                       closed-form bounds (|x - q s| <= s / 2, the largest |x| at +-qmax)
  *   orc_gguf_ternary_rows               numpy restatement: the codes byte for byte, every fp16 scale value
- *                                       against numpy's binary16, the mean in block order
+ *                                       against numpy's binary16, the block order sum times 1 / blocks;
+ *                                       bit-exact vs the compiled reference's GGUF loader
  */
 #include <math.h>
 #include <stdint.h>
@@ -647,6 +648,8 @@ void orc_gguf_ternary_rows(int type, const uint8_t *src, int rows, int cols, uin
                 }
             }
         }
-        scales[r] = blocks > 0 ? s_sum / blocks : 1.0f;
+        /* the reference as its build compiles it: -ffast-math turns s_sum / blocks, blocks loop-invariant, into a
+         * multiply by the reciprocal (bit-exact vs the compiled reference, tests/test_gguf_model.py) */
+        scales[r] = blocks > 0 ? s_sum * (1.0f / (float)blocks) : 1.0f;
     }
 }

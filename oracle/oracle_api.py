@@ -129,4 +129,6 @@ REF_TINYLLM_SIGS = {
     "ref_bitnet_destroy": (None, [_vp]),
     "ref_svlm_create": (_vp, [C.c_char_p]),
     "ref_ttml_create": (_vp, [C.c_char_p]),
+    "ref_gguf_create": (_vp, [C.c_char_p]),
+    "ref_tinyllm_view": (C.c_int, [_vp, _vp, _vp, _vp]),
 }

@@ -142,3 +142,51 @@ void *ref_ttml_create(const char *path)
     }
     return r;
 }
+
+/* A GGUF causal model read by the reference itself, as its engine does (src/eif_llm.c:312-319, :370-389):
+ * tinyllm_read_gguf_config, tinyllm_init, then tinyllm_load_gguf (src/eif_tinyllm.c:3529) into a zeroed weight
+ * buffer (so regions the loader leaves unwritten compare as zeros). */
+void *ref_gguf_create(const char *path)
+{
+    tinyllm_config_t cfg;
+    char arch[64] = {0};
+    if (tinyllm_read_gguf_config(path, &cfg, arch, sizeof(arch)) != 0) return NULL;
+    FILE *f = fopen(path, "rb");
+    if (!f) return NULL;
+    fseek(f, 0, SEEK_END);
+    const long fsize = ftell(f);
+    fclose(f);
+    ref_bitnet *r = (ref_bitnet *)calloc(1, sizeof(ref_bitnet));
+    if (!r) return NULL;
+    const size_t sz = tinyllm_memory_size(&cfg);
+    const size_t wsz = (size_t)fsize * 8 + (size_t)cfg.vocab_size * cfg.dim * 2 + ((size_t)16 << 20);
+    r->pool = malloc(sz);
+    r->wbuf = calloc(1, wsz);
+    if (!r->pool || !r->wbuf || tinyllm_init(&r->llm, &cfg, r->pool, sz) != 0 ||
+        tinyllm_load_gguf(&r->llm, path, r->wbuf, wsz) != 0) {
+        free(r->pool), free(r->wbuf), free(r);
+        return NULL;
+    }
+    return r;
+}
+
+/* A loaded model's configuration (cfg[0..9]: dim, hidden, layers, heads, kv heads, head_dim, vocab, seq_len,
+ * qtype, rope_interleaved; *theta) and weight pointers (ptrs[0..18]: token_embedding, its scale, wq, wk, wv, wo,
+ * w1, w2, w3, attn_scale, ffn_scale, rms_att, rms_ffn, rms_final, wcls, wcls_scale, rms_sub_att, rms_sub_ffn,
+ * bq), as the decode reads them. */
+int ref_tinyllm_view(void *h, int *cfg, float *theta, const void **ptrs)
+{
+    const tinyllm_t *t = &((ref_bitnet *)h)->llm;
+    const tinyllm_config_t *c = &t->config;
+    const tinyllm_weights_t *w = &t->weights;
+    const int v[10] = {c->dim, c->hidden_dim, c->n_layers, c->n_heads, c->n_kv_heads, c->head_dim, c->vocab_size,
+                       c->seq_len, (int)c->qtype, c->rope_interleaved};
+    memcpy(cfg, v, sizeof(v));
+    *theta = c->rope_theta;
+    const void *p[19] = {w->token_embedding, w->token_embedding_scale, w->wq, w->wk, w->wv, w->wo, w->w1, w->w2,
+                         w->w3, w->attn_scale, w->ffn_scale, w->rms_att_weight, w->rms_ffn_weight,
+                         w->rms_final_weight, w->wcls, w->wcls_scale, w->rms_sub_att_weight, w->rms_sub_ffn_weight,
+                         w->bq};
+    memcpy(ptrs, p, sizeof(p));
+    return 0;
+}

@@ -335,18 +335,116 @@ def test_svlm_rejects(gpu, tmp_path):
         gpu.BitnetModel.from_svlm(str(tmp_path / "missing.svlm"))
 
 
+def _same_decode(models):
+    prompt = [3, 141, 59, 26]
+    out = []
+    for m in models:
+        m.reset(prompt)
+        m.prefill(3)
+        m.steps(9, graph=True)
+        out.append((m.tokens(13), m.logits()))
+    return out
+
+
+GGUF_CASES = {   # (dim, hidden, layers, heads, kv heads, head_dim), writer options
+    "tl1_f16emb_tied": ((128, 256, 2, 4, 2, 32), dict(proj_types=(synth.GGUF_TL1,), emb_type=synth.GGUF_F16)),
+    "mixed_q8head": ((96, 224, 2, 3, 1, 32), dict(proj_types=(synth.GGUF_TL1, synth.GGUF_Q8_0, synth.GGUF_TL2),
+                                                  emb_type=synth.GGUF_F32, head_type=synth.GGUF_Q8_0, alignment=64)),
+    "hd_apart_f16head": ((128, 256, 2, 4, 2, 64), dict(proj_types=(synth.GGUF_TL2,), emb_type=synth.GGUF_Q8_0,
+                                                       head_type=synth.GGUF_F16, key_length=True)),
+}
+
+
+@pytest.mark.parametrize("case", sorted(GGUF_CASES))
+def test_gguf_file_equals_in_memory(gpu, tmp_path, case):
+    """A BitNet GGUF file read by eif_hip_bitnet_load_gguf decodes bit for bit as the arrays eif_gguf_bitnet_open
+    converts from it (those are the reference loader's own, tests/test_gguf_model.py) set in memory."""
+    shape, kw = GGUF_CASES[case]
+    cfg = synth.bitnet_config(*shape, 300, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    img, _ = synth.bitnet_gguf(cfg, (8,), **kw)
+    path = tmp_path / "m.gguf"
+    path.write_bytes(img)
+    g = gpu.GgufBitnet(str(path))
+    mcfg, w = g.model()
+    g.close()
+    mf = gpu.BitnetModel.from_gguf(str(path))
+    mm = gpu.BitnetModel(mcfg, w)
+    try:
+        for k in ("dim", "hidden", "n_layers", "n_heads", "n_kv_heads", "head_dim", "vocab", "seq_len", "g_q",
+                  "g_o", "g_13", "g_2", "wht_dim", "wht_q", "wht_hidden"):
+            assert mf.cfg[k] == mcfg[k] == (cfg[k] if k in cfg else 0), k
+        assert np.float32(mf.cfg["rope_theta"]) == np.float32(10000.0)
+        out = _same_decode((mf, mm))
+        assert np.array_equal(out[0][0], out[1][0])
+        assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    finally:
+        mf.close()
+        mm.close()
+
+
+def test_gguf_interleaved_equals_reordered(gpu, tmp_path):
+    """A llama-architecture GGUF file (RoPE on interleaved pairs) loads as the bitnet-architecture file of the
+    same draws with its q / k rows reordered for half-split pairs, bit for bit (the reference decodes the two as
+    one model, tests/test_gguf_model.py); the rows as drawn, half-split, give other logits."""
+    from test_gguf_model import interleaved_files
+    cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    ms = [gpu.BitnetModel.from_gguf(p) for p in interleaved_files(tmp_path, cfg)]
+    try:
+        out = _same_decode(ms)
+        assert np.array_equal(out[0][0], out[1][0])
+        assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+        assert not np.array_equal(out[0][1], out[2][1])
+    finally:
+        for m in ms:
+            m.close()
+
+
+def test_ttml_interleaved_equals_reordered(gpu, tmp_path):
+    """A TTML file with rope_interleaved set loads as the half-split file whose wq / wk rows (and scales) are
+    reordered within each head, bit for bit."""
+    cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    w = synth.bitnet_model((14, 32), cfg)
+    L, hd = cfg["n_layers"], cfg["head_dim"]
+    w2 = dict(w)
+    for name, heads in (("q", cfg["n_heads"]), ("k", cfg["n_kv_heads"])):
+        h = np.arange(L * heads)[:, None] * hd
+        order = np.concatenate([h + np.arange(0, hd, 2), h + np.arange(1, hd, 2)], axis=1).ravel()
+        w2["w" + name], w2["g" + name] = w["w" + name][order], w["g" + name][order]
+    pa, pb = str(tmp_path / "inter.ttml"), str(tmp_path / "split.ttml")
+    synth.write_ttml(pa, cfg, w, interleaved=1)
+    synth.write_ttml(pb, cfg, w2)
+    ms = [gpu.BitnetModel.from_svlm(p) for p in (pa, pb)]
+    try:
+        out = _same_decode(ms)
+        assert np.array_equal(out[0][0], out[1][0])
+        assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+    finally:
+        for m in ms:
+            m.close()
+
+
+def test_gguf_load_rejects(gpu, tmp_path):
+    cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
+    img, _ = synth.bitnet_gguf(cfg, (8,))
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(img[:len(img) - 1000])
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_gguf(str(bad))
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_gguf(str(tmp_path / "missing.gguf"))
+
+
 def test_ttml_rejects(gpu, tmp_path):
     cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
     w = synth.bitnet_model((14, 32), cfg)
     path = tmp_path / "m.ttml"
     synth.write_ttml(str(path), cfg, w)
-    for word, value in ((7, 1), (9, 1)):      # qtype INT8; RoPE on interleaved pairs (the decoder's are half-split)
-        raw = bytearray(path.read_bytes())
-        raw[36 + 4 * word] = value
-        bad = tmp_path / "bad.ttml"
-        bad.write_bytes(bytes(raw))
-        with pytest.raises(gpu.HipError):
-            gpu.BitnetModel.from_svlm(str(bad))
+    raw = bytearray(path.read_bytes())
+    raw[36 + 4 * 7] = 1                       # qtype INT8: not a BitNet model
+    bad = tmp_path / "bad.ttml"
+    bad.write_bytes(bytes(raw))
+    with pytest.raises(gpu.HipError):
+        gpu.BitnetModel.from_svlm(str(bad))
     bad.write_bytes(path.read_bytes()[:2000])  # truncated
     with pytest.raises(gpu.HipError):
         gpu.BitnetModel.from_svlm(str(bad))

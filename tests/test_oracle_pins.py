@@ -414,7 +414,7 @@ def test_gguf_ternary_rows(oracle, kind, rows, cols):
         s = np.float32(0.0)
         for b in range(blocks):
             s = np.float32(s + h[i, b].view(np.float16).astype(np.float32))
-        want_sc[i] = np.float32(s / np.float32(blocks))
+        want_sc[i] = np.float32(s * (np.float32(1.0) / np.float32(blocks)))   # the reference build's mean
     assert np.array_equal(sc.view(np.uint32), want_sc.view(np.uint32))
     if kind == 8:
         q = raw[:, :, 2:].view(np.int8).reshape(rows, -1)[:, :cols]
@@ -439,7 +439,7 @@ def test_gguf_fp16_scales_every_value(oracle):
     sc = np.zeros(rows, np.float32)
     oracle.orc_gguf_ternary_rows(34, P(raw), rows, 32, P(codes), P(sc))
     want = np.arange(rows, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
-    want = (np.float32(0.0) + want) / np.float32(1.0)   # the mean's sum starts at +0 (so -0 becomes +0)
+    want = (np.float32(0.0) + want) * np.float32(1.0)   # the mean's sum starts at +0 (so -0 becomes +0)
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(sc), nan)
     assert np.array_equal(sc[~nan].view(np.uint32), want[~nan].view(np.uint32))

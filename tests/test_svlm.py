@@ -130,3 +130,39 @@ def test_ttml_writer_layout(tmp_path):
     assert hdr[4] == 4 * (2 * V + L * (4 * d + 2 * kvd + 2 * h + d))
     assert hdr[5] == 4 * (2 * L * d + d + L * (d + h))
     assert 36 + hdr[2] + hdr[3] + hdr[4] + hdr[5] == len(raw)
+
+
+def test_ttml_interleaved_rope_is_reordered_rows(tmp_path):
+    """A TTML file with rope_interleaved set decodes in the reference as the same model written half-split with
+    the rows of wq and wk (and their scales) reordered within each head (0, 2, 4, ... then 1, 3, 5, ...), the
+    reordering eif_hip_bitnet_load_svlm applies, to 1e-5 of the logits; the rows as they are, half-split, are
+    another model."""
+    if not os.path.exists(REF):
+        pytest.skip("oracle/_ref/libref_scalar.so not built (no reference tree)")
+    ref = oracle_api.load_ref_tinyllm(REF)
+    cfg, w = ttml_config(32)
+    L, nh, nkv, hd = cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"]
+    w2 = dict(w)
+    for name, heads in (("q", nh), ("k", nkv)):
+        h = np.arange(L * heads)[:, None] * hd
+        order = np.concatenate([h + np.arange(0, hd, 2), h + np.arange(1, hd, 2)], axis=1).ravel()
+        w2["w" + name], w2["g" + name] = w["w" + name][order], w["g" + name][order]
+    paths = [str(tmp_path / n) for n in ("inter.ttml", "split.ttml", "plain.ttml")]
+    synth.write_ttml(paths[0], cfg, w, interleaved=1)
+    synth.write_ttml(paths[1], cfg, w2)
+    synth.write_ttml(paths[2], cfg, w)
+    hs = [ref.ref_ttml_create(os.fsencode(p)) for p in paths]
+    assert all(hs)
+    V = cfg["vocab"]
+    try:
+        tok, worst, apart = 17, 0.0, 0.0
+        for pos in range(10):
+            la, lb, lc = (np.ctypeslib.as_array(ref.ref_bitnet_forward(h, tok, pos), shape=(V,)).copy() for h in hs)
+            worst = max(worst, np.abs(la - lb).max() / np.abs(la).max())
+            apart = max(apart, np.abs(la - lc).max() / np.abs(la).max())
+            assert int(np.argmax(la)) == int(np.argmax(lb)), pos
+            tok = int(np.argmax(la))
+        assert worst <= 1e-5 and apart > 1e-3
+    finally:
+        for h in hs:
+            ref.ref_bitnet_destroy(h)
