@@ -28,7 +28,7 @@
 namespace {
 
 constexpr uint32_t kGgufMagic = 0x46554747u;
-constexpr int kF32 = 0, kF16 = 1, kQ8_0 = 8, kTL1 = 34, kTL2 = 35;
+constexpr int kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ4_1 = 3, kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kTL1 = 34, kTL2 = 35;
 
 struct Mapped {   // the file, memory-mapped read-only
     const uint8_t *p = nullptr;
@@ -137,7 +137,8 @@ struct Tensor {
     uint64_t ne[4] = {1, 1, 1, 1}, offset = 0;
 };
 
-// bytes of a [rows, cols] tensor of ggml type t as the reference strides it (0: a type it is not read as)
+// bytes of a [rows, cols] tensor of ggml type t as the reference strides it (0: a type it is not read as, or a
+// row that is not whole blocks of a type whose rows the reference strides by cols / block)
 uint64_t tensor_bytes(int t, uint64_t rows, uint64_t cols)
 {
     const uint64_t blocks = (cols + 31) / 32;
@@ -146,14 +147,97 @@ uint64_t tensor_bytes(int t, uint64_t rows, uint64_t cols)
     case kF16: return rows * cols * 2;
     case kQ8_0: return rows * blocks * 34;
     case kTL1: case kTL2: return rows * blocks * 10;
+    case kQ4_0: return cols % 32 ? 0 : rows * (cols / 32) * 18;
+    case kQ4_1: return cols % 32 ? 0 : rows * (cols / 32) * 20;
+    case kQ4_K: return cols % 256 ? 0 : rows * (cols / 256) * 144;
+    case kQ6_K: return cols % 256 ? 0 : rows * (cols / 256) * 210;
     default: return 0;
+    }
+}
+
+float half_at(const uint8_t *p)
+{
+    uint16_t h;
+    std::memcpy(&h, p, 2);
+    return eif::half_to_float(h);
+}
+
+// One row of a block-quantized tensor -> floats, ggml's published block layouts, as the reference's dequantisers
+// compute them (src/eif_tinyllm.c:3166-3256). The block fields are fp16, so every product below is exact and
+// each value takes one rounding whatever the order of evaluation.
+//   Q4_0  18 bytes / 32 values: d, then 16 bytes; value j = (low nibble of byte j) - 8, value 16 + j = (high) - 8;
+//         y = q * d
+//   Q4_1  20 bytes / 32 values: d, m, 16 bytes as Q4_0 without the -8; y = q * d + m
+//   Q4_K  144 bytes / 256 values: d, dmin, 12 bytes of eight 6-bit (scale, min) pairs, 128 bytes of nibbles; per
+//         64 values, 32 bytes: their low nibbles with pair 2i, then their high nibbles with pair 2i + 1;
+//         y = (d * scale) * q - dmin * min. Pair j < 4: scale = b[j] & 63, min = b[j + 4] & 63; j >= 4: scale =
+//         (b[j + 4] & 15) | (b[j - 4] >> 6) << 4, min = (b[j + 4] >> 4) | (b[j] >> 6) << 4
+//   Q6_K  210 bytes / 256 values: 128 bytes low nibbles (ql), 64 bytes of 2-bit pairs (qh), 16 int8 scales, d;
+//         per 128 values (ql 64 bytes, qh 32, scales 8), for l < 32 with s = l / 16:
+//         value l      = (ql[l] & 15 | (qh[l] & 3) << 4) - 32,       scale s
+//         value l + 32 = (ql[l + 32] & 15 | (qh[l] >> 2 & 3) << 4) - 32, scale s + 2
+//         value l + 64 = (ql[l] >> 4 | (qh[l] >> 4 & 3) << 4) - 32,     scale s + 4
+//         value l + 96 = (ql[l + 32] >> 4 | (qh[l] >> 6) << 4) - 32,     scale s + 6;   y = (d * scale) * q
+void dequant_row(int type, const uint8_t *b, int cols, float *y)
+{
+    if (type == kQ4_0 || type == kQ4_1) {
+        const int bb = type == kQ4_0 ? 18 : 20;
+        for (int i = 0; i < cols / 32; ++i, b += bb) {
+            const float d = half_at(b), m = type == kQ4_1 ? half_at(b + 2) : 0.0f;
+            const uint8_t *qs = b + bb - 16;
+            for (int j = 0; j < 16; ++j) {
+                const int lo = qs[j] & 15, hi = qs[j] >> 4;
+                if (type == kQ4_0) {
+                    y[32 * i + j] = (float)(lo - 8) * d;
+                    y[32 * i + j + 16] = (float)(hi - 8) * d;
+                } else {
+                    y[32 * i + j] = (float)lo * d + m;
+                    y[32 * i + j + 16] = (float)hi * d + m;
+                }
+            }
+        }
+    } else if (type == kQ4_K) {
+        for (int i = 0; i < cols / 256; ++i, b += 144) {
+            const float d = half_at(b), dmin = half_at(b + 2);
+            const uint8_t *sm = b + 4, *qs = b + 16;
+            float *o = y + 256 * i;
+            for (int j = 0; j < 8; ++j) {
+                int sc, mn;
+                if (j < 4) {
+                    sc = sm[j] & 63, mn = sm[j + 4] & 63;
+                } else {
+                    sc = (sm[j + 4] & 15) | ((sm[j - 4] >> 6) << 4);
+                    mn = (sm[j + 4] >> 4) | ((sm[j] >> 6) << 4);
+                }
+                const float ds = d * (float)sc, dm = dmin * (float)mn;
+                const uint8_t *q = qs + 32 * (j / 2);
+                for (int l = 0; l < 32; ++l) o[32 * j + l] = ds * (float)((j & 1) ? q[l] >> 4 : q[l] & 15) - dm;
+            }
+        }
+    } else {   // Q6_K
+        for (int i = 0; i < cols / 256; ++i, b += 210) {
+            const float d = half_at(b + 208);
+            for (int n = 0; n < 2; ++n) {
+                const uint8_t *ql = b + 64 * n, *qh = b + 128 + 32 * n;
+                const int8_t *sc = reinterpret_cast<const int8_t *>(b + 192) + 8 * n;
+                float *o = y + 256 * i + 128 * n;
+                for (int l = 0; l < 32; ++l) {
+                    const int s = l / 16;
+                    const int q[4] = {((ql[l] & 15) | ((qh[l] & 3) << 4)) - 32,
+                                      ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32,
+                                      ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32,
+                                      ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32};
+                    for (int k = 0; k < 4; ++k) o[32 * k + l] = d * (float)sc[s + 2 * k] * (float)q[k];
+                }
+            }
+        }
     }
 }
 
 // per row: s = max|x| * (1 / 127), q = round-half-away(x * (127 / max|x|)) clamped; s = 1 and q = round(x) when s is
 // below 1e-12 (load_embedding_tensor, quantize_row_f32_to_int8, src/eif_tinyllm.c:3258-3349, as the reference's
-// -ffast-math build computes the source's s = max / 127 and inv = 1 / s); rows of F32, F16 or Q8_0 blocks
-// dequantised first
+// -ffast-math build computes the source's s = max / 127 and inv = 1 / s); rows of F32, F16 or Q8_0 / Q4_0 / Q4_1 /
+// Q4_K / Q6_K blocks dequantised first
 void int8_rows(int type, const uint8_t *src, int rows, int cols, int8_t *q, float *scale)
 {
     std::vector<float> x((size_t)cols);
@@ -168,6 +252,8 @@ void int8_rows(int type, const uint8_t *src, int rows, int cols, int8_t *q, floa
                 std::memcpy(&h, rs + 2 * (size_t)c, 2);
                 x[c] = eif::half_to_float(h);
             }
+        } else if (type != kQ8_0) {   // Q4_0, Q4_1, Q4_K, Q6_K: rows of whole blocks
+            dequant_row(type, src + (size_t)r * tensor_bytes(type, 1, (uint64_t)cols), cols, x.data());
         } else {   // Q8_0: 32-value blocks of an fp16 scale then 32 int8
             const uint8_t *rs = src + (size_t)r * blocks * 34;
             for (size_t b = 0; b < blocks; ++b) {
@@ -403,7 +489,9 @@ int open_model(eif_gguf_bitnet &m, const char *path)
     // embedding and head
     auto int8_tensor = [&](const Tensor *t, std::vector<int8_t> &q, std::vector<float> &s) -> int {
         const uint8_t *src = t ? bytes_of(t, (uint64_t)vocab, (uint64_t)dim) : nullptr;
-        if (!src || (t->type != kF32 && t->type != kF16 && t->type != kQ8_0)) return EIF_HIP_E_ARG;
+        const bool ok = t && (t->type == kF32 || t->type == kF16 || t->type == kQ8_0 || t->type == kQ4_0 ||
+                              t->type == kQ4_1 || t->type == kQ4_K || t->type == kQ6_K);
+        if (!src || !ok) return EIF_HIP_E_ARG;
         try {
             q.resize((size_t)vocab * dim), s.resize(vocab);
         } catch (...) {

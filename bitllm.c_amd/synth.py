@@ -431,7 +431,10 @@ def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C, interleaved=0):
 
 
 # ---- GGUF containers (the reference's GGUF causal-model reader, src/eif_tinyllm.c:2843-3009, :3529-3838) ----
-GGUF_F32, GGUF_F16, GGUF_Q8_0, GGUF_TL1, GGUF_TL2 = 0, 1, 8, 34, 35
+GGUF_F32, GGUF_F16, GGUF_Q4_0, GGUF_Q4_1, GGUF_Q8_0, GGUF_Q4_K, GGUF_Q6_K, GGUF_TL1, GGUF_TL2 = 0, 1, 2, 3, 8, 12, 14, 34, 35
+# bytes per block and values per block of the block types (ggml's published layouts)
+GGUF_BLOCK = {GGUF_Q4_0: (18, 32), GGUF_Q4_1: (20, 32), GGUF_Q8_0: (34, 32), GGUF_Q4_K: (144, 256),
+              GGUF_Q6_K: (210, 256)}
 GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32V, GGUF_BOOL, GGUF_STR, GGUF_ARR, GGUF_U64, \
     GGUF_I64, GGUF_F64 = range(13)
 _GGUF_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
@@ -496,7 +499,29 @@ def gguf_ternary_tensor(r, rows, cols, ty):
 
 
 def gguf_dense_tensor(r, rows, cols, ty):
-    """An embedding / output matrix as a GGUF tensor of type F32, F16 or Q8_0 (raw bytes)."""
+    """An embedding / output matrix as a GGUF tensor (raw bytes): F32, F16, or blocks of Q4_0 (fp16 d, 16 bytes of
+    nibbles: the block's first 16 values low, last 16 high), Q4_1 (fp16 d, fp16 m, 16 bytes), Q8_0 (fp16 d, 32
+    int8), Q4_K (fp16 d, fp16 dmin, 12 bytes of 6-bit scales and mins, 128 bytes of nibbles), Q6_K (128 bytes of
+    low nibbles, 64 of high 2-bit pairs, 16 int8 scales, fp16 d); the codes uniform, the fp16 fields drawn in a
+    range that keeps every value finite."""
+    if ty in (GGUF_Q4_0, GGUF_Q4_1, GGUF_Q4_K, GGUF_Q6_K):
+        bb, bv = GGUF_BLOCK[ty]
+        assert cols % bv == 0
+        nb = rows * (cols // bv)
+        blk = r.integers(0, 256, size=(nb, bb), dtype=np.uint16).astype(np.uint8)
+
+        def f16(lo, hi):
+            return (r.uniform(lo, hi, size=nb) * np.where(r.uniform(size=nb) < 0.5, -1, 1)).astype(
+                np.float16).view(np.uint8).reshape(nb, 2)
+        if ty == GGUF_Q4_0:
+            blk[:, 0:2] = f16(0.001, 0.02)
+        elif ty == GGUF_Q4_1:
+            blk[:, 0:2], blk[:, 2:4] = f16(0.001, 0.02), f16(0.0, 0.1)
+        elif ty == GGUF_Q4_K:
+            blk[:, 0:2], blk[:, 2:4] = f16(0.0001, 0.002), f16(0.0001, 0.002)
+        else:
+            blk[:, 208:210] = f16(0.0001, 0.002)
+        return blk.tobytes()
     x = (r.standard_normal((rows, cols)) * 0.05).astype(np.float32)
     x[r.uniform(size=rows) < 0.05] *= 0.0          # some all-zero rows (scale 1)
     if ty == GGUF_F32:

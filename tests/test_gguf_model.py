@@ -4,7 +4,9 @@ A GGUF file of the test writer (synth.bitnet_gguf) is read both by the reference
 (tinyllm_read_gguf_config, tinyllm_init, tinyllm_load_gguf: src/eif_tinyllm.c:2843-3838, compiled with the
 reference's own flags into oracle/_ref/libref.so), and by eif_gguf_bitnet_open. The configuration and every
 converted array agree bit for bit: 2-bit rows and row scales of TL1 / TL2 / Q8_0 projections, the INT8 embedding
-and head with their row scales from F32, F16 and Q8_0 tensors, the norm weights; over odd block counts, data
+and head with their row scales from F32, F16, Q8_0, Q4_0, Q4_1, Q4_K and Q6_K tensors (a vocabulary of 1200 rows
+for the block types, whose fp16 block fields leave each dequantised value one rounding), the norm weights; over
+odd block counts, data
 alignments, integer value types of the metadata and a head_dim set apart from dim / heads. The codes the reference
 decodes are the writer's ternary values, so the writer lays out what the reference reads. The configuration rules
 (context length default and clamp, RoPE theta defaults, interleaved architectures, the key prefix before
@@ -38,6 +40,7 @@ SHAPES = {   # dim, hidden, layers, heads, kv heads, head_dim (key_length writte
     "d128": (128, 256, 2, 4, 2, 32),
     "odd_blocks": (96, 224, 2, 3, 1, 32),        # 3 and 7 blocks of 32 per row: the mean's 1 / blocks is inexact
     "hd_apart": (128, 256, 2, 4, 2, 64),
+    "d256": (256, 256, 1, 4, 2, 64),            # rows of whole 256-value K-quant blocks
 }
 CASES = {
     "tl1_f16emb": dict(proj_types=(TL1,), emb_type=F16),
@@ -45,10 +48,13 @@ CASES = {
                                 int_type=synth.GGUF_U64),
     "tl2_q8emb_f16head_f16norms": dict(proj_types=(TL2, TL1), emb_type=Q8, head_type=F16, norm_type=F16,
                                        int_type=synth.GGUF_I32),
+    "q4k_emb_q6k_head": dict(proj_types=(TL1,), emb_type=synth.GGUF_Q4_K, head_type=synth.GGUF_Q6_K),
+    "q4_0_emb_q4_1_head": dict(proj_types=(TL2,), emb_type=synth.GGUF_Q4_0, head_type=synth.GGUF_Q4_1),
 }
 
 
 def config(shape, vocab=300, seq_len=64):
+    vocab = 1200 if shape == "d256" else vocab
     d, h, L, nh, nkv, hd = SHAPES[shape]
     return synth.bitnet_config(d, h, L, nh, nkv, hd, vocab, seq_len, 0, 0, 0, 0, 0, rope_theta=10000.0)
 
@@ -106,7 +112,8 @@ def same_bits(a, b):
 
 
 @pytest.mark.parametrize("shape,case", [("d128", "tl1_f16emb"), ("odd_blocks", "mixed_f32emb_q8head"),
-                                        ("hd_apart", "tl2_q8emb_f16head_f16norms"), ("odd_blocks", "tl1_f16emb")])
+                                        ("hd_apart", "tl2_q8emb_f16head_f16norms"), ("odd_blocks", "tl1_f16emb"),
+                                        ("d256", "q4k_emb_q6k_head"), ("d256", "q4_0_emb_q4_1_head")])
 def test_gguf_matches_reference_loader(reft, tmp_path, shape, case):
     cfg = config(shape)
     path, vals = write(tmp_path, cfg, **CASES[case])
@@ -232,6 +239,9 @@ def test_gguf_rejects(reft, tmp_path):
     bad["block_count as f32"] = variant(kv_edit=lambda kv: _set(kv, "bitnet.block_count", synth.GGUF_F32V, 2.0))
     bad["F16 projection"] = variant(drop=("blk.0.attn_v.weight",), extra_tensors=[
         ("blk.0.attn_v.weight", F16, (128, 64), np.zeros(64 * 128, np.float16).tobytes())])
+    bad["Q4_K embedding of part blocks"] = synth.bitnet_gguf(config("odd_blocks"), (3,), drop=("token_embd.weight",),
+                                                           extra_tensors=[("token_embd.weight", synth.GGUF_Q4_K,
+                                                                           (96, 300), bytes(300 * 144))])[0]
     bad["misshapen projection"] = variant(drop=("blk.0.attn_v.weight",), extra_tensors=[
         ("blk.0.attn_v.weight", TL1, (128, 32), bytes(32 * 4 * 10))])
     for name, b in bad.items():

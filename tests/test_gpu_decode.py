@@ -352,6 +352,8 @@ GGUF_CASES = {   # (dim, hidden, layers, heads, kv heads, head_dim), writer opti
                                                   emb_type=synth.GGUF_F32, head_type=synth.GGUF_Q8_0, alignment=64)),
     "hd_apart_f16head": ((128, 256, 2, 4, 2, 64), dict(proj_types=(synth.GGUF_TL2,), emb_type=synth.GGUF_Q8_0,
                                                        head_type=synth.GGUF_F16, key_length=True)),
+    "q4k_emb_q6k_head": ((256, 512, 1, 4, 2, 64), dict(proj_types=(synth.GGUF_TL1,), emb_type=synth.GGUF_Q4_K,
+                                                       head_type=synth.GGUF_Q6_K, key_length=True)),
 }
 
 
