@@ -364,7 +364,8 @@ int open_model(eif_gguf_bitnet &m, const char *path)
     std::vector<Tensor> tensors;
     std::unordered_map<std::string, size_t> index;   // the first tensor of a name, as the reference's search
     try {
-        names.reserve((size_t)n_tensors), tensors.reserve((size_t)n_tensors);
+        const size_t hint = n_tensors < 4096 ? (size_t)n_tensors : 4096;   // the table itself bounds the rest
+        names.reserve(hint), tensors.reserve(hint);
         for (uint64_t i = 0; i < n_tensors && c.ok; ++i) {
             Tensor t;
             names.push_back(c.str());
