@@ -73,6 +73,8 @@ _SIGS = {
     "eif_hip_bitnet_load_svlm": (_i, [_vp, C.c_char_p, _i]),
     "eif_qwen35_parse": (_i, [_vp, _sz, _vp]),
     "eif_hip_qwen35_load": (_i, [_vp, C.c_char_p, _vp]),
+    "eif_qwen35_gguf_image": (_i, [C.c_char_p, _sz, C.POINTER(_vp), C.POINTER(_sz)]),
+    "eif_qwen35_image_free": (None, [_vp]),
     "eif_hip_qwen35_destroy": (None, [_vp]),
     "eif_hip_qwen35_get_layout": (_vp, [_vp]),
     "eif_hip_qwen35_linear": (_vp, [_vp, _i, _i]),
@@ -494,6 +496,17 @@ def qwen35_parse(image):
     lay = Q35Layout()
     check(load().eif_qwen35_parse(C.cast(buf, _vp), len(image), C.byref(lay)), "eif_qwen35_parse")
     return lay
+
+
+def qwen35_gguf_image(gguf_bytes):
+    """The QWN5 image (bytes) of a Qwen3.5 GGUF file's bytes (eif_qwen35_gguf_image; host code, no GPU)."""
+    lib = load()
+    out, n = C.c_void_p(), C.c_size_t()
+    check(lib.eif_qwen35_gguf_image(gguf_bytes, len(gguf_bytes), C.byref(out), C.byref(n)), "eif_qwen35_gguf_image")
+    try:
+        return C.string_at(out, n.value)
+    finally:
+        lib.eif_qwen35_image_free(out)
 
 
 class Qwen35Model:

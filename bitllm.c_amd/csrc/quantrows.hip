@@ -1,8 +1,9 @@
 // quantrows.hip -- FP32 weight rows -> the INT8 / INT4 row-scaled formats of eif_hip_qweight_create, on the GPU.
 //
 // The arithmetic of the reference's GGUF import, quant_rows (src/eif_qwen35_gguf.c:225-258), applied to rows it
-// has dequantised: amax = max(1e-8, max |x|), s = amax / qmax (127 for INT8, 7 for INT4), inv = 1 / s,
-// q = round-half-even(x * inv) clamped to the format's range; INT4 stores columns (2i, 2i+1) in byte i as
+// has dequantised: amax = max(1e-8, max |x|), s = amax * (1 / qmax) (qmax 127 for INT8, 7 for INT4), inv = 1 / s,
+// q = round-half-even(x * inv) clamped to the format's range (the source writes s = amax / qmax; the reference's
+// -ffast-math build multiplies by the reciprocal, which is what its images hold); INT4 stores columns (2i, 2i+1) in byte i as
 // ((a + 8) << 4) | (b + 8), a zero column padding an odd count. A NaN input takes the code the reference's x86
 // conversion gives it after the clamp (the lowest).
 #include "hip_common.h"
@@ -29,8 +30,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float *x, int ldx
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
     const float amax = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-8f);
-    const float qmax = bits == 8 ? 127.0f : 7.0f;
-    const float sc = amax / qmax, inv = 1.0f / sc;
+    const float rq = bits == 8 ? 1.0f / 127.0f : 1.0f / 7.0f;
+    const float sc = amax * rq, inv = 1.0f / sc;
     if (t == 0) scales[r] = sc;
     uint8_t *o = dst + (size_t)r * rb;
     if (bits == 8) {

@@ -314,6 +314,20 @@ extern "C" int eif_hip_qwen35_load(eif_hip_qwen35 **out, const char *path, void 
     }
     std::fclose(f);
     if (!ok) return EIF_HIP_E_ARG;
+    if (img.size() >= 4 && img[0] == 'G' && img[1] == 'G' && img[2] == 'U' && img[3] == 'F') {
+        // a Qwen3.5 GGUF file: its QWN5 image, as the reference's qwen35_load builds it (src/eif_qwen35.c:1236-1246)
+        void *built = nullptr;
+        size_t n = 0;
+        const int rc = eif_qwen35_gguf_image(img.data(), img.size(), &built, &n);
+        if (rc) return rc;
+        try {
+            img.assign(static_cast<uint8_t *>(built), static_cast<uint8_t *>(built) + n);
+        } catch (...) {
+            eif_qwen35_image_free(built);
+            return EIF_HIP_E_NOMEM;
+        }
+        eif_qwen35_image_free(built);
+    }
 
     eif_hip_qwen35 *m = new (std::nothrow) eif_hip_qwen35;
     if (!m) return EIF_HIP_E_NOMEM;

@@ -431,10 +431,11 @@ def write_ttml(path, cfg, w, rope_theta=None, magic=0x54544D4C, interleaved=0):
 
 
 # ---- GGUF containers (the reference's GGUF causal-model reader, src/eif_tinyllm.c:2843-3009, :3529-3838) ----
-GGUF_F32, GGUF_F16, GGUF_Q4_0, GGUF_Q4_1, GGUF_Q8_0, GGUF_Q4_K, GGUF_Q6_K, GGUF_TL1, GGUF_TL2 = 0, 1, 2, 3, 8, 12, 14, 34, 35
+GGUF_F32, GGUF_F16, GGUF_Q4_0, GGUF_Q4_1, GGUF_Q8_0, GGUF_Q4_K, GGUF_Q5_K, GGUF_Q6_K, GGUF_BF16, GGUF_TL1, \
+    GGUF_TL2 = 0, 1, 2, 3, 8, 12, 13, 14, 30, 34, 35
 # bytes per block and values per block of the block types (ggml's published layouts)
 GGUF_BLOCK = {GGUF_Q4_0: (18, 32), GGUF_Q4_1: (20, 32), GGUF_Q8_0: (34, 32), GGUF_Q4_K: (144, 256),
-              GGUF_Q6_K: (210, 256)}
+              GGUF_Q5_K: (176, 256), GGUF_Q6_K: (210, 256)}
 GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32V, GGUF_BOOL, GGUF_STR, GGUF_ARR, GGUF_U64, \
     GGUF_I64, GGUF_F64 = range(13)
 _GGUF_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
@@ -502,9 +503,13 @@ def gguf_dense_tensor(r, rows, cols, ty):
     """An embedding / output matrix as a GGUF tensor (raw bytes): F32, F16, or blocks of Q4_0 (fp16 d, 16 bytes of
     nibbles: the block's first 16 values low, last 16 high), Q4_1 (fp16 d, fp16 m, 16 bytes), Q8_0 (fp16 d, 32
     int8), Q4_K (fp16 d, fp16 dmin, 12 bytes of 6-bit scales and mins, 128 bytes of nibbles), Q6_K (128 bytes of
-    low nibbles, 64 of high 2-bit pairs, 16 int8 scales, fp16 d); the codes uniform, the fp16 fields drawn in a
-    range that keeps every value finite."""
-    if ty in (GGUF_Q4_0, GGUF_Q4_1, GGUF_Q4_K, GGUF_Q6_K):
+    low nibbles, 64 of high 2-bit pairs, 16 int8 scales, fp16 d), Q5_K (fp16 d, fp16 dmin, 12 bytes of scales and
+    mins, 32 bytes of fifth bits, 128 bytes of nibbles), BF16; the codes uniform, the fp16 fields drawn in a range
+    that keeps every value finite."""
+    if ty == GGUF_BF16:
+        x = (r.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        return (x.view(np.uint32) >> 16).astype(np.uint16).tobytes()
+    if ty in (GGUF_Q4_0, GGUF_Q4_1, GGUF_Q4_K, GGUF_Q5_K, GGUF_Q6_K):
         bb, bv = GGUF_BLOCK[ty]
         assert cols % bv == 0
         nb = rows * (cols // bv)
@@ -517,7 +522,7 @@ def gguf_dense_tensor(r, rows, cols, ty):
             blk[:, 0:2] = f16(0.001, 0.02)
         elif ty == GGUF_Q4_1:
             blk[:, 0:2], blk[:, 2:4] = f16(0.001, 0.02), f16(0.0, 0.1)
-        elif ty == GGUF_Q4_K:
+        elif ty in (GGUF_Q4_K, GGUF_Q5_K):
             blk[:, 0:2], blk[:, 2:4] = f16(0.0001, 0.002), f16(0.0001, 0.002)
         else:
             blk[:, 208:210] = f16(0.0001, 0.002)
@@ -601,3 +606,73 @@ def bitnet_gguf(cfg, key, arch="bitnet", proj_types=(GGUF_TL1,), emb_type=GGUF_F
 def _norm_bytes(r, n, ty):
     x = (1.0 + 0.1 * r.standard_normal(n)).astype(np.float32)
     return x.astype(np.float16).tobytes() if ty == GGUF_F16 else x.tobytes()
+
+
+def qwen35_gguf(key, dim=256, hidden=512, n_heads=4, n_kv_heads=2, head_dim=64, vocab=300, heads_k=4, k_dim=32,
+                v_dim=64, conv_k=4, interval=4, ctx=2048, lin_types=(GGUF_Q4_K, GGUF_Q6_K, GGUF_Q8_0, GGUF_Q5_K,
+                                                                        GGUF_Q4_0, GGUF_F16, GGUF_BF16, GGUF_F32),
+                emb_type=GGUF_Q6_K, kv_edit=None, drop=(), extra_tensors=()):
+    """A Qwen3.5 text model as a llama.cpp-style GGUF image (what qwen35_gguf_build_image reads,
+    src/eif_qwen35_gguf.c:262-454): qwen35.* metadata (24 blocks, a full-attention layer every `interval`), the
+    tied token_embd, per DeltaNet layer attn_qkv / attn_gate / ssm_out / ssm_beta / ssm_alpha, ssm_conv1d, ssm_dt.bias,
+    ssm_a (negative), ssm_norm; per attention layer attn_q (with its gate rows) / attn_k / attn_v / attn_output,
+    attn_q_norm / attn_k_norm; per layer ffn_gate / ffn_up / ffn_down, attn_norm, post_attention_norm; output_norm.
+    Linear types cycle through lin_types."""
+    L = 24
+    nv = heads_k
+    key_dim, val_dim = heads_k * k_dim, nv * v_dim
+    conv_dim, q_dim, kv_dim = 2 * key_dim + val_dim, n_heads * head_dim, n_kv_heads * head_dim
+    a = "qwen35."
+    kv = [("general.architecture", GGUF_STR, "qwen35"), ("general.alignment", GGUF_U32, 32),
+          (a + "block_count", GGUF_U32, L), (a + "embedding_length", GGUF_U32, dim),
+          (a + "feed_forward_length", GGUF_U32, hidden), (a + "attention.head_count", GGUF_U32, n_heads),
+          (a + "attention.head_count_kv", GGUF_U32, n_kv_heads), (a + "attention.key_length", GGUF_U32, head_dim),
+          (a + "context_length", GGUF_U64, ctx), (a + "full_attention_interval", GGUF_U32, interval),
+          (a + "attention.layer_norm_rms_epsilon", GGUF_F32V, 1e-6), (a + "ssm.conv_kernel", GGUF_U32, conv_k),
+          (a + "ssm.state_size", GGUF_U32, k_dim), (a + "ssm.group_count", GGUF_U32, heads_k),
+          (a + "ssm.time_step_rank", GGUF_U32, nv), (a + "ssm.inner_size", GGUF_U32, val_dim),
+          ("misc.note", GGUF_STR, "synthetic"), ("tokenizer.ggml.tokens", GGUF_ARR, (GGUF_STR, ["a"] * 4))]
+    if kv_edit is not None:
+        kv = kv_edit(kv)
+    r = rng(*key, 80)
+    tensors = [("token_embd.weight", emb_type, (dim, vocab), gguf_dense_tensor(r, vocab, dim, emb_type))]
+    it = [0]
+
+    def lin(name, rows, cols):
+        ty = lin_types[it[0] % len(lin_types)]
+        it[0] += 1
+        blk = GGUF_BLOCK.get(ty, (0, 1))[1]
+        if cols % blk:
+            ty = GGUF_F16
+        tensors.append((name, ty, (cols, rows), gguf_dense_tensor(r, rows, cols, ty)))
+
+    def vec(name, n, lo=0.5, hi=1.5, dims=None):
+        x = r.uniform(lo, hi, size=n).astype(np.float32)
+        tensors.append((name, GGUF_F32, dims or (n,), x.tobytes()))
+    for l in range(L):
+        b = f"blk.{l}."
+        vec(b + "attn_norm.weight", dim)
+        if (l + 1) % interval:
+            lin(b + "attn_qkv.weight", conv_dim, dim)
+            lin(b + "attn_gate.weight", val_dim, dim)
+            lin(b + "ssm_out.weight", dim, val_dim)
+            lin(b + "ssm_beta.weight", nv, dim)
+            lin(b + "ssm_alpha.weight", nv, dim)
+            vec(b + "ssm_conv1d.weight", conv_dim * conv_k, -0.5, 0.5, dims=(conv_k, conv_dim))
+            vec(b + "ssm_dt.bias", nv, -1.0, 1.0)
+            vec(b + "ssm_a", nv, -8.0, -0.01)
+            vec(b + "ssm_norm.weight", v_dim)
+        else:
+            lin(b + "attn_q.weight", 2 * q_dim, dim)
+            lin(b + "attn_k.weight", kv_dim, dim)
+            lin(b + "attn_v.weight", kv_dim, dim)
+            lin(b + "attn_output.weight", dim, q_dim)
+            vec(b + "attn_q_norm.weight", head_dim)
+            vec(b + "attn_k_norm.weight", head_dim)
+        lin(b + "ffn_gate.weight", hidden, dim)
+        lin(b + "ffn_up.weight", hidden, dim)
+        lin(b + "ffn_down.weight", dim, hidden)
+        vec(b + "post_attention_norm.weight", dim)
+    vec("output_norm.weight", dim)
+    tensors = [t for t in tensors if t[0] not in drop] + list(extra_tensors)
+    return gguf_image(kv, tensors)

@@ -140,8 +140,9 @@ int eif_hip_qlinear_prep_acc(const eif_hip_qweight *w, const eif_hip_prep_spec *
                              void *stream);
 
 /* FP32 weight rows -> the INT8 / INT4 row-scaled formats eif_hip_qweight_create takes, with the arithmetic of the
- * reference's GGUF import, quant_rows (src/eif_qwen35_gguf.c:225-258): per row s = max(1e-8, max |x|) / qmax
- * (qmax 127 for bits 8, 7 for bits 4), q = round-half-even(x * (1 / s)) clamped to [-128, 127] / [-8, 7];
+ * reference's GGUF import, quant_rows (src/eif_qwen35_gguf.c:225-258), as its -ffast-math build computes it: per
+ * row s = max(1e-8, max |x|) * (1 / qmax) (qmax 127 for bits 8, 7 for bits 4), q = round-half-even(x * (1 / s))
+ * clamped to [-128, 127] / [-8, 7];
  * bits 4 packs columns (2i, 2i+1) into byte i as ((a + 8) << 4) | (b + 8), a zero column padding an odd count.
  * x [rows, ldx] FP32, dst [rows, cols or (cols + 1) / 2] bytes and scales [rows], all device memory.   */
 int eif_hip_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8_t *dst, float *scales,

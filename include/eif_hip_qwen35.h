@@ -69,6 +69,17 @@ typedef struct eif_hip_qwen35 eif_hip_qwen35;
 
 /* Read and parse a QWN5 file, upload every quantized linear and the embedding / tied head. Synchronous.       */
 int eif_hip_qwen35_load(eif_hip_qwen35 **out, const char *path, void *stream);
+
+/* A llama.cpp-style Qwen3.5 text GGUF (bytes in memory) -> the QWN5 image the loader reads, as the reference's
+ * qwen35_gguf_build_image builds it (src/eif_qwen35_gguf.c:262-454; eif_hip_qwen35_load calls it for a GGUF path,
+ * as qwen35_load does, src/eif_qwen35.c:1236-1246): F32 / F16 / BF16 / Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K tensors
+ * dequantised, the linears requantised to INT4 rows and the tied embedding to INT8 rows (quant_rows as the
+ * reference's -ffast-math build computes it: s = max(1e-8, max |x|) * (1 / qmax), q = round-half-even(x / s)
+ * through inv = 1 / s), ssm_a stored as A_log = logf(-ssm_a). The builder's limits are the reference's: 24
+ * layers, tied head, as many key as value heads, RMSNorm epsilon 1e-6. Host only. *image is released with
+ * eif_qwen35_image_free.                                                                                 */
+int eif_qwen35_gguf_image(const void *file, size_t bytes, void **image, size_t *image_bytes);
+void eif_qwen35_image_free(void *image);
 void eif_hip_qwen35_destroy(eif_hip_qwen35 *m);
 
 /* The parsed layout (offsets into the file's bytes). */

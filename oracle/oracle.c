@@ -23,7 +23,8 @@
  *   FP32-activation GEMVs, GEMM, softmax  float64 references with the reference tests' bounds
  *                                       (test_int8_gemv.c:10-44, test_q35_int4.c:24-33, test_gemm.c:9-34)
  *   orc_quant_rows                      numpy float32 restatement, nibble order of test_q35_int4.c:20,
- *                                       closed-form bounds (|x - q s| <= s / 2, the largest |x| at +-qmax)
+ *                                       closed-form bounds (|x - q s| <= s / 2, the largest |x| at +-qmax);
+ *                                       bit-exact vs the compiled reference's GGUF image builder
  *   orc_gguf_ternary_rows               numpy restatement: the codes byte for byte, every fp16 scale value
  *                                       against numpy's binary16, the block order sum times 1 / blocks;
  *                                       bit-exact vs the compiled reference's GGUF loader
@@ -569,7 +570,9 @@ int orc_num_threads(void)
 void orc_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8_t *dst, float *scales)
 {
     const size_t rb = bits == 8 ? (size_t)cols : (size_t)(cols + 1) / 2;
-    const float qmax = bits == 8 ? 127.0f : 7.0f;
+    /* s = amax * (1 / qmax): the reference build (-ffast-math) multiplies by the reciprocal where its source divides
+     * (bit-exact vs the images of the compiled qwen35_gguf_build_image, tests/test_qwen35_gguf.py) */
+    const float rq = bits == 8 ? 1.0f / 127.0f : 1.0f / 7.0f;
     for (int r = 0; r < rows; r++) {
         const float *xr = x + (size_t)r * ldx;
         float amax = 1e-8f;
@@ -577,7 +580,7 @@ void orc_quant_rows(const float *x, int ldx, int rows, int cols, int bits, uint8
             const float a = fabsf(xr[c]);
             if (a > amax) amax = a;
         }
-        const float sc = amax / qmax, inv = 1.0f / sc;
+        const float sc = amax * rq, inv = 1.0f / sc;
         scales[r] = sc;
         uint8_t *o = dst + (size_t)r * rb;
         if (bits == 8) {

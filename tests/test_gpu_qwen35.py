@@ -121,3 +121,40 @@ def test_qwen35_load_rejects(gpu, tmp_path):
         gpu.Qwen35Model(str(path))
     with pytest.raises(gpu.HipError):
         gpu.Qwen35Model(str(tmp_path / "missing.eifm"))
+
+
+def test_qwen35_gguf_loads_as_its_image(gpu, tmp_path):
+    """A Qwen3.5 GGUF path given to eif_hip_qwen35_load loads as the QWN5 image eif_qwen35_gguf_image builds from
+    it (the reference's image, tests/test_qwen35_gguf.py): the same layout, every INT4 linear and the INT8 head
+    giving the same output bits, the same FP32 vectors."""
+    gguf = synth.qwen35_gguf((6,), dim=256, hidden=512, vocab=500)
+    pg, pi = tmp_path / "m.gguf", tmp_path / "m.eifm"
+    pg.write_bytes(gguf)
+    pi.write_bytes(gpu.qwen35_gguf_image(gguf))
+    mg, mi = gpu.Qwen35Model(str(pg)), gpu.Qwen35Model(str(pi))
+    try:
+        lg, li = mg.layout, mi.layout
+        assert lg.n_layers == li.n_layers == 24 and list(lg.layer_types[:24]) == list(li.layer_types[:24])
+        n = 0
+        for l in range(24):
+            for k in range(gpu.Q35_KINDS):
+                a, b = mg.linear(l, k), mi.linear(l, k)
+                assert (a is None) == (b is None), (l, k)
+                if a is not None:
+                    same_outputs(gpu, a, b, (l, k))
+                    n += 1
+        assert n == 18 * 5 + 6 * 4 + 24 * 3
+        same_outputs(gpu, mg.head(), mi.head(), (77,))
+        # lengths of the writer's defaults: dim 256, hidden 512, 4 value heads of 64, key 4 x 32, head_dim 64
+        size = {"rms_att": 256, "rms_ffn": 256, "sub_att": 256, "sub_ffn": 512, "conv": 512 * 4, "dt_bias": 4,
+                "a_log": 4, "delta_norm": 64, "q_norm": 64, "k_norm": 64}
+        for l in range(24):
+            for field in VECTORS:
+                off = getattr(lg, field)[l]
+                assert off == getattr(li, field)[l]
+                if off:
+                    np.testing.assert_array_equal(device_floats(mg.vector(off), size[field]),
+                                                  device_floats(mi.vector(off), size[field]))
+    finally:
+        mg.close()
+        mi.close()

@@ -337,13 +337,14 @@ def test_gemm_softmax_vs_double(oracle):
 
 
 def _quant_rows_np(x, bits):
-    """The reference's quant_rows (src/eif_qwen35_gguf.c:225-258) in numpy float32 arithmetic."""
+    """The reference's quant_rows (src/eif_qwen35_gguf.c:225-258) in numpy float32 arithmetic, as its -ffast-math
+    build computes it: s = amax * (1 / qmax) where the source divides."""
     x = np.asarray(x, np.float32)
     rows, cols = x.shape
     qmax = np.float32(127.0 if bits == 8 else 7.0)
     lo, hi = (-128, 127) if bits == 8 else (-8, 7)
     amax = np.maximum(np.abs(x).max(axis=1), np.float32(1e-8)).astype(np.float32)
-    sc = (amax / qmax).astype(np.float32)
+    sc = (amax * (np.float32(1.0) / qmax)).astype(np.float32)
     inv = (np.float32(1.0) / sc).astype(np.float32)
     q = np.clip(np.rint((x * inv[:, None]).astype(np.float32)), lo, hi).astype(np.int32)
     if bits == 8:
@@ -365,7 +366,7 @@ def test_quant_rows(oracle, bits, rows, cols):
     if rows > 1 and cols > 3:
         amax = np.abs(x[1]).max()
         qmax = 127.0 if bits == 8 else 7.0
-        x[1, 1] = np.float32(amax / qmax * 2.5)           # an exact tie at 2.5 -> 2 (half to even)
+        x[1, 1] = np.float32(amax / qmax * 2.5)           # at 2.5 steps: a tie goes to even
     rb = cols if bits == 8 else (cols + 1) // 2
     dst = np.zeros((rows, rb), np.uint8)
     sc = np.zeros(rows, np.float32)
