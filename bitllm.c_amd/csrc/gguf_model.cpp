@@ -332,7 +332,12 @@ extern "C" int eif_gguf_bitnet_open(eif_gguf_bitnet **out, const char *path)
     *out = nullptr;
     eif_gguf_bitnet *m = new (std::nothrow) eif_gguf_bitnet;
     if (!m) return EIF_HIP_E_NOMEM;
-    const int rc = open_model(*m, path);
+    int rc;
+    try {
+        rc = open_model(*m, path);
+    } catch (...) {   // allocation failures of the host-side bookkeeping
+        rc = EIF_HIP_E_NOMEM;
+    }
     if (rc) {
         delete m;
         return rc;

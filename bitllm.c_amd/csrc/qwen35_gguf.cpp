@@ -131,17 +131,24 @@ struct Model {
             work(0, rows);
             return;
         }
+        auto lo_of = [&](int i) { return (int)((int64_t)rows * i / nt); };
         std::vector<std::thread> pool;
-        for (int i = 0; i < nt; ++i) pool.emplace_back(work, (int)((int64_t)rows * i / nt), (int)((int64_t)rows * (i + 1) / nt));
+        int started = 0;
+        try {
+            for (; started < nt; ++started) pool.emplace_back(work, lo_of(started), lo_of(started + 1));
+        } catch (...) {   // no more threads: the caller takes the rest
+        }
+        for (int i = started; i < nt; ++i) work(lo_of(i), lo_of(i + 1));
         for (auto &th : pool) th.join();
     }
 };
 
 }  // namespace
 
-extern "C" int eif_qwen35_gguf_image(const void *file, size_t bytes, void **image, size_t *image_bytes)
+namespace {
+
+int build_image(const void *file, size_t bytes, void **image, size_t *image_bytes)
 {
-    if (!file || !image || !image_bytes) return EIF_HIP_E_ARG;
     *image = nullptr, *image_bytes = 0;
     Cursor c{static_cast<const uint8_t *>(file), bytes};
     if (c.get<uint32_t>() != kMagic) return EIF_HIP_E_ARG;
@@ -242,6 +249,7 @@ extern "C" int eif_qwen35_gguf_image(const void *file, size_t bytes, void **imag
     if (total > 0xFFFFFFFFu) return EIF_HIP_E_LIMIT;
     uint8_t *img = static_cast<uint8_t *>(std::calloc(1, total + 64));
     if (!img) return EIF_HIP_E_NOMEM;
+    *image = img;   // released by the caller's error path from here on
 
     uint32_t hdr[12] = {kQwn5Magic, kQwn5Version, (uint32_t)kHdr, (uint32_t)(kHdr + kCfg + kLt)};
     hdr[4] = hdr[3] + (uint32_t)w_total, hdr[5] = hdr[4] + (uint32_t)s_total, hdr[6] = hdr[5] + (uint32_t)n_total;
@@ -333,12 +341,28 @@ extern "C" int eif_qwen35_gguf_image(const void *file, size_t bytes, void **imag
             m.copy_f32(p + "attn_k_norm.weight", 1, hd, next(np, hd));
         }
     }
-    if (m.bad) {
-        std::free(img);
-        return EIF_HIP_E_ARG;
-    }
-    *image = img, *image_bytes = total;
+    if (m.bad) return EIF_HIP_E_ARG;
+    *image_bytes = total;
     return EIF_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int eif_qwen35_gguf_image(const void *file, size_t bytes, void **image, size_t *image_bytes)
+{
+    if (!file || !image || !image_bytes) return EIF_HIP_E_ARG;
+    *image = nullptr, *image_bytes = 0;
+    int rc;
+    try {
+        rc = build_image(file, bytes, image, image_bytes);
+    } catch (...) {   // allocation failures of the host-side bookkeeping
+        rc = EIF_HIP_E_NOMEM;
+    }
+    if (rc) {
+        std::free(*image);
+        *image = nullptr, *image_bytes = 0;
+    }
+    return rc;
 }
 
 extern "C" void eif_qwen35_image_free(void *image) { std::free(image); }
