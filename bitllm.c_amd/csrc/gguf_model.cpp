@@ -93,6 +93,42 @@ void int8_rows(int type, const uint8_t *src, int rows, int cols, int8_t *q, floa
     }
 }
 
+// Projections of other types ternarized by their absolute mean (load_projection_tensor's BitNet branch,
+// src/eif_tinyllm.c:3403-3461): per row gamma = sum |x| * (1 / cols) (1 below 1e-12), code +1 where
+// x * (1 / gamma) > 0.5, -1 where < -0.5, else 0. The sum is the one the reference's -ffast-math build forms:
+// in column order for F32 / F16 rows, and for rows dequantised from blocks (Q4_0, Q4_1, Q4_K, Q6_K) as eight
+// lane sums over columns c = l (mod 8), added pairwise (lanes l and l + 4, then l and l + 2, then 0 and 1).
+void absmean_rows(int type, const uint8_t *src, int rows, int cols, uint8_t *codes, float *scales)
+{
+    std::vector<float> x((size_t)cols);
+    const size_t rb = (size_t)(cols + 3) / 4;
+    for (int r = 0; r < rows; ++r) {
+        dequant_row(type, src + (size_t)r * tensor_bytes(type, 1, (uint64_t)cols), cols, x.data());
+        float sum = 0.0f;
+        if (type == kF32 || type == kF16) {
+            for (int c = 0; c < cols; ++c) sum += std::fabs(x[c]);
+        } else {   // cols is a multiple of 32
+            float lane[8] = {};
+            for (int c = 0; c < cols; c += 8)
+                for (int l = 0; l < 8; ++l) lane[l] += std::fabs(x[c + l]);
+            for (int w = 4; w >= 1; w >>= 1)
+                for (int l = 0; l < w; ++l) lane[l] += lane[l + w];
+            sum = lane[0];
+        }
+        float gamma = sum * (1.0f / (float)cols);
+        if (gamma < 1e-12f) gamma = 1.0f;
+        scales[r] = gamma;
+        const float inv = 1.0f / gamma;
+        uint8_t *o = codes + (size_t)r * rb;
+        std::memset(o, 0, rb);
+        for (int c = 0; c < cols; ++c) {
+            const float v = x[c] * inv;
+            const uint8_t code = v > 0.5f ? 1 : (v < -0.5f ? 2 : 0);
+            o[c / 4] |= (uint8_t)(code << ((c % 4) * 2));
+        }
+    }
+}
+
 }  // namespace
 
 // kinds in the order of eif_hip_bitnet_layer: q, k, v, o, w1 (gate), w3 (up), w2 (down)
@@ -267,11 +303,16 @@ int open_model(eif_gguf_bitnet &m, const char *path)
                 t = find(name);
             }
             const uint8_t *src = t ? bytes_of(t, shape[k][0], shape[k][1]) : nullptr;
-            if (!src || (t->type != kTL1 && t->type != kTL2 && t->type != kQ8_0)) return EIF_HIP_E_ARG;
-            const int rc = eif_gguf_ternary_rows((int)t->type, src, (int)shape[k][0], (int)shape[k][1],
-                                                 m.codes[k].data() + (size_t)l * m.rows[k] * m.row_bytes[k],
-                                                 m.scales[k].data() + (size_t)l * m.rows[k]);
-            if (rc) return rc;
+            if (!src) return EIF_HIP_E_ARG;
+            uint8_t *codes = m.codes[k].data() + (size_t)l * m.rows[k] * m.row_bytes[k];
+            float *scales = m.scales[k].data() + (size_t)l * m.rows[k];
+            if (t->type == kTL1 || t->type == kTL2 || t->type == kQ8_0) {
+                const int rc = eif_gguf_ternary_rows((int)t->type, src, (int)shape[k][0], (int)shape[k][1], codes,
+                                                     scales);
+                if (rc) return rc;
+            } else {   // F32, F16, Q4_0, Q4_1, Q4_K, Q6_K (bytes_of has taken only these, in whole blocks)
+                absmean_rows((int)t->type, src, (int)shape[k][0], (int)shape[k][1], codes, scales);
+            }
         }
     }
     // norms (load_rmsnorm, src/eif_tinyllm.c:3112-3130): F32 / F16; absent or another type -> 1

@@ -584,8 +584,12 @@ def bitnet_gguf(cfg, key, arch="bitnet", proj_types=(GGUF_TL1,), emb_type=GGUF_F
         for kind, rows, cols in shapes:
             ty = proj_types[i % len(proj_types)]
             i += 1
-            raw, v, sc = gguf_ternary_tensor(r, rows, cols, ty)
+            if ty in (GGUF_TL1, GGUF_TL2, GGUF_Q8_0):
+                raw, v, sc = gguf_ternary_tensor(r, rows, cols, ty)
+            else:               # a dense tensor the reference ternarizes by its absolute mean
+                raw, v, sc = gguf_dense_tensor(r, rows, cols, ty), None, None
             if permute is not None and kind in ("attn_q", "attn_k"):
+                assert v is not None
                 order = permute(kind, rows)            # new row i = written row order[i]
                 raw = np.frombuffer(raw, np.uint8).reshape(rows, -1)[order].tobytes()
                 v, sc = v[order], sc[order]

@@ -12,10 +12,9 @@
  *
  * What is refused (EIF_HIP_E_ARG) where the reference would read out of bounds or produce a model this decoder
  * does not run: a truncated or malformed container, a metadata value of an unexpected type for a key that is
- * read, a missing or misshapen projection, embedding or norm tensor, projections other than TL1 / TL2 / Q8_0
- * (the reference would ternarize F32 / F16 / Q4 projections by absmean), an embedding or output tensor other
- * than F32 / F16 / Q8_0 / Q4_0 / Q4_1 / Q4_K / Q6_K or whose rows are not whole blocks, Q/K/V biases, no token
- * list (vocabulary 0).
+ * read, a missing or misshapen projection, embedding or norm tensor, a tensor of another type than TL1 / TL2 /
+ * Q8_0 / F32 / F16 / Q4_0 / Q4_1 / Q4_K / Q6_K (TL only for projections) or whose rows are not whole blocks, Q/K/V
+ * biases, no token list (vocabulary 0).
  * Host code only; no call here touches the GPU except eif_hip_bitnet_load_gguf.
  */
 #ifndef EIF_HIP_GGUF_H
@@ -49,8 +48,10 @@ typedef struct eif_gguf_bitnet_info {
  *    .attention.head_count_kv (0: head_count), .attention.key_length (0: dim / heads), .context_length (<= 0:
  *    2048, at most 4096), any key holding "rope.freq_base" / "rope_freq_base", the vocabulary from the count of
  *    tokenizer.ggml.tokens; <arch> is the architecture read so far ("llama" before general.architecture);
- *  - projections (TL1 / TL2 blocks copied, Q8_0 by sign; row scale = the block scales summed in order times
- *    1 / blocks): eif_gguf_ternary_rows;
+ *  - projections: TL1 / TL2 blocks copied, Q8_0 by sign, row scale = the block scales summed in order times
+ *    1 / blocks (eif_gguf_ternary_rows); F32 / F16 / Q4_0 / Q4_1 / Q4_K / Q6_K ternarized by the row's absolute
+ *    mean gamma = sum |x| * (1 / cols), code = +1 / -1 where x / gamma > 0.5 / < -0.5 (the sum in the order the
+ *    reference's -ffast-math build forms it: sequential for F32 / F16, eight lanes for block types);
  *  - token_embd.weight and output.weight (else lm_head.weight, else tied): per row s = max|x| * (1 / 127) and
  *    q = round-half-away(x * (127 / max|x|)) clamped to [-128, 127] (s = 1, q = round(x) when s < 1e-12);
  *    Q8_0, Q4_0, Q4_1, Q4_K and Q6_K blocks dequantised first (ggml's block layouts). The reference's source writes s = max / 127, inv = 1 / s and the projections'

@@ -3,7 +3,9 @@
 A GGUF file of the test writer (synth.bitnet_gguf) is read both by the reference itself, as its engine reads one
 (tinyllm_read_gguf_config, tinyllm_init, tinyllm_load_gguf: src/eif_tinyllm.c:2843-3838, compiled with the
 reference's own flags into oracle/_ref/libref.so), and by eif_gguf_bitnet_open. The configuration and every
-converted array agree bit for bit: 2-bit rows and row scales of TL1 / TL2 / Q8_0 projections, the INT8 embedding
+converted array agree bit for bit: 2-bit rows and row scales of TL1 / TL2 / Q8_0 projections and of F32 / F16 / Q4_0
+/ Q4_1 / Q4_K / Q6_K projections ternarized by their absolute mean (odd column counts make the mean's 1 / cols
+inexact; the block types' sum runs over eight lanes as the reference's build forms it), the INT8 embedding
 and head with their row scales from F32, F16, Q8_0, Q4_0, Q4_1, Q4_K and Q6_K tensors (a vocabulary of 1200 rows
 for the block types, whose fp16 block fields leave each dequantised value one rounding), the norm weights; over
 odd block counts, data
@@ -50,6 +52,9 @@ CASES = {
                                        int_type=synth.GGUF_I32),
     "q4k_emb_q6k_head": dict(proj_types=(TL1,), emb_type=synth.GGUF_Q4_K, head_type=synth.GGUF_Q6_K),
     "q4_0_emb_q4_1_head": dict(proj_types=(TL2,), emb_type=synth.GGUF_Q4_0, head_type=synth.GGUF_Q4_1),
+    # projections the reference ternarizes by their absolute mean (the probe stays TL1 / TL2)
+    "absmean_block32": dict(proj_types=(TL1, F32, F16, synth.GGUF_Q4_0, synth.GGUF_Q4_1, Q8, TL2)),
+    "absmean_kquants": dict(proj_types=(TL2, synth.GGUF_Q4_K, synth.GGUF_Q6_K, TL1)),
 }
 
 
@@ -113,7 +118,8 @@ def same_bits(a, b):
 
 @pytest.mark.parametrize("shape,case", [("d128", "tl1_f16emb"), ("odd_blocks", "mixed_f32emb_q8head"),
                                         ("hd_apart", "tl2_q8emb_f16head_f16norms"), ("odd_blocks", "tl1_f16emb"),
-                                        ("d256", "q4k_emb_q6k_head"), ("d256", "q4_0_emb_q4_1_head")])
+                                        ("d256", "q4k_emb_q6k_head"), ("d256", "q4_0_emb_q4_1_head"),
+                                        ("odd_blocks", "absmean_block32"), ("d256", "absmean_kquants")])
 def test_gguf_matches_reference_loader(reft, tmp_path, shape, case):
     cfg = config(shape)
     path, vals = write(tmp_path, cfg, **CASES[case])
@@ -134,7 +140,8 @@ def test_gguf_matches_reference_loader(reft, tmp_path, shape, case):
                 assert same_bits(ours[k], a), (l, k)
             for k, kind in kinds.items():    # the reference decodes the writer's values
                 cols = ours["w" + k].shape[1] * 4
-                assert np.array_equal(synth.unpack_ternary(rlayers[l]["w" + k], cols), vals[f"L{l}.{kind}"]), (l, k)
+                if vals[f"L{l}.{kind}"] is not None:
+                    assert np.array_equal(synth.unpack_ternary(rlayers[l]["w" + k], cols), vals[f"L{l}.{kind}"]), (l, k)
         ours = g.globals()
         for k, a in rglob.items():
             assert same_bits(ours[k], a), k
@@ -237,8 +244,8 @@ def test_gguf_rejects(reft, tmp_path):
         kv_edit=lambda kv: _set(kv, "tokenizer.ggml.tokens", synth.GGUF_ARR, (synth.GGUF_STR, ["t"] * 301)))
     bad["alignment 24"] = variant(kv_edit=lambda kv: _set(kv, "general.alignment", synth.GGUF_U32, 24))
     bad["block_count as f32"] = variant(kv_edit=lambda kv: _set(kv, "bitnet.block_count", synth.GGUF_F32V, 2.0))
-    bad["F16 projection"] = variant(drop=("blk.0.attn_v.weight",), extra_tensors=[
-        ("blk.0.attn_v.weight", F16, (128, 64), np.zeros(64 * 128, np.float16).tobytes())])
+    bad["BF16 projection (a type tinyllm's loader does not read)"] = variant(drop=("blk.0.attn_v.weight",), extra_tensors=[
+        ("blk.0.attn_v.weight", synth.GGUF_BF16, (128, 64), np.zeros(64 * 128, np.uint16).tobytes())])
     bad["Q4_K embedding of part blocks"] = synth.bitnet_gguf(config("odd_blocks"), (3,), drop=("token_embd.weight",),
                                                            extra_tensors=[("token_embd.weight", synth.GGUF_Q4_K,
                                                                            (96, 300), bytes(300 * 144))])[0]

@@ -354,6 +354,8 @@ GGUF_CASES = {   # (dim, hidden, layers, heads, kv heads, head_dim), writer opti
                                                        head_type=synth.GGUF_F16, key_length=True)),
     "q4k_emb_q6k_head": ((256, 512, 1, 4, 2, 64), dict(proj_types=(synth.GGUF_TL1,), emb_type=synth.GGUF_Q4_K,
                                                        head_type=synth.GGUF_Q6_K, key_length=True)),
+    "absmean_projections": ((128, 256, 2, 4, 2, 32), dict(proj_types=(synth.GGUF_TL1, synth.GGUF_F32, synth.GGUF_F16,
+                                                                      synth.GGUF_Q4_0, synth.GGUF_Q4_1))),
 }
 
 
