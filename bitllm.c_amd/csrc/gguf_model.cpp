@@ -239,7 +239,9 @@ int open_model(eif_gguf_bitnet &m, const char *path)
     if (seq > 4096) seq = 4096;
     if (theta <= 0.0f)
         theta = (key_arch.find("qwen") != std::string::npos || std::strstr(path, "qwen")) ? 1000000.0f : 10000.0f;
-    if (dim <= 0 || hidden <= 0 || L <= 0 || nh <= 0 || nkv <= 0 || hd <= 0 || vocab <= 0 || hd % 2) return EIF_HIP_E_ARG;
+    if (dim <= 0 || hidden <= 0 || L <= 0 || nh <= 0 || nkv <= 0 || hd <= 0 || vocab <= 0 || hd % 2 || L > 4096 ||
+        (int64_t)nh * hd > (1 << 30) || (int64_t)nkv * hd > (1 << 30) || dim > (1 << 30) || hidden > (1 << 30))
+        return EIF_HIP_E_ARG;
     std::snprintf(in.arch, sizeof(in.arch), "%s", has_arch ? arch.c_str() : "");
     in.dim = dim, in.hidden = hidden, in.n_layers = L, in.n_heads = nh, in.n_kv_heads = nkv, in.head_dim = hd;
     in.vocab = vocab, in.seq_len = seq, in.rope_theta = theta;
@@ -281,6 +283,27 @@ int open_model(eif_gguf_bitnet &m, const char *path)
                                 {(size_t)hidden, (size_t)dim}, {(size_t)hidden, (size_t)dim},
                                 {(size_t)dim, (size_t)hidden}};
     const char *kind_name[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+    // every tensor is found and lies inside the file before anything is allocated, so the arrays below stay
+    // within a small multiple of the file's size whatever the metadata says
+    char name[160];
+    std::vector<std::pair<const Tensor *, const uint8_t *>> proj((size_t)L * 7);
+    for (int l = 0; l < L; ++l) {
+        for (int k = 0; k < 7; ++k) {
+            std::snprintf(name, sizeof(name), "blk.%d.%s.weight", l, kind_name[k]);
+            const Tensor *t = find(name);
+            if (!t && k == 3) {
+                std::snprintf(name, sizeof(name), "blk.%d.attn_out.weight", l);
+                t = find(name);
+            }
+            const uint8_t *src = t ? bytes_of(t, shape[k][0], shape[k][1]) : nullptr;
+            if (!src) return EIF_HIP_E_ARG;
+            proj[(size_t)l * 7 + k] = {t, src};
+        }
+    }
+    const Tensor *te = find("token_embd.weight"), *th = find("output.weight");
+    if (!th) th = find("lm_head.weight");
+    if (!te || !bytes_of(te, (uint64_t)vocab, (uint64_t)dim) || (th && !bytes_of(th, (uint64_t)vocab, (uint64_t)dim)))
+        return EIF_HIP_E_ARG;
     try {
         for (int k = 0; k < 7; ++k) {
             m.rows[k] = shape[k][0], m.row_bytes[k] = (shape[k][1] + 3) / 4;
@@ -293,17 +316,10 @@ int open_model(eif_gguf_bitnet &m, const char *path)
     } catch (...) {
         return EIF_HIP_E_NOMEM;
     }
-    char name[160];
     for (int l = 0; l < L; ++l) {
         for (int k = 0; k < 7; ++k) {
-            std::snprintf(name, sizeof(name), "blk.%d.%s.weight", l, kind_name[k]);
-            const Tensor *t = find(name);
-            if (!t && k == 3) {
-                std::snprintf(name, sizeof(name), "blk.%d.attn_out.weight", l);
-                t = find(name);
-            }
-            const uint8_t *src = t ? bytes_of(t, shape[k][0], shape[k][1]) : nullptr;
-            if (!src) return EIF_HIP_E_ARG;
+            const Tensor *t = proj[(size_t)l * 7 + k].first;
+            const uint8_t *src = proj[(size_t)l * 7 + k].second;
             uint8_t *codes = m.codes[k].data() + (size_t)l * m.rows[k] * m.row_bytes[k];
             float *scales = m.scales[k].data() + (size_t)l * m.rows[k];
             if (t->type == kTL1 || t->type == kTL2 || t->type == kQ8_0) {
@@ -354,12 +370,9 @@ int open_model(eif_gguf_bitnet &m, const char *path)
         int8_rows((int)t->type, src, vocab, dim, q.data(), s.data());
         return EIF_HIP_OK;
     };
-    const Tensor *te = find("token_embd.weight");
     int rc = int8_tensor(te, m.emb, m.emb_scale);
     if (rc) return rc;
     in.emb_type = (int)te->type;
-    const Tensor *th = find("output.weight");
-    if (!th) th = find("lm_head.weight");
     in.head_type = th ? (int)th->type : -1;
     if (th && (rc = int8_tensor(th, m.head, m.head_scale))) return rc;
     return EIF_HIP_OK;

@@ -102,6 +102,10 @@ extern "C" int eif_qwen35_parse(const void *image, size_t bytes, eif_qwen35_layo
         (out->layer_types[l] ? seen_fa : seen_dn)++;
     }
     if (seen_dn != n_dn || seen_fa != n_fa) return EIF_HIP_E_ARG;
+    const int64_t cap = (int64_t)1 << 26;   // the products below stay far inside int
+    if (dim > cap || hidden > cap || ck > cap || (int64_t)nk * kd > cap || (int64_t)nv * vd > cap ||
+        (int64_t)nh * hd > cap || (int64_t)nkv * hd > cap)
+        return EIF_HIP_E_ARG;
     const int key_dim = nk * kd, val_dim = nv * vd, conv_dim = 2 * key_dim + val_dim;
     const int q_dim = nh * hd, kv_dim = nkv * hd, qg_dim = 2 * q_dim;
     if (g != 0 && (g < 32 || g > 4096 || g % 32 != 0 || qlm != EIF_Q35_TERN2 ||

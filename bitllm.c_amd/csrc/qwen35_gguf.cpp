@@ -224,6 +224,10 @@ int build_image(const void *file, size_t bytes, void **image, size_t *image_byte
     if (L != kLayers || nk != nv || std::fabs(v_eps - 1e-6) > 1e-8 || m.find("output.weight") || dim <= 0 ||
         hidden <= 0 || nh <= 0 || nkv <= 0 || hd <= 0 || ck <= 0 || kd <= 0 || vd <= 0 || interval <= 0)
         return EIF_HIP_E_ARG;
+    const int64_t cap = (int64_t)1 << 26;   // products below stay far inside int
+    if (dim > cap || hidden > cap || ck > cap || (int64_t)nk * kd > cap || (int64_t)nv * vd > cap ||
+        (int64_t)nh * hd > cap || (int64_t)nkv * hd > cap)
+        return EIF_HIP_E_ARG;
     const Tensor *te = m.find("token_embd.weight");
     if (!te || te->n_dims < 2 || te->ne[1] == 0 || te->ne[1] > 0x7fffffff) return EIF_HIP_E_ARG;
     const int vocab = (int)te->ne[1];

@@ -100,7 +100,10 @@ extern "C" int eif_hip_bitnet_load_svlm(eif_hip_bitnet **out, const char *path, 
         return EIF_HIP_E_ARG;
     }
     if (dim <= 0 || hidden <= 0 || L <= 0 || nh <= 0 || nkv <= 0 || vocab <= 0 || hd <= 0 || bound < 0 ||
-        file_seq <= 0)
+        file_seq <= 0 || (interleaved && hd % 2))
+        return EIF_HIP_E_ARG;
+    const int64_t cap = (int64_t)1 << 26;   // the sizes below stay far inside int
+    if (dim > cap || hidden > cap || vocab > cap || L > 4096 || (int64_t)nh * hd > cap || (int64_t)nkv * hd > cap)
         return EIF_HIP_E_ARG;
     const bool rowwise = bound == 0 && !had;   // the per-row scale layout
     const int q_dim = nh * hd, kv_dim = nkv * hd;
