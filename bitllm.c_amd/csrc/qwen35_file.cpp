@@ -297,10 +297,10 @@ extern "C" void eif_hip_qwen35_destroy(eif_hip_qwen35 *m)
     delete m;
 }
 
-extern "C" int eif_hip_qwen35_load(eif_hip_qwen35 **out, const char *path, void *stream)
+namespace {
+
+int load_model(eif_hip_qwen35 **out, const char *path, void *stream)
 {
-    if (!out || !path) return EIF_HIP_E_ARG;
-    *out = nullptr;
     std::FILE *f = std::fopen(path, "rb");
     if (!f) return EIF_HIP_E_ARG;
     std::vector<uint8_t> img;
@@ -376,6 +376,19 @@ extern "C" int eif_hip_qwen35_load(eif_hip_qwen35 **out, const char *path, void 
     }
     *out = m;
     return EIF_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" int eif_hip_qwen35_load(eif_hip_qwen35 **out, const char *path, void *stream)
+{
+    if (!out || !path) return EIF_HIP_E_ARG;
+    *out = nullptr;
+    try {
+        return load_model(out, path, stream);
+    } catch (...) {   // allocation failures of the host-side bookkeeping
+        return EIF_HIP_E_NOMEM;
+    }
 }
 
 extern "C" const eif_qwen35_layout *eif_hip_qwen35_get_layout(const eif_hip_qwen35 *m)
