@@ -137,6 +137,10 @@ _SIGS = {
 _lib = None
 
 
+# return codes of include/eif_hip.h
+OK, E_ARG, E_DEVICE, E_NOMEM, E_LIMIT = 0, -1, -2, -3, -4
+
+
 class HipError(RuntimeError):
     pass
 

@@ -553,8 +553,13 @@ int dev_upload(T **dst, const T *src, size_t n)
 {
     *dst = nullptr;
     if (!src) return EIF_HIP_OK;
-    EIF_HIP_TRY(hipMalloc(dst, n * sizeof(T)));
-    EIF_HIP_TRY(hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+    T *p = nullptr;
+    if (hipMalloc(&p, n * sizeof(T)) != hipSuccess) return EIF_HIP_E_NOMEM;
+    if (hipMemcpy(p, src, n * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(p);
+        return EIF_HIP_E_DEVICE;
+    }
+    *dst = p;
     return EIF_HIP_OK;
 }
 
@@ -831,6 +836,13 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
         eif_hip_bitnet_destroy(m);
         return EIF_HIP_E_NOMEM;
     }
+    // defined device state before the first reset (steps and prefill refuse to run until then)
+    if (hipMemset(m->state, 0, sizeof(int) * 4) != hipSuccess ||
+        hipMemset(m->prompt, 0, sizeof(int) * c.seq_len) != hipSuccess ||
+        hipMemset(m->seq, 0, sizeof(int) * c.seq_len) != hipSuccess) {
+        eif_hip_bitnet_destroy(m);
+        return EIF_HIP_E_DEVICE;
+    }
     // the shares start at zero: a share a step does not reach keeps finite values, weighed by 0
     const size_t n_sh_o = (size_t)c.n_heads * kAttnShares * c.head_dim, n_sh_ml = (size_t)c.n_heads * 2 * kAttnShares;
     if (hipMalloc(&m->rope, sizeof(float2) * c.seq_len * (c.head_dim / 2)) != hipSuccess ||
@@ -857,28 +869,63 @@ int eif_hip_bitnet_set_layer(eif_hip_bitnet *m, int l, const eif_hip_bitnet_laye
         return EIF_HIP_E_ARG;
     const eif_hip_bitnet_config &c = m->c;
     if (m->exec) return EIF_HIP_E_ARG;   // weights are baked into the captured step
+    if (m->wqkv[l]) return EIF_HIP_E_ARG;   // each layer is set once
+    // All of the layer's device objects are made first and kept only when every one succeeded: a failed call
+    // leaves the layer unset (and may be repeated).
+    eif_hip_qweight *qkv = nullptr, *wo = nullptr, *w13 = nullptr, *w2 = nullptr;
+    float *n_att = nullptr, *n_ffn = nullptr, *n_sa = nullptr, *n_sf = nullptr;
+    size_t bytes = 0;
     std::vector<uint8_t> codes;
     std::vector<float> scales;
     int rc;
-    stack_rows(codes, scales, w->wq, w->gq, m->q_dim, c.dim, c.g_q);
-    stack_rows(codes, scales, w->wk, w->gk, m->kv_dim, c.dim, c.g_q);
-    stack_rows(codes, scales, w->wv, w->gv, m->kv_dim, c.dim, c.g_q);
-    if ((rc = make_tern(&m->wqkv[l], codes, scales, m->q_dim + 2 * m->kv_dim, c.dim, c.g_q, &m->weight_bytes))) return rc;
-    codes.clear(), scales.clear();
-    stack_rows(codes, scales, w->wo, w->go, c.dim, m->q_dim, c.g_o);
-    if ((rc = make_tern(&m->wo[l], codes, scales, c.dim, m->q_dim, c.g_o, &m->weight_bytes))) return rc;
-    codes.clear(), scales.clear();
-    stack_rows(codes, scales, w->w1, w->g1, c.hidden, c.dim, c.g_13);
-    stack_rows(codes, scales, w->w3, w->g3, c.hidden, c.dim, c.g_13);
-    if ((rc = make_tern(&m->w13[l], codes, scales, 2 * c.hidden, c.dim, c.g_13, &m->weight_bytes))) return rc;
-    codes.clear(), scales.clear();
-    stack_rows(codes, scales, w->w2, w->g2, c.dim, c.hidden, c.g_2);
-    if ((rc = make_tern(&m->w2[l], codes, scales, c.dim, c.hidden, c.g_2, &m->weight_bytes))) return rc;
-    if ((rc = dev_upload(&m->rms_att[l], w->rms_att, c.dim)) || (rc = dev_upload(&m->rms_ffn[l], w->rms_ffn, c.dim)) ||
-        (rc = dev_upload(&m->rms_sub_att[l], w->rms_sub_att, m->q_dim)) ||
-        (rc = dev_upload(&m->rms_sub_ffn[l], w->rms_sub_ffn, c.hidden)))
+    do {
+        try {
+            stack_rows(codes, scales, w->wq, w->gq, m->q_dim, c.dim, c.g_q);
+            stack_rows(codes, scales, w->wk, w->gk, m->kv_dim, c.dim, c.g_q);
+            stack_rows(codes, scales, w->wv, w->gv, m->kv_dim, c.dim, c.g_q);
+        } catch (const std::bad_alloc &) {
+            rc = EIF_HIP_E_NOMEM;
+            break;
+        }
+        if ((rc = make_tern(&qkv, codes, scales, m->q_dim + 2 * m->kv_dim, c.dim, c.g_q, &bytes))) break;
+        codes.clear(), scales.clear();
+        try {
+            stack_rows(codes, scales, w->wo, w->go, c.dim, m->q_dim, c.g_o);
+        } catch (const std::bad_alloc &) {
+            rc = EIF_HIP_E_NOMEM;
+            break;
+        }
+        if ((rc = make_tern(&wo, codes, scales, c.dim, m->q_dim, c.g_o, &bytes))) break;
+        codes.clear(), scales.clear();
+        try {
+            stack_rows(codes, scales, w->w1, w->g1, c.hidden, c.dim, c.g_13);
+            stack_rows(codes, scales, w->w3, w->g3, c.hidden, c.dim, c.g_13);
+        } catch (const std::bad_alloc &) {
+            rc = EIF_HIP_E_NOMEM;
+            break;
+        }
+        if ((rc = make_tern(&w13, codes, scales, 2 * c.hidden, c.dim, c.g_13, &bytes))) break;
+        codes.clear(), scales.clear();
+        try {
+            stack_rows(codes, scales, w->w2, w->g2, c.dim, c.hidden, c.g_2);
+        } catch (const std::bad_alloc &) {
+            rc = EIF_HIP_E_NOMEM;
+            break;
+        }
+        if ((rc = make_tern(&w2, codes, scales, c.dim, c.hidden, c.g_2, &bytes))) break;
+        if ((rc = dev_upload(&n_att, w->rms_att, c.dim)) || (rc = dev_upload(&n_ffn, w->rms_ffn, c.dim)) ||
+            (rc = dev_upload(&n_sa, w->rms_sub_att, m->q_dim)) || (rc = dev_upload(&n_sf, w->rms_sub_ffn, c.hidden)))
+            break;
+    } while (false);
+    if (rc) {
+        for (eif_hip_qweight *q : {qkv, wo, w13, w2}) eif_hip_qweight_destroy(q);
+        for (float *p : {n_att, n_ffn, n_sa, n_sf})
+            if (p) (void)hipFree(p);
         return rc;
-    m->weight_bytes += sizeof(float) * (2 * c.dim + m->q_dim + c.hidden);
+    }
+    m->wqkv[l] = qkv, m->wo[l] = wo, m->w13[l] = w13, m->w2[l] = w2;
+    m->rms_att[l] = n_att, m->rms_ffn[l] = n_ffn, m->rms_sub_att[l] = n_sa, m->rms_sub_ffn[l] = n_sf;
+    m->weight_bytes += bytes + sizeof(float) * (2 * c.dim + m->q_dim + c.hidden);
     return EIF_HIP_OK;
 }
 
@@ -937,6 +984,7 @@ int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, voi
 int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream)
 {
     if (!m || n < 0 || !m->head || !m->emb) return EIF_HIP_E_ARG;
+    if (m->n_prompt == 0) return EIF_HIP_E_ARG;   // no eif_hip_bitnet_reset yet: no position or token
     for (int l = 0; l < m->c.n_layers; ++l)
         if (!m->wqkv[l]) return EIF_HIP_E_ARG;
     if (m->hpos + n > m->c.seq_len) return EIF_HIP_E_LIMIT;

@@ -30,6 +30,7 @@
 #include <algorithm>
 #include <mutex>
 #include <new>
+#include <thread>
 #include <type_traits>
 #include <unordered_map>
 
@@ -998,18 +999,30 @@ int g_gemv_prep_cols = 0;   // fewest columns per thread of the fused prep (4, 8
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
 
-// Per-stream workspaces (launches on one stream run in order, so one buffer per stream and purpose suffices):
-// slot 0 the GEMM's split along K, slot 1 the int8 rows of a separate prep. Grown outside graph capture (inside
-// a capture a missing buffer returns NULL and the caller takes another path). Buffers are never freed before the
-// process ends, also when replaced by larger ones: a graph captured on the stream keeps using the buffers it was
-// captured with.
+// Workspaces per (stream, issuing thread): launches that one thread issues on one stream run in order, so one
+// buffer per such pair and purpose suffices, and two threads issuing on the same stream (e.g. the null stream)
+// never share one. Slot 0 the GEMM's split along K, slot 1 the int8 rows of a separate prep. Grown outside graph
+// capture (inside a capture a missing buffer returns NULL and the caller takes another path). Buffers are never
+// freed before the process ends, also when replaced by larger ones: a graph captured on the stream keeps using
+// the buffers it was captured with.
+struct WsKey {
+    hipStream_t st;
+    std::thread::id tid;
+    bool operator==(const WsKey &o) const { return st == o.st && tid == o.tid; }
+};
+struct WsKeyHash {
+    size_t operator()(const WsKey &k) const
+    {
+        return std::hash<const void *>()((const void *)k.st) * 31u + std::hash<std::thread::id>()(k.tid);
+    }
+};
 std::mutex g_ws_mu;
-std::unordered_map<hipStream_t, std::pair<float *, size_t>> g_ws[2];
+std::unordered_map<WsKey, std::pair<float *, size_t>, WsKeyHash> g_ws[2];
 
 float *split_ws(hipStream_t st, size_t bytes, int slot = 0)
 {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto &w = g_ws[slot][st];
+    auto &w = g_ws[slot][WsKey{st, std::this_thread::get_id()}];
     if (w.second < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;

@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <memory>
 #include <vector>
 
 #include <hip/hip_runtime.h>
@@ -333,7 +334,10 @@ int load_model(eif_hip_qwen35 **out, const char *path, void *stream)
         eif_qwen35_image_free(built);
     }
 
-    eif_hip_qwen35 *m = new (std::nothrow) eif_hip_qwen35;
+    // Owned until the end: an exception (host allocation) or an error after this point frees every uploaded weight.
+    std::unique_ptr<eif_hip_qwen35, void (*)(eif_hip_qwen35 *)> owner(new (std::nothrow) eif_hip_qwen35,
+                                                                       eif_hip_qwen35_destroy);
+    eif_hip_qwen35 *m = owner.get();
     if (!m) return EIF_HIP_E_NOMEM;
     int rc = eif_qwen35_parse(img.data(), img.size(), &m->layout);
     const hipStream_t st = (hipStream_t)stream;
@@ -370,11 +374,8 @@ int load_model(eif_hip_qwen35 **out, const char *path, void *stream)
                 rc = EIF_HIP_E_DEVICE;
         }
     }
-    if (rc) {
-        eif_hip_qwen35_destroy(m);
-        return rc;
-    }
-    *out = m;
+    if (rc) return rc;   // owner frees m
+    *out = owner.release();
     return EIF_HIP_OK;
 }
 

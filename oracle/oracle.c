@@ -47,6 +47,13 @@
 #else
 #define ORC_PAR_ROWS
 #endif
+/* Exact integer row sums (every row's int32 accumulators are independent of the others and of any order):
+ * split over threads whenever OpenMP is on, the checker build included; the results are the same bits. */
+#if defined(_OPENMP)
+#define ORC_PAR_INT _Pragma("omp parallel for schedule(static)")
+#else
+#define ORC_PAR_INT
+#endif
 
 /* ---- a1: 2-bit codes.  src/eif_quantize_bitnet.c:15-41, format include/eif_quantize_bitnet.h:4-11 ---- */
 
@@ -222,7 +229,7 @@ void orc_ternary_acc_i32(const uint8_t *w, const int8_t *xq, int ldq, int M, int
     const int rb = (cols + 3) / 4;
     const int g = (group > 0 && group < cols) ? group : cols;
     const int ng = (cols + g - 1) / g;
-    ORC_PAR_ROWS
+    ORC_PAR_INT
     for (int r = 0; r < rows; r++)
         for (int m = 0; m < M; m++) {
             const int8_t *xm = xq + (size_t)m * ldq;
@@ -327,7 +334,7 @@ static inline int int4_val(const uint8_t *row, int c)
 
 void orc_int8_acc_i32(const int8_t *w, const int8_t *xq, int ldq, int M, int rows, int cols, int32_t *acc)
 {
-    ORC_PAR_ROWS
+    ORC_PAR_INT
     for (int r = 0; r < rows; r++)
         for (int m = 0; m < M; m++) {
             int32_t s = 0;
@@ -339,7 +346,7 @@ void orc_int8_acc_i32(const int8_t *w, const int8_t *xq, int ldq, int M, int row
 void orc_int4_acc_i32(const uint8_t *w, const int8_t *xq, int ldq, int M, int rows, int cols, int32_t *acc)
 {
     const int pc = (cols + 1) / 2;
-    ORC_PAR_ROWS
+    ORC_PAR_INT
     for (int r = 0; r < rows; r++)
         for (int m = 0; m < M; m++) {
             int32_t s = 0;

@@ -7,6 +7,7 @@ import pytest
 
 import bitllm_hip as bh
 import synth
+import model_files
 
 
 def mutations(img, seed, n, span):
@@ -24,7 +25,7 @@ def mutations(img, seed, n, span):
 
 def test_bitnet_gguf_fuzz(tmp_path):
     cfg = synth.bitnet_config(128, 256, 1, 4, 2, 32, 64, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
-    img, _ = synth.bitnet_gguf(cfg, (9,), proj_types=(synth.GGUF_TL1, synth.GGUF_F16, synth.GGUF_Q4_0))
+    img, _ = model_files.bitnet_gguf(cfg, (9,), proj_types=(model_files.GGUF_TL1, model_files.GGUF_F16, model_files.GGUF_Q4_0))
     path = tmp_path / "f.gguf"
     ok = 0
     for b in mutations(img, 1, 300, 2600):
@@ -39,9 +40,9 @@ def test_bitnet_gguf_fuzz(tmp_path):
 
 
 def test_qwen35_gguf_fuzz():
-    img = synth.qwen35_gguf((9,), dim=64, hidden=128, n_heads=2, n_kv_heads=1, head_dim=32, vocab=64, heads_k=2,
-                            k_dim=16, v_dim=32, emb_type=synth.GGUF_F16,
-                            lin_types=(synth.GGUF_Q8_0, synth.GGUF_F16, synth.GGUF_Q4_0))
+    img = model_files.qwen35_gguf((9,), dim=64, hidden=128, n_heads=2, n_kv_heads=1, head_dim=32, vocab=64, heads_k=2,
+                            k_dim=16, v_dim=32, emb_type=model_files.GGUF_F16,
+                            lin_types=(model_files.GGUF_Q8_0, model_files.GGUF_F16, model_files.GGUF_Q4_0))
     ok = 0
     for b in mutations(img, 2, 300, 12000):
         try:

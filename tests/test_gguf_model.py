@@ -1,6 +1,6 @@
 """BitNet models in GGUF files (include/eif_hip_gguf.h), on the CPU.
 
-A GGUF file of the test writer (synth.bitnet_gguf) is read both by the reference itself, as its engine reads one
+A GGUF file of the test writer (model_files.bitnet_gguf) is read both by the reference itself, as its engine reads one
 (tinyllm_read_gguf_config, tinyllm_init, tinyllm_load_gguf: src/eif_tinyllm.c:2843-3838, compiled with the
 reference's own flags into oracle/_ref/libref.so), and by eif_gguf_bitnet_open. The configuration and every
 converted array agree bit for bit: 2-bit rows and row scales of TL1 / TL2 / Q8_0 projections and of F32 / F16 / Q4_0
@@ -26,9 +26,10 @@ from conftest import ROOT, P
 import bitllm_hip as bh
 import oracle_api
 import synth
+import model_files
 
 REF = os.path.join(ROOT, "oracle", "_ref", "libref.so")
-TL1, TL2, Q8, F16, F32 = synth.GGUF_TL1, synth.GGUF_TL2, synth.GGUF_Q8_0, synth.GGUF_F16, synth.GGUF_F32
+TL1, TL2, Q8, F16, F32 = model_files.GGUF_TL1, model_files.GGUF_TL2, model_files.GGUF_Q8_0, model_files.GGUF_F16, model_files.GGUF_F32
 
 
 @pytest.fixture(scope="module")
@@ -47,14 +48,14 @@ SHAPES = {   # dim, hidden, layers, heads, kv heads, head_dim (key_length writte
 CASES = {
     "tl1_f16emb": dict(proj_types=(TL1,), emb_type=F16),
     "mixed_f32emb_q8head": dict(proj_types=(TL1, Q8, TL2), emb_type=F32, head_type=Q8, alignment=64,
-                                int_type=synth.GGUF_U64),
+                                int_type=model_files.GGUF_U64),
     "tl2_q8emb_f16head_f16norms": dict(proj_types=(TL2, TL1), emb_type=Q8, head_type=F16, norm_type=F16,
-                                       int_type=synth.GGUF_I32),
-    "q4k_emb_q6k_head": dict(proj_types=(TL1,), emb_type=synth.GGUF_Q4_K, head_type=synth.GGUF_Q6_K),
-    "q4_0_emb_q4_1_head": dict(proj_types=(TL2,), emb_type=synth.GGUF_Q4_0, head_type=synth.GGUF_Q4_1),
+                                       int_type=model_files.GGUF_I32),
+    "q4k_emb_q6k_head": dict(proj_types=(TL1,), emb_type=model_files.GGUF_Q4_K, head_type=model_files.GGUF_Q6_K),
+    "q4_0_emb_q4_1_head": dict(proj_types=(TL2,), emb_type=model_files.GGUF_Q4_0, head_type=model_files.GGUF_Q4_1),
     # projections the reference ternarizes by their absolute mean (the probe stays TL1 / TL2)
-    "absmean_block32": dict(proj_types=(TL1, F32, F16, synth.GGUF_Q4_0, synth.GGUF_Q4_1, Q8, TL2)),
-    "absmean_kquants": dict(proj_types=(TL2, synth.GGUF_Q4_K, synth.GGUF_Q6_K, TL1)),
+    "absmean_block32": dict(proj_types=(TL1, F32, F16, model_files.GGUF_Q4_0, model_files.GGUF_Q4_1, Q8, TL2)),
+    "absmean_kquants": dict(proj_types=(TL2, model_files.GGUF_Q4_K, model_files.GGUF_Q6_K, TL1)),
 }
 
 
@@ -66,7 +67,7 @@ def config(shape, vocab=300, seq_len=64):
 
 def write(tmp_path, cfg, name="m.gguf", key=(3,), **kw):
     kw.setdefault("key_length", cfg["head_dim"] != cfg["dim"] // cfg["n_heads"])
-    img, vals = synth.bitnet_gguf(cfg, key, **kw)
+    img, vals = model_files.bitnet_gguf(cfg, key, **kw)
     path = tmp_path / name
     path.write_bytes(img)
     return str(path), vals
@@ -162,12 +163,12 @@ def _drop(kv, *keys):
 
 RULES = {   # name: (arch, kv_edit, file name, n_kv_heads): the reference's defaults and clamps
     "no_context": ("bitnet", lambda kv: _drop(kv, "bitnet.context_length"), "m.gguf", 2),
-    "long_context": ("bitnet", lambda kv: _set(kv, "bitnet.context_length", synth.GGUF_U32, 10000), "m.gguf", 2),
+    "long_context": ("bitnet", lambda kv: _set(kv, "bitnet.context_length", model_files.GGUF_U32, 10000), "m.gguf", 2),
     "qwen_theta": ("qwen2", lambda kv: _drop(kv, "qwen2.rope.freq_base"), "m.gguf", 2),
     "qwen_in_path": ("bitnet", lambda kv: _drop(kv, "bitnet.rope.freq_base"), "my_qwen_model.gguf", 2),
     "plain_theta": ("bitnet", lambda kv: _drop(kv, "bitnet.rope.freq_base"), "m.gguf", 2),
     "theta_f64_alt_key": ("bitnet", lambda kv: _drop(kv, "bitnet.rope.freq_base") +
-                          [("foo.rope_freq_base", synth.GGUF_F64, 250000.0)], "m.gguf", 2),
+                          [("foo.rope_freq_base", model_files.GGUF_F64, 250000.0)], "m.gguf", 2),
     "llama_interleaved": ("llama", None, "m.gguf", 2),
     "no_arch_llama_keys": ("llama", lambda kv: _drop(kv, "general.architecture"), "m.gguf", 2),
     "kv_heads_default": ("bitnet", lambda kv: _drop(kv, "bitnet.attention.head_count_kv"), "m.gguf", 4),
@@ -234,20 +235,20 @@ def test_gguf_rejects(reft, tmp_path):
     }
 
     def variant(**kw):
-        return synth.bitnet_gguf(cfg, (3,), **kw)[0]
+        return model_files.bitnet_gguf(cfg, (3,), **kw)[0]
     bad["probe Q8_0 (an INT8 model for the reference)"] = variant(proj_types=(Q8, TL1))
     bad["missing projection"] = variant(drop=("blk.1.ffn_up.weight",))
     bad["missing embedding"] = variant(drop=("token_embd.weight",))
     bad["q bias"] = variant(extra_tensors=[("blk.0.attn_q.bias", F32, (128,), np.zeros(128, np.float32).tobytes())])
     bad["no token list"] = variant(kv_edit=lambda kv: _drop(kv, "tokenizer.ggml.tokens"))
     bad["vocabulary != embedding rows"] = variant(
-        kv_edit=lambda kv: _set(kv, "tokenizer.ggml.tokens", synth.GGUF_ARR, (synth.GGUF_STR, ["t"] * 301)))
-    bad["alignment 24"] = variant(kv_edit=lambda kv: _set(kv, "general.alignment", synth.GGUF_U32, 24))
-    bad["block_count as f32"] = variant(kv_edit=lambda kv: _set(kv, "bitnet.block_count", synth.GGUF_F32V, 2.0))
+        kv_edit=lambda kv: _set(kv, "tokenizer.ggml.tokens", model_files.GGUF_ARR, (model_files.GGUF_STR, ["t"] * 301)))
+    bad["alignment 24"] = variant(kv_edit=lambda kv: _set(kv, "general.alignment", model_files.GGUF_U32, 24))
+    bad["block_count as f32"] = variant(kv_edit=lambda kv: _set(kv, "bitnet.block_count", model_files.GGUF_F32V, 2.0))
     bad["BF16 projection (a type tinyllm's loader does not read)"] = variant(drop=("blk.0.attn_v.weight",), extra_tensors=[
-        ("blk.0.attn_v.weight", synth.GGUF_BF16, (128, 64), np.zeros(64 * 128, np.uint16).tobytes())])
-    bad["Q4_K embedding of part blocks"] = synth.bitnet_gguf(config("odd_blocks"), (3,), drop=("token_embd.weight",),
-                                                           extra_tensors=[("token_embd.weight", synth.GGUF_Q4_K,
+        ("blk.0.attn_v.weight", model_files.GGUF_BF16, (128, 64), np.zeros(64 * 128, np.uint16).tobytes())])
+    bad["Q4_K embedding of part blocks"] = model_files.bitnet_gguf(config("odd_blocks"), (3,), drop=("token_embd.weight",),
+                                                           extra_tensors=[("token_embd.weight", model_files.GGUF_Q4_K,
                                                                            (96, 300), bytes(300 * 144))])[0]
     bad["misshapen projection"] = variant(drop=("blk.0.attn_v.weight",), extra_tensors=[
         ("blk.0.attn_v.weight", TL1, (128, 32), bytes(32 * 4 * 10))])

@@ -19,6 +19,7 @@ from conftest import ROOT, P
 
 sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
 import synth  # noqa: E402
+import model_files  # noqa: E402
 import oracle_api  # noqa: E402
 import make_golden  # noqa: E402
 
@@ -168,6 +169,184 @@ def test_decode_limits(gpu):
         m.close()
 
 
+def test_decode_api_order(gpu):
+    """Steps before the first reset have no position or token and are refused before any launch; a layer's
+    weights are set once."""
+    cfg, w = tiny()
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        with pytest.raises(gpu.HipError):
+            m.steps(1)
+        lib = gpu.load()
+        d, L = cfg["dim"], cfg["n_layers"]
+        qd, kvd, hid = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"], cfg["hidden"]
+        rows = {"q": qd, "k": kvd, "v": kvd, "o": d, "1": hid, "3": hid, "2": d}
+        f = {}
+        for k, n in rows.items():
+            f["w" + k] = np.ascontiguousarray(w["w" + k]).reshape(L, n, -1)[0].ctypes.data
+            f["g" + k] = np.ascontiguousarray(w["g" + k]).reshape(L, n, -1)[0].ctypes.data
+        assert lib.eif_hip_bitnet_set_layer(m.h, 0, C.byref(gpu.BitnetLayer(**f))) == gpu.E_ARG
+        m.reset([3])
+        m.steps(2)
+        assert m.position() == 2
+    finally:
+        m.close()
+
+
+def test_decode_bitnet2b_width(gpu, oracle):
+    """Two layers at the full width of the BitNet-b1.58-2B-shaped model (dim 2560, FFN 6912, 20 query and 5 KV
+    heads of 128, g128 / g96 down, WHT-128, the 128256-row INT8 head, context 2048) under the tight bounds of the
+    small models: a 513-token prompt, 512 positions prefilled as one batch, then teacher-forced steps at positions
+    512..519 (the 20-head shares-combining O projection over five-chunk attention, the 6912-wide SiLU-gate prep,
+    the argmax over 8016 head tiles), greedy tokens against the oracle's, graph replays against eager."""
+    c = dict(synth.BITNET_2B_DECODE, n_layers=2)
+    cfg = synth.bitnet_config(**c)
+    w = synth.bitnet_model((33,), cfg)
+    prompt = [int(t) for t in np.random.default_rng(34).integers(0, cfg["vocab"], 513)]
+    toks, _ = compare_steps(gpu, oracle, cfg, w, prompt, 520, graph=True, prefill=512)
+    assert list(toks[:513]) == prompt
+
+
+def _rrms(a, b):
+    return float(np.sqrt(np.mean((a - b) ** 2)) / np.sqrt(np.mean(b ** 2)))
+
+
+def _rmax(a, b):
+    return float(np.abs(a - b).max() / np.abs(b).max())
+
+
+class Sensitivity:
+    """The oracle's own spread under perturbations the size of a summation-order change: every RMSNorm weight
+    times (1 + 2^-23), every RMSNorm weight times (1 - 2^-24), every embedding scale times (1 + 2^-23). Through a
+    deep INT8-activation stack such a change flips activations that sit on an int8 rounding boundary, and the
+    flips compound layer by layer; the GPU, which sums norms and softmaxes in another order, is held to a small
+    multiple of that spread, per layer, pooled over the checked positions."""
+
+    FACTORS = ((("rms_att", "rms_ffn", "rms_sub_att", "rms_sub_ffn", "rms_final"), 1 + 2.0 ** -23),
+               (("rms_att", "rms_ffn", "rms_sub_att", "rms_sub_ffn", "rms_final"), 1 - 2.0 ** -24),
+               (("emb_scale",), 1 + 2.0 ** -23))
+
+    def __init__(self, oracle, cfg, w):
+        self.runs = []
+        for keys, f in self.FACTORS:
+            wp = dict(w)
+            for k in keys:
+                wp[k] = (w[k] * np.float32(f)).astype(np.float32)
+            self.runs.append((OracleRun(oracle, cfg, wp), wp))
+        L = cfg["n_layers"]
+        self.kv_rms, self.kv_max = np.zeros(L), np.zeros(L)
+        self.lg_rms, self.lg_max = 0.0, 0.0
+
+    def add(self, orc, token, pos, lo):
+        """One position: each perturbed oracle run from the cache orc holds; the spread against orc's outputs."""
+        L = len(self.kv_rms)
+        for run, _ in self.runs:
+            run.kc[:, :pos], run.vc[:, :pos] = orc.kc[:, :pos], orc.vc[:, :pos]
+            lp = run.step(token, pos)
+            for layer in range(L):
+                for got, want in ((run.kc[layer, pos], orc.kc[layer, pos]), (run.vc[layer, pos], orc.vc[layer, pos])):
+                    self.kv_rms[layer] = max(self.kv_rms[layer], _rrms(got, want))
+                    self.kv_max[layer] = max(self.kv_max[layer], _rmax(got, want))
+            self.lg_rms = max(self.lg_rms, _rrms(lp, lo))
+            self.lg_max = max(self.lg_max, _rmax(lp, lo))
+
+
+# GPU deviation <= K_SPREAD x the oracle's own spread at that layer, or the floor where the spread is smaller
+K_SPREAD, FLOOR_RMS, FLOOR_MAX = 2.5, 0.02, 0.05
+
+
+def test_decode_bitnet2b_full_size(gpu, oracle):
+    """The 30-layer BitNet-b1.58-2B-shaped decode model at its own shape: dim 2560, FFN 6912, 20 query and 5 KV
+    heads of 128, g128 scales (g96 down), WHT-128 before every linear, 128256-row INT8 head, context 2048.
+
+    A 513-token prompt; positions 0..511 prefilled as one batch; then teacher-forced token steps at positions
+    512..514 (the prompt's last token, then two greedy tokens). At sampled prefill positions and at every step the
+    oracle runs one step from the GPU's cache of the positions before:
+      - layer 0's keys and values (before any int8 flip can compound) agree to 1e-3 of their largest magnitude
+        (fp16 rounding of the cache);
+      - every layer's keys and values, and the logits, deviate from the oracle's by at most K_SPREAD times the
+        oracle's own spread under 1-ulp perturbations at that layer (Sensitivity), or a floor (2% rms, 5% max);
+        a mistake planted in the oracle (two KV heads' key rows swapped in one layer) must exceed that bound;
+      - each greedy token is the first maximum of the returned logits, and the oracle's where its top-two margin
+        exceeds the step's deviation;
+    the same steps replayed as a HIP graph after a second prefill give the eager bits."""
+    cfg = synth.bitnet_config(**synth.BITNET_2B_DECODE)
+    w = synth.bitnet_model((31,), cfg)
+    prompt = [int(t) for t in np.random.default_rng(32).integers(0, cfg["vocab"], 513)]
+    L, n = cfg["n_layers"], 512
+    m = gpu.BitnetModel(cfg, w)
+    orc = OracleRun(oracle, cfg, w)
+    sens = Sensitivity(oracle, cfg, w)
+    dev = []   # (pos, layer, K or V, rms, max) of the GPU against the oracle
+
+    def record(pos, kv_at):
+        for layer in range(L):
+            for name, got, want in (("K", kv_at[layer][0], orc.kc[layer, pos]), ("V", kv_at[layer][1], orc.vc[layer, pos])):
+                dev.append((pos, layer, name, _rrms(got, want), _rmax(got, want)))
+                if layer == 0:
+                    assert _rmax(got, want) <= 1e-3, (pos, name, _rmax(got, want))
+
+    try:
+        m.reset(prompt)
+        m.prefill(n)
+        assert m.position() == n
+        kv = [m.kv_cache(layer, 0, n) for layer in range(L)]
+        pre_lg = m.logits()
+        lg_dev = []
+        for p in (0, 255, 511):
+            for layer in range(L):
+                orc.kc[layer, :p], orc.vc[layer, :p] = kv[layer][0][:p], kv[layer][1][:p]
+            lo = orc.step(prompt[p], p)
+            sens.add(orc, prompt[p], p, lo)
+            record(p, [(kv[layer][0][p], kv[layer][1][p]) for layer in range(L)])
+        lg_dev.append((_rrms(pre_lg, lo), _rmax(pre_lg, lo)))
+        # a planted mistake: the oracle with the key rows of layer 7's first two KV heads swapped (a wrong head
+        # index; every other array the same)
+        wbad = dict(w)
+        kvd, hd = cfg["n_kv_heads"] * cfg["head_dim"], cfg["head_dim"]
+        wk = np.ascontiguousarray(w["wk"]).reshape(L * kvd, -1).copy()
+        gk = np.ascontiguousarray(w["gk"]).reshape(L * kvd, -1).copy()
+        r0 = 7 * kvd
+        for a in (wk, gk):
+            a[r0:r0 + 2 * hd] = np.concatenate([a[r0 + hd:r0 + 2 * hd], a[r0:r0 + hd]])
+        wbad["wk"], wbad["gk"] = wk.reshape(w["wk"].shape), gk.reshape(w["gk"].shape)
+        bad = OracleRun(oracle, cfg, wbad)
+        bad.kc[:, :255], bad.vc[:, :255] = orc.kc[:, :255], orc.vc[:, :255]
+        bad.step(prompt[255], 255)
+        for pos in (512, 513, 514):
+            for layer in range(L):
+                orc.kc[layer, :pos], orc.vc[layer, :pos] = m.kv_cache(layer, 0, pos)
+            m.steps(1, graph=False)
+            lg = m.logits()
+            seq = m.tokens(pos + 2)
+            lo = orc.step(seq[pos], pos)
+            sens.add(orc, seq[pos], pos, lo)
+            record(pos, [tuple(a[0] for a in m.kv_cache(layer, pos, 1)) for layer in range(L)])
+            lg_dev.append((_rrms(lg, lo), _rmax(lg, lo)))
+            assert seq[pos + 1] == int(np.argmax(lg)), pos          # greedy = first maximum of the logits
+            top2 = np.sort(lo)[-2:]
+            if top2[1] - top2[0] > 2 * _rmax(lg, lo) * np.abs(lo).max() + 1e-6:
+                assert seq[pos + 1] == int(np.argmax(lo)), pos
+        for pos, layer, name, r, mx in dev:
+            assert r <= max(K_SPREAD * sens.kv_rms[layer], FLOOR_RMS), (pos, layer, name, r, sens.kv_rms[layer])
+            assert mx <= max(K_SPREAD * sens.kv_max[layer], FLOOR_MAX), (pos, layer, name, mx, sens.kv_max[layer])
+        for r, mx in lg_dev:
+            assert r <= max(K_SPREAD * sens.lg_rms, FLOOR_RMS), (r, sens.lg_rms)
+            assert mx <= max(K_SPREAD * sens.lg_max, FLOOR_MAX), (mx, sens.lg_max)
+        # the bound separates a real mistake from rounding: the planted one exceeds it at layer 7
+        over = _rrms(bad.kc[7, 255], kv[7][0][255]) / max(K_SPREAD * sens.kv_rms[7], FLOOR_RMS)
+        assert over > 1.0, over
+        eager_t, eager_l = m.tokens(n + 4), m.logits()
+        m.reset(prompt)
+        m.prefill(n)
+        m.steps(3, graph=True)
+        graph_t, graph_l = m.tokens(n + 4), m.logits()
+        assert np.array_equal(eager_t, graph_t)
+        assert np.array_equal(eager_l.view(np.uint32), graph_l.view(np.uint32))
+    finally:
+        m.close()
+
+
 def check_prefill(gpu, oracle, cfg, w, prompt, chunks):
     """Prefill in the given chunks; every prompt position checked one step at a time against the oracle given
     the GPU's cache of the positions before it: that position's keys and values in every layer and, at the
@@ -267,7 +446,7 @@ def test_svlm_file_equals_in_memory(gpu, tmp_path, bound, group):
         cfg[k] = gpu.wht_norm(cfg[b])
     w = synth.bitnet_model((12, group), cfg)
     path = str(tmp_path / "model.svlm")
-    synth.write_svlm(path, cfg, w, bound)
+    model_files.write_svlm(path, cfg, w, bound)
     mf = gpu.BitnetModel.from_svlm(path)
     mm = gpu.BitnetModel(cfg, w)
     try:
@@ -297,7 +476,7 @@ def test_ttml_file_equals_in_memory(gpu, tmp_path, head_dim):
     cfg = synth.bitnet_config(128, 256, 2, 4, 2, head_dim, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
     w = synth.bitnet_model((14, head_dim), cfg)
     path = str(tmp_path / "model.ttml")
-    synth.write_ttml(path, cfg, w)
+    model_files.write_ttml(path, cfg, w)
     mf = gpu.BitnetModel.from_svlm(path)
     mm = gpu.BitnetModel(cfg, w)
     try:
@@ -321,7 +500,7 @@ def test_ttml_file_equals_in_memory(gpu, tmp_path, head_dim):
 def test_svlm_rejects(gpu, tmp_path):
     cfg, w = tiny()
     path = tmp_path / "m.svlm"
-    synth.write_svlm(str(path), cfg, w, 32)
+    model_files.write_svlm(str(path), cfg, w, 32)
     raw = bytearray(path.read_bytes())
     bad = tmp_path / "bad.svlm"
     raw[48 + 12 * 4] = 1                      # qtype INT8: not a BitNet file
@@ -347,15 +526,15 @@ def _same_decode(models):
 
 
 GGUF_CASES = {   # (dim, hidden, layers, heads, kv heads, head_dim), writer options
-    "tl1_f16emb_tied": ((128, 256, 2, 4, 2, 32), dict(proj_types=(synth.GGUF_TL1,), emb_type=synth.GGUF_F16)),
-    "mixed_q8head": ((96, 224, 2, 3, 1, 32), dict(proj_types=(synth.GGUF_TL1, synth.GGUF_Q8_0, synth.GGUF_TL2),
-                                                  emb_type=synth.GGUF_F32, head_type=synth.GGUF_Q8_0, alignment=64)),
-    "hd_apart_f16head": ((128, 256, 2, 4, 2, 64), dict(proj_types=(synth.GGUF_TL2,), emb_type=synth.GGUF_Q8_0,
-                                                       head_type=synth.GGUF_F16, key_length=True)),
-    "q4k_emb_q6k_head": ((256, 512, 1, 4, 2, 64), dict(proj_types=(synth.GGUF_TL1,), emb_type=synth.GGUF_Q4_K,
-                                                       head_type=synth.GGUF_Q6_K, key_length=True)),
-    "absmean_projections": ((128, 256, 2, 4, 2, 32), dict(proj_types=(synth.GGUF_TL1, synth.GGUF_F32, synth.GGUF_F16,
-                                                                      synth.GGUF_Q4_0, synth.GGUF_Q4_1))),
+    "tl1_f16emb_tied": ((128, 256, 2, 4, 2, 32), dict(proj_types=(model_files.GGUF_TL1,), emb_type=model_files.GGUF_F16)),
+    "mixed_q8head": ((96, 224, 2, 3, 1, 32), dict(proj_types=(model_files.GGUF_TL1, model_files.GGUF_Q8_0, model_files.GGUF_TL2),
+                                                  emb_type=model_files.GGUF_F32, head_type=model_files.GGUF_Q8_0, alignment=64)),
+    "hd_apart_f16head": ((128, 256, 2, 4, 2, 64), dict(proj_types=(model_files.GGUF_TL2,), emb_type=model_files.GGUF_Q8_0,
+                                                       head_type=model_files.GGUF_F16, key_length=True)),
+    "q4k_emb_q6k_head": ((256, 512, 1, 4, 2, 64), dict(proj_types=(model_files.GGUF_TL1,), emb_type=model_files.GGUF_Q4_K,
+                                                       head_type=model_files.GGUF_Q6_K, key_length=True)),
+    "absmean_projections": ((128, 256, 2, 4, 2, 32), dict(proj_types=(model_files.GGUF_TL1, model_files.GGUF_F32, model_files.GGUF_F16,
+                                                                      model_files.GGUF_Q4_0, model_files.GGUF_Q4_1))),
 }
 
 
@@ -365,7 +544,7 @@ def test_gguf_file_equals_in_memory(gpu, tmp_path, case):
     converts from it (those are the reference loader's own, tests/test_gguf_model.py) set in memory."""
     shape, kw = GGUF_CASES[case]
     cfg = synth.bitnet_config(*shape, 300, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
-    img, _ = synth.bitnet_gguf(cfg, (8,), **kw)
+    img, _ = model_files.bitnet_gguf(cfg, (8,), **kw)
     path = tmp_path / "m.gguf"
     path.write_bytes(img)
     g = gpu.GgufBitnet(str(path))
@@ -415,8 +594,8 @@ def test_ttml_interleaved_equals_reordered(gpu, tmp_path):
         order = np.concatenate([h + np.arange(0, hd, 2), h + np.arange(1, hd, 2)], axis=1).ravel()
         w2["w" + name], w2["g" + name] = w["w" + name][order], w["g" + name][order]
     pa, pb = str(tmp_path / "inter.ttml"), str(tmp_path / "split.ttml")
-    synth.write_ttml(pa, cfg, w, interleaved=1)
-    synth.write_ttml(pb, cfg, w2)
+    model_files.write_ttml(pa, cfg, w, interleaved=1)
+    model_files.write_ttml(pb, cfg, w2)
     ms = [gpu.BitnetModel.from_svlm(p) for p in (pa, pb)]
     try:
         out = _same_decode(ms)
@@ -429,7 +608,7 @@ def test_ttml_interleaved_equals_reordered(gpu, tmp_path):
 
 def test_gguf_load_rejects(gpu, tmp_path):
     cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
-    img, _ = synth.bitnet_gguf(cfg, (8,))
+    img, _ = model_files.bitnet_gguf(cfg, (8,))
     bad = tmp_path / "bad.gguf"
     bad.write_bytes(img[:len(img) - 1000])
     with pytest.raises(gpu.HipError):
@@ -442,7 +621,7 @@ def test_ttml_rejects(gpu, tmp_path):
     cfg = synth.bitnet_config(128, 256, 2, 4, 2, 32, 300, 32, 0, 0, 0, 0, 0, rope_theta=10000.0)
     w = synth.bitnet_model((14, 32), cfg)
     path = tmp_path / "m.ttml"
-    synth.write_ttml(str(path), cfg, w)
+    model_files.write_ttml(str(path), cfg, w)
     raw = bytearray(path.read_bytes())
     raw[36 + 4 * 7] = 1                       # qtype INT8: not a BitNet model
     bad = tmp_path / "bad.ttml"

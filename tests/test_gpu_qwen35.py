@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 
 import synth
+import model_files
 from test_qwn5 import CASES, DN_KINDS, FA_KINDS, FF_KINDS, KIND_ID, make
 
 pytestmark = pytest.mark.gpu
@@ -20,11 +21,11 @@ VEC_NAME = {"rms_att": "rms_att", "rms_ffn": "rms_ffn", "sub_att": "sub_att", "s
 
 def expected_weight(gpu, qt, values, scales, group):
     rows, cols = values.shape
-    if qt == synth.Q35_INT4:
+    if qt == model_files.Q35_INT4:
         return gpu.QWeight(gpu.W_INT4, rows, cols, 0, np.ascontiguousarray(synth.pack_int4(values)), scales)
     if qt == 4:
         return gpu.QWeight(gpu.W_INT8, rows, cols, 0, np.ascontiguousarray(values), scales)
-    g = group if qt == synth.Q35_TERN2 else 0
+    g = group if qt == model_files.Q35_TERN2 else 0
     return gpu.QWeight(gpu.W_TERNARY, rows, cols, g, np.ascontiguousarray(synth.pack_ternary(values)),
                        np.ascontiguousarray(scales.reshape(rows, -1) if g else scales))
 
@@ -66,9 +67,9 @@ def test_qwen35_file_weights(gpu, tmp_path, case):
         for l, t in enumerate(cfg["layer_types"]):
             for k in (DN_KINDS if t == 0 else FA_KINDS) + FF_KINDS:
                 _, values, scales, _ = arrays[f"L{l}.{k}"]
-                qt = synth.Q35_FP32 if k in ("pb", "pa") and g > 0 else qlm
+                qt = model_files.Q35_FP32 if k in ("pb", "pa") and g > 0 else qlm
                 w = m.linear(l, KIND_ID[k])
-                if qt == synth.Q35_FP32:
+                if qt == model_files.Q35_FP32:
                     assert w is None, (l, k)
                     continue
                 want = expected_weight(gpu, qt, values, scales, g)
@@ -79,13 +80,13 @@ def test_qwen35_file_weights(gpu, tmp_path, case):
                 names = (DN_KINDS if t == 0 else FA_KINDS) + FF_KINDS
                 if other not in [KIND_ID[k] for k in names]:
                     assert m.linear(l, other) is None
-        assert n_checked == 0 or qlm != synth.Q35_FP32
+        assert n_checked == 0 or qlm != model_files.Q35_FP32
         # the tied head
-        emb_qt = {synth.Q35_EMBED_INT8: 4, synth.Q35_EMBED_INT4: synth.Q35_INT4, synth.Q35_EMBED_2BIT: synth.Q35_TERN2,
-                  synth.Q35_EMBED_DENSE: synth.Q35_TERN3, synth.Q35_EMBED_FP32: synth.Q35_FP32}[cfg["quant_embed"]]
+        emb_qt = {model_files.Q35_EMBED_INT8: 4, model_files.Q35_EMBED_INT4: model_files.Q35_INT4, model_files.Q35_EMBED_2BIT: model_files.Q35_TERN2,
+                  model_files.Q35_EMBED_DENSE: model_files.Q35_TERN3, model_files.Q35_EMBED_FP32: model_files.Q35_FP32}[cfg["quant_embed"]]
         _, values, scales, _ = arrays["embed"]
         h = m.head()
-        if emb_qt == synth.Q35_FP32:
+        if emb_qt == model_files.Q35_FP32:
             assert h is None
         else:
             want = expected_weight(gpu, emb_qt, values, scales, g)
@@ -127,7 +128,7 @@ def test_qwen35_gguf_loads_as_its_image(gpu, tmp_path):
     """A Qwen3.5 GGUF path given to eif_hip_qwen35_load loads as the QWN5 image eif_qwen35_gguf_image builds from
     it (the reference's image, tests/test_qwen35_gguf.py): the same layout, every INT4 linear and the INT8 head
     giving the same output bits, the same FP32 vectors."""
-    gguf = synth.qwen35_gguf((6,), dim=256, hidden=512, vocab=500)
+    gguf = model_files.qwen35_gguf((6,), dim=256, hidden=512, vocab=500)
     pg, pi = tmp_path / "m.gguf", tmp_path / "m.eifm"
     pg.write_bytes(gguf)
     pi.write_bytes(gpu.qwen35_gguf_image(gguf))

@@ -10,6 +10,7 @@ import pytest
 
 from conftest import ROOT
 import synth
+import model_files
 from test_file_fuzz import mutations
 
 SRC = os.path.join(ROOT, "bitllm.c_amd", "csrc")
@@ -52,15 +53,15 @@ def write_all(tmp_path, tag, base, seed, n, span):
 def test_readers_under_sanitizers(harness, tmp_path):
     from test_qwn5 import make
     cfg = synth.bitnet_config(128, 256, 1, 4, 2, 32, 64, 64, 32, 32, 0, 0, 0, rope_theta=10000.0)
-    synth.write_svlm(str(tmp_path / "b.svlm"), cfg, synth.bitnet_model((3, 32), cfg), 32)
+    model_files.write_svlm(str(tmp_path / "b.svlm"), cfg, synth.bitnet_model((3, 32), cfg), 32)
     c2 = synth.bitnet_config(128, 256, 1, 4, 2, 32, 64, 64, 0, 0, 0, 0, 0, rope_theta=10000.0)
-    synth.write_ttml(str(tmp_path / "b.ttml"), c2, synth.bitnet_model((4, 32), c2), interleaved=1)
+    model_files.write_ttml(str(tmp_path / "b.ttml"), c2, synth.bitnet_model((4, 32), c2), interleaved=1)
     svlm = write_all(tmp_path, "svlm", (tmp_path / "b.svlm").read_bytes(), 7, 400, 176) + \
         write_all(tmp_path, "ttml", (tmp_path / "b.ttml").read_bytes(), 8, 400, 84)
-    gg, _ = synth.bitnet_gguf(c2, (9,), proj_types=(synth.GGUF_TL1, synth.GGUF_F16, synth.GGUF_Q4_0))
-    q = synth.qwen35_gguf((9,), dim=64, hidden=128, n_heads=2, n_kv_heads=1, head_dim=32, vocab=64, heads_k=2,
-                          k_dim=16, v_dim=32, emb_type=synth.GGUF_F16,
-                          lin_types=(synth.GGUF_Q8_0, synth.GGUF_F16, synth.GGUF_Q4_0))
+    gg, _ = model_files.bitnet_gguf(c2, (9,), proj_types=(model_files.GGUF_TL1, model_files.GGUF_F16, model_files.GGUF_Q4_0))
+    q = model_files.qwen35_gguf((9,), dim=64, hidden=128, n_heads=2, n_kv_heads=1, head_dim=32, vocab=64, heads_k=2,
+                          k_dim=16, v_dim=32, emb_type=model_files.GGUF_F16,
+                          lin_types=(model_files.GGUF_Q8_0, model_files.GGUF_F16, model_files.GGUF_Q4_0))
     _, w, _ = make("tern_g32_hadamard")
     run(harness, "svlm", svlm + [str(tmp_path / "b.svlm"), str(tmp_path / "b.ttml")])
     run(harness, "bitnet", write_all(tmp_path, "gguf", gg, 9, 400, 2600))

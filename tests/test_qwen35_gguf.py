@@ -1,6 +1,6 @@
 """Qwen3.5 GGUF files -> QWN5 images (eif_qwen35_gguf_image, include/eif_hip_qwen35.h), on the CPU.
 
-A llama.cpp-style Qwen3.5 GGUF of the test writer (synth.qwen35_gguf: 24 blocks, DeltaNet and attention layers,
+A llama.cpp-style Qwen3.5 GGUF of the test writer (model_files.qwen35_gguf: 24 blocks, DeltaNet and attention layers,
 linears in F32 / F16 / BF16 / Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K, embeddings in several of them) goes through the
 reference's own image builder (qwen35_gguf_build_image, src/eif_qwen35_gguf.c:262-454, compiled into
 oracle/_ref/libref.so with the reference's flags) and through eif_qwen35_gguf_image. The images are byte for byte
@@ -19,6 +19,7 @@ import pytest
 from conftest import ROOT, P
 import bitllm_hip as bh
 import synth
+import model_files
 
 REF = os.path.join(ROOT, "oracle", "_ref", "libref.so")
 REF_SCALAR = os.path.join(ROOT, "oracle", "_ref", "libref_scalar.so")
@@ -57,11 +58,11 @@ def ref_scalar_build():
 SMALL = dict(dim=64, hidden=128, n_heads=2, n_kv_heads=1, head_dim=32, vocab=100, heads_k=2, k_dim=16, v_dim=32)
 CASES = {   # writer options
     "kquants_q6k_emb": dict(),
-    "q4k_emb_mixed": dict(emb_type=synth.GGUF_Q4_K, lin_types=(synth.GGUF_Q5_K, synth.GGUF_BF16, synth.GGUF_Q4_0,
-                                                                synth.GGUF_Q6_K), ctx=1000),
-    "small_block32": dict(SMALL, emb_type=synth.GGUF_F16, lin_types=(synth.GGUF_Q8_0, synth.GGUF_Q4_0, synth.GGUF_F32,
-                                                                      synth.GGUF_BF16, synth.GGUF_F16)),
-    "small_f32_emb_q8": dict(SMALL, emb_type=synth.GGUF_F32, lin_types=(synth.GGUF_F32,), ctx=9000),
+    "q4k_emb_mixed": dict(emb_type=model_files.GGUF_Q4_K, lin_types=(model_files.GGUF_Q5_K, model_files.GGUF_BF16, model_files.GGUF_Q4_0,
+                                                                model_files.GGUF_Q6_K), ctx=1000),
+    "small_block32": dict(SMALL, emb_type=model_files.GGUF_F16, lin_types=(model_files.GGUF_Q8_0, model_files.GGUF_Q4_0, model_files.GGUF_F32,
+                                                                      model_files.GGUF_BF16, model_files.GGUF_F16)),
+    "small_f32_emb_q8": dict(SMALL, emb_type=model_files.GGUF_F32, lin_types=(model_files.GGUF_F32,), ctx=9000),
 }
 # (a full-attention layer every 4 of the 24 gives the 18 DeltaNet and 6 attention layers the reference's loader
 # holds; the builder itself accepts other intervals)
@@ -75,7 +76,7 @@ def a_log_slots(img):
 
 @pytest.mark.parametrize("case", sorted(CASES))
 def test_image_matches_reference_builder(ref_build, ref_scalar_build, case):
-    gguf = synth.qwen35_gguf((2,), **CASES[case])
+    gguf = model_files.qwen35_gguf((2,), **CASES[case])
     rc, ref = ref_build(gguf)
     assert rc == 0
     ours = bh.qwen35_gguf_image(gguf)
@@ -97,17 +98,17 @@ def test_oracle_quant_rows_matches_reference_image(ref_build, oracle):
     """The image's INT4 and INT8 rows of F32 tensors are orc_quant_rows of those rows (the oracle's arithmetic is
     the compiled reference's)."""
     cap = []
-    orig = synth.gguf_dense_tensor
+    orig = model_files.gguf_dense_tensor
 
     def spy(r, rows, cols, ty):
         raw = orig(r, rows, cols, ty)
-        cap.append((np.frombuffer(raw, np.float32).reshape(rows, cols).copy() if ty == synth.GGUF_F32 else None))
+        cap.append((np.frombuffer(raw, np.float32).reshape(rows, cols).copy() if ty == model_files.GGUF_F32 else None))
         return raw
-    synth.gguf_dense_tensor = spy
+    model_files.gguf_dense_tensor = spy
     try:
-        gguf = synth.qwen35_gguf((3,), emb_type=synth.GGUF_F32, lin_types=(synth.GGUF_F32,))
+        gguf = model_files.qwen35_gguf((3,), emb_type=model_files.GGUF_F32, lin_types=(model_files.GGUF_F32,))
     finally:
-        synth.gguf_dense_tensor = orig
+        model_files.gguf_dense_tensor = orig
     rc, img = ref_build(gguf)
     assert rc == 0
     lay = bh.qwen35_parse(img)
@@ -130,15 +131,15 @@ def _set(kv, key, t, v):
 
 def test_gguf_image_rejects(ref_build):
     def edit(**kw):
-        return synth.qwen35_gguf((4,), **dict(SMALL, emb_type=synth.GGUF_F16, **kw))
+        return model_files.qwen35_gguf((4,), **dict(SMALL, emb_type=model_files.GGUF_F16, **kw))
     bad = {
-        "arch": edit(kv_edit=lambda kv: _set(kv, "general.architecture", synth.GGUF_STR, "llama")),
-        "23 blocks": edit(kv_edit=lambda kv: _set(kv, "qwen35.block_count", synth.GGUF_U32, 23)),
-        "eps 1e-5": edit(kv_edit=lambda kv: _set(kv, "qwen35.attention.layer_norm_rms_epsilon", synth.GGUF_F32V, 1e-5)),
-        "k heads != v heads": edit(kv_edit=lambda kv: _set(kv, "qwen35.ssm.time_step_rank", synth.GGUF_U32, 4)),
-        "untied head": edit(extra_tensors=[("output.weight", synth.GGUF_F32, (64, 100), bytes(64 * 100 * 4))]),
+        "arch": edit(kv_edit=lambda kv: _set(kv, "general.architecture", model_files.GGUF_STR, "llama")),
+        "23 blocks": edit(kv_edit=lambda kv: _set(kv, "qwen35.block_count", model_files.GGUF_U32, 23)),
+        "eps 1e-5": edit(kv_edit=lambda kv: _set(kv, "qwen35.attention.layer_norm_rms_epsilon", model_files.GGUF_F32V, 1e-5)),
+        "k heads != v heads": edit(kv_edit=lambda kv: _set(kv, "qwen35.ssm.time_step_rank", model_files.GGUF_U32, 4)),
+        "untied head": edit(extra_tensors=[("output.weight", model_files.GGUF_F32, (64, 100), bytes(64 * 100 * 4))]),
         "missing tensor": edit(drop=("blk.5.ffn_up.weight",)),
-        "Q4_1 linear": edit(lin_types=(synth.GGUF_Q4_1,)),
+        "Q4_1 linear": edit(lin_types=(model_files.GGUF_Q4_1,)),
     }
     good = edit()
     bad["truncated"] = good[:len(good) - 4096]

@@ -1,6 +1,6 @@
 """Qwen3.5 model files (QWN5, include/eif_hip_qwen35.h), on the CPU.
 
-The test writer (synth.qwen35_image) is checked against the reference's own loader, qwen35_load
+The test writer (model_files.qwen35_image) is checked against the reference's own loader, qwen35_load
 (src/eif_qwen35.c:1223-1481, compiled from the reference sources into oracle/_ref/libref.so): every pointer the
 loader sets lands on the array the writer put there, for INT4, ternary 2-bit (row and group scales, Hadamard
 signs), ternary base-3 and FP32 files, with and without SubLN vectors, plain linears, and regions off their
@@ -17,6 +17,7 @@ import pytest
 from conftest import P
 import bitllm_hip as bh
 import synth
+import model_files
 
 DN_KINDS = ("qkv", "z", "out", "pb", "pa")
 FA_KINDS = ("q", "k", "v", "o")
@@ -29,21 +30,21 @@ KIND_ID = {"qkv": bh.Q35_DN_QKV, "z": bh.Q35_DN_Z, "out": bh.Q35_DN_OUT, "pb": b
 BASE = dict(dim=64, hidden=128, layer_types=[0, 1, 0, 1], n_heads=2, n_kv_heads=1, head_dim=32, vocab=100,
             lin_k_heads=2, lin_k_dim=16, lin_v_heads=2, lin_v_dim=32)
 CASES = {
-    "int4_int8emb": (dict(quant_lm=synth.Q35_INT4, quant_embed=synth.Q35_EMBED_INT8), True, 0),
-    "tern_rows_2bitemb": (dict(quant_lm=synth.Q35_TERN2, quant_embed=synth.Q35_EMBED_2BIT), True, 0),
-    "tern_g32_hadamard": (dict(quant_lm=synth.Q35_TERN2, quant_embed=synth.Q35_EMBED_2BIT, group=32, hadamard=32),
+    "int4_int8emb": (dict(quant_lm=model_files.Q35_INT4, quant_embed=model_files.Q35_EMBED_INT8), True, 0),
+    "tern_rows_2bitemb": (dict(quant_lm=model_files.Q35_TERN2, quant_embed=model_files.Q35_EMBED_2BIT), True, 0),
+    "tern_g32_hadamard": (dict(quant_lm=model_files.Q35_TERN2, quant_embed=model_files.Q35_EMBED_2BIT, group=32, hadamard=32),
                           True, 1),
-    "dense_no_subln": (dict(quant_lm=synth.Q35_TERN3, quant_embed=synth.Q35_EMBED_DENSE), False, 3),
-    "g64_plain_int8emb": (dict(quant_lm=synth.Q35_TERN2, quant_embed=synth.Q35_EMBED_INT8, group=64, plain=1),
+    "dense_no_subln": (dict(quant_lm=model_files.Q35_TERN3, quant_embed=model_files.Q35_EMBED_DENSE), False, 3),
+    "g64_plain_int8emb": (dict(quant_lm=model_files.Q35_TERN2, quant_embed=model_files.Q35_EMBED_INT8, group=64, plain=1),
                           True, 0),
-    "fp32": (dict(quant_lm=synth.Q35_FP32, quant_embed=synth.Q35_EMBED_FP32), True, 2),
+    "fp32": (dict(quant_lm=model_files.Q35_FP32, quant_embed=model_files.Q35_EMBED_FP32), True, 2),
 }
 
 
 def make(case, key=(1,)):
     kw, subs, pad = CASES[case]
-    cfg = synth.qwen35_config(**dict(BASE, **kw))
-    img, arrays = synth.qwen35_image(cfg, key, sub_norms=subs, region_pad=pad)
+    cfg = model_files.qwen35_config(**dict(BASE, **kw))
+    img, arrays = model_files.qwen35_image(cfg, key, sub_norms=subs, region_pad=pad)
     return cfg, img, arrays
 
 
@@ -117,8 +118,8 @@ def test_parse_matches_writer(case):
     assert lay.hadamard_block == cfg["hadamard"]
     # shapes, storage types and groups of the matrices
     g = cfg["group"]
-    qtype = {synth.Q35_TERN2: bh.Q35_TERN2, synth.Q35_TERN3: bh.Q35_TERN3, synth.Q35_INT4: bh.Q35_INT4,
-             synth.Q35_FP32: bh.Q35_FP32}[cfg["quant_lm"]]
+    qtype = {model_files.Q35_TERN2: bh.Q35_TERN2, model_files.Q35_TERN3: bh.Q35_TERN3, model_files.Q35_INT4: bh.Q35_INT4,
+             model_files.Q35_FP32: bh.Q35_FP32}[cfg["quant_lm"]]
     for l, t in enumerate(cfg["layer_types"]):
         for k in (DN_KINDS if t == 0 else FA_KINDS) + FF_KINDS:
             a, m = arrays[f"L{l}.{k}"], lay.lin[l][KIND_ID[k]]
@@ -127,9 +128,9 @@ def test_parse_matches_writer(case):
             want_qt = bh.Q35_FP32 if small and g > 0 else qtype
             assert m.qtype == want_qt, (l, k)
             assert m.group == (g if want_qt == bh.Q35_TERN2 else 0), (l, k)
-    emb_qt = {synth.Q35_EMBED_INT8: bh.Q35_INT8, synth.Q35_EMBED_INT4: bh.Q35_INT4,
-              synth.Q35_EMBED_2BIT: bh.Q35_TERN2, synth.Q35_EMBED_DENSE: bh.Q35_TERN3,
-              synth.Q35_EMBED_FP32: bh.Q35_FP32}[cfg["quant_embed"]]
+    emb_qt = {model_files.Q35_EMBED_INT8: bh.Q35_INT8, model_files.Q35_EMBED_INT4: bh.Q35_INT4,
+              model_files.Q35_EMBED_2BIT: bh.Q35_TERN2, model_files.Q35_EMBED_DENSE: bh.Q35_TERN3,
+              model_files.Q35_EMBED_FP32: bh.Q35_FP32}[cfg["quant_embed"]]
     assert (lay.embed.rows, lay.embed.cols, lay.embed.qtype) == (cfg["vocab"], cfg["dim"], emb_qt)
     if not cfg["plain"]:                    # a plain file's SubLN vectors are ignored, as the reference does
         assert lay.norms_end == len(img)
@@ -143,7 +144,7 @@ def test_dense_packing_matches_reference_gemv(ref):
         sc = (np.abs(r.standard_normal(rows)) + 0.1).astype(np.float32)
         x = r.integers(-4, 5, size=cols).astype(np.float32)   # small integers: the sums are exact
         out = np.zeros(rows, np.float32)
-        packed = np.ascontiguousarray(synth.pack_ternary_dense(v))
+        packed = np.ascontiguousarray(model_files.pack_ternary_dense(v))
         ref.ref_q35_dense_gemv(P(out), P(packed), P(sc), P(x), rows, cols)
         np.testing.assert_array_equal(out, (v.astype(np.float32) @ x) * sc)
     # every byte value: five digits, the first column least significant (bytes above 242 keep five digits)

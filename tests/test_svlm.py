@@ -17,6 +17,7 @@ from conftest import ROOT
 
 sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
 import synth  # noqa: E402
+import model_files  # noqa: E402
 import oracle_api  # noqa: E402
 import make_golden  # noqa: E402
 
@@ -38,7 +39,7 @@ def test_svlm_file_read_by_reference(tmp_path, bound, group):
     ref = oracle_api.load_ref_tinyllm(REF)
     cfg, w = tiny(group)
     path = str(tmp_path / "model.svlm")
-    synth.write_svlm(path, cfg, w, bound)
+    model_files.write_svlm(path, cfg, w, bound)
     hf = ref.ref_svlm_create(os.fsencode(path))
     assert hf
     c, ws = oracle_api.bitnet_structs(cfg, w)
@@ -59,7 +60,7 @@ def test_svlm_writer_layout(tmp_path):
     """Header words and region sizes as the reader takes them."""
     cfg, w = tiny(32)
     path = str(tmp_path / "m.svlm")
-    synth.write_svlm(path, cfg, w, 32)
+    model_files.write_svlm(path, cfg, w, 32)
     raw = open(path, "rb").read()
     hdr = np.frombuffer(raw[:48], np.uint32)
     ci = np.frombuffer(raw[48:176], np.int32)
@@ -91,7 +92,7 @@ def test_ttml_file_read_by_reference(oracle, tmp_path, head_dim):
     ref = oracle_api.load_ref_tinyllm(REF)
     cfg, w = ttml_config(head_dim)
     path = str(tmp_path / "model.ttml")
-    synth.write_ttml(path, cfg, w)
+    model_files.write_ttml(path, cfg, w)
     h = ref.ref_ttml_create(os.fsencode(path))
     assert h
     ocfg = dict(cfg, g_q=cfg["dim"], g_o=cfg["n_heads"] * cfg["head_dim"], g_13=cfg["dim"], g_2=cfg["hidden"])
@@ -118,7 +119,7 @@ def test_ttml_writer_layout(tmp_path):
     """Header words, configuration words and region sizes as the reader takes them."""
     cfg, w = ttml_config(32)
     path = str(tmp_path / "m.ttml")
-    synth.write_ttml(path, cfg, w)
+    model_files.write_ttml(path, cfg, w)
     raw = open(path, "rb").read()
     hdr = np.frombuffer(raw[:36], np.uint32)
     ci = np.frombuffer(raw[36:36 + 48], np.int32)
@@ -148,9 +149,9 @@ def test_ttml_interleaved_rope_is_reordered_rows(tmp_path):
         order = np.concatenate([h + np.arange(0, hd, 2), h + np.arange(1, hd, 2)], axis=1).ravel()
         w2["w" + name], w2["g" + name] = w["w" + name][order], w["g" + name][order]
     paths = [str(tmp_path / n) for n in ("inter.ttml", "split.ttml", "plain.ttml")]
-    synth.write_ttml(paths[0], cfg, w, interleaved=1)
-    synth.write_ttml(paths[1], cfg, w2)
-    synth.write_ttml(paths[2], cfg, w)
+    model_files.write_ttml(paths[0], cfg, w, interleaved=1)
+    model_files.write_ttml(paths[1], cfg, w2)
+    model_files.write_ttml(paths[2], cfg, w)
     hs = [ref.ref_ttml_create(os.fsencode(p)) for p in paths]
     assert all(hs)
     V = cfg["vocab"]
