@@ -69,6 +69,7 @@ _SIGS = {
     "eif_hip_bitnet_set_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
     "eif_hip_bitnet_reset": (_i, [_vp, _vp, _i, _vp]),
     "eif_hip_bitnet_steps": (_i, [_vp, _i, _i, _vp]),
+    "eif_hip_bitnet_set_persistent": (_i, [_vp, _i]),
     "eif_hip_bitnet_prefill": (_i, [_vp, _i, _vp]),
     "eif_hip_bitnet_load_svlm": (_i, [_vp, C.c_char_p, _i]),
     "eif_qwen35_parse": (_i, [_vp, _sz, _vp]),
@@ -367,6 +368,14 @@ class BitnetModel:
         if p < 0:
             check(p, "eif_hip_bitnet_position")
         return p
+
+    def set_persistent(self, on):
+        """Token steps as one persistent kernel (on=True) or as separate launches; returns whether steps run
+        persistent (False when the model's shapes are outside the persistent kernel). on=None only queries."""
+        rc = load().eif_hip_bitnet_set_persistent(self.h, -1 if on is None else int(bool(on)))
+        if rc < 0:
+            check(rc, "eif_hip_bitnet_set_persistent")
+        return rc == 1
 
     def kv_cache(self, layer, pos0, n, stream=None):
         """Keys and values of one layer at positions [pos0, pos0 + n), float [n, kv_dim] each."""

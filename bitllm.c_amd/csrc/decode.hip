@@ -20,6 +20,8 @@
 #include <vector>
 
 #include "hip_common.h"
+#include "attn_dev.h"
+#include "persist.h"
 #include "../../include/eif_hip_decode.h"
 
 namespace {
@@ -35,17 +37,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const int8_t *emb, const flo
     const float sc = emb_scale ? emb_scale[tok] : 1.0f;
     const int8_t *row = emb + (size_t)tok * dim;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = (float)row[i] * sc;
-}
-
-// 8 consecutive fp16 values -> float.
-EIF_DEV void half8_to_float(const uint4 &raw, float (&f)[8])
-{
-    const __half2 *hp = reinterpret_cast<const __half2 *>(&raw);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float2 v = __half22float2(hp[i]);
-        f[2 * i] = v.x, f[2 * i + 1] = v.y;
-    }
 }
 
 // RoPE angle of pair j (dims j, j + HD/2) at position pos: freq = 1 / powf(theta, 2j / HD), val = pos * freq;
@@ -68,132 +59,6 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
     }
 }
 
-// Softmax attention of one query (q_l, HD floats in LDS) over cache rows 0 .. n_cache - 1 (fp16 [HD] rows at
-// kcg / vcg) and, when k_x is not NULL, one more row (k_x, v_x in LDS) after them, as a share of the query's
-// attention (below). NT threads. A thread holds 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG
-// row groups; row group r takes rows r, r + RG, r + 2 RG, ... in batches of UNR rows whose keys and values are
-// loaded together, and keeps a running softmax over them (max m, sum l, the weighted value sums o of its dims):
-//   s_t = (q . k_t) / sqrt(HD), m' = max(m, s_t), l = l e^(m - m') + sum e^(s_t - m'),
-//   o = o e^(m - m') + sum e^(s_t - m') v_t;
-// the row groups are then combined, M = max_r m_r: out[0 .. HD) = sum_r e^(m_r - M) o_r unnormalized,
-// out_ml[0] = M, out_ml[kAttnShares] = sum_r e^(m_r - M) l_r (a chunk's share, combined by the next linear's prep
-// into out / l: the softmax of the scores followed by the weighted sum of the values, the sums in another order).
-// pro(): called once the first batch's loads are issued, before q_l is read (the caller fills q_l, k_x and v_x
-// there and synchronizes the workgroup), so those loads overlap the caller's set-up.
-template <int HD, int NT, class Pro>
-EIF_DEV void attend(const float *q_l, const __half *kcg, const __half *vcg, int n_cache, const float *k_x,
-                    const float *v_x, float inv_sqrt_hd, float *out, float *out_ml, Pro &&pro)
-{
-    constexpr int DPR = HD / 8, RG = NT / DPR, UNR = 8;
-    constexpr int PARTS = NT / HD;   // threads per output dimension in the combine
-    __shared__ __align__(16) float m_l[RG];
-    __shared__ float l_l[RG];
-    __shared__ float o_l[RG][HD + 4];
-    __shared__ float po_l[PARTS][HD], pl_l[PARTS];
-    const int t = threadIdx.x;
-    const int sub = t % DPR, r0 = t / DPR;
-    uint4 kr[UNR], vr[UNR];
-    auto load_batch = [&](int base) {
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int tt = base + u * RG + r0;
-            const size_t off = (size_t)(tt < n_cache ? tt : 0) * HD + 8 * sub;
-            kr[u] = *reinterpret_cast<const uint4 *>(kcg + off);
-            vr[u] = *reinterpret_cast<const uint4 *>(vcg + off);
-        }
-    };
-    load_batch(0);
-    pro();
-    float qv[8], o[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qv[i] = q_l[8 * sub + i], o[i] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
-    auto score = [&](const float (&k8)[8]) {
-        float d = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) d = fmaf(qv[i], k8[i], d);
-#pragma unroll
-        for (int off = 1; off < DPR; off <<= 1) d += __shfl_xor(d, off, 64);
-        return d * inv_sqrt_hd;
-    };
-    for (int base = 0; base < n_cache; base += RG * UNR) {
-        if (base > 0) load_batch(base);
-        float sv[UNR];
-        float bm = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            float k8[8];
-            half8_to_float(kr[u], k8);
-            const float d = score(k8);
-            sv[u] = base + u * RG + r0 < n_cache ? d : -INFINITY;
-            bm = fmaxf(bm, sv[u]);
-        }
-        const float mn = fmaxf(m, bm);
-        if (mn != -INFINITY) {   // the row group has rows in this batch or before
-            const float sc = expf(m - mn);
-            l = l * sc;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = o[i] * sc;
-#pragma unroll
-            for (int u = 0; u < UNR; ++u) {
-                const float pw = expf(sv[u] - mn);
-                const bool ok = base + u * RG + r0 < n_cache;   // a row past the end holds a stand-in row
-                float v8[8];
-                half8_to_float(vr[u], v8);
-                l = l + pw;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, ok ? v8[i] : 0.0f, o[i]);
-            }
-            m = mn;
-        }
-    }
-    if (k_x) {   // uniform
-        float k8[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) k8[i] = k_x[8 * sub + i];
-        const float d = score(k8);   // every row group computes it (uniform shuffles); row group 0 keeps it
-        if (r0 == 0) {
-            const float mn = fmaxf(m, d);
-            const float sc = expf(m - mn), pw = expf(d - mn);
-            l = l * sc + pw;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o[i] = fmaf(pw, v_x[8 * sub + i], o[i] * sc);
-            m = mn;
-        }
-    }
-
-    // combine the row groups
-    if (sub == 0) m_l[r0] = m, l_l[r0] = l;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o_l[r0][8 * sub + i] = o[i];
-    __syncthreads();
-    float mx = -INFINITY;
-#pragma unroll 4
-    for (int r = 0; r < RG; r += 4) {
-        const float4 m4 = *reinterpret_cast<const float4 *>(&m_l[r]);
-        mx = fmaxf(mx, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
-    }
-    {
-        const int d = t % HD, part = t / HD;
-        float os = 0.0f, ls = 0.0f;
-        for (int r = part; r < RG; r += PARTS) {
-            const float w = expf(m_l[r] - mx);   // 0 for a row group without rows
-            os = fmaf(w, o_l[r][d], os);
-            ls = fmaf(w, l_l[r], ls);
-        }
-        po_l[part][d] = os;
-        if (d == 0) pl_l[part] = ls;
-    }
-    __syncthreads();
-    if (t < HD) {
-        float os = po_l[0][t], ls = pl_l[0];
-#pragma unroll
-        for (int q = 1; q < PARTS; ++q) os += po_l[q][t], ls += pl_l[q];
-        out[t] = os;
-        if (t == 0) out_ml[0] = mx, out_ml[kAttnShares] = ls;
-    }
-}
-
 // Decode, split over the positions: workgroup (h, s) takes query head h (kv head g = h / kv_mul) over the
 // positions of chunk s, [s CH, (s + 1) CH), CH = the fewest whole UNITs (the rows one batch of attend<HD, 256>
 // covers) that cover positions 0 .. pos in kAttnShares chunks; cache rows below pos, and row pos itself in the
@@ -213,6 +78,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __hal
 {
     constexpr int HALF = HD / 2, UNIT = attn_chunk<HD>();
     __shared__ float q_l[HD], k_l[HD], v_l[HD];
+    __shared__ AttnLds<HD, 256> att_l;
     const int h = blockIdx.x, sc = blockIdx.y, kv_mul = n_heads / n_kv, g = h / kv_mul;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
     const int t = threadIdx.x;
@@ -251,8 +117,8 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __hal
     };
     const size_t base = ((size_t)g * seq_len + c0) * HD;
     const int rows = (last ? pos : c0 + ch) - c0;
-    attend<HD, 256>(q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr, inv_sqrt_hd,
-                          sh_o + ((size_t)h * kAttnShares + sc) * HD, ml, rotate);
+    attend<HD, 256>(att_l, t, true, q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr,
+                    inv_sqrt_hd, sh_o + ((size_t)h * kAttnShares + sc) * HD, ml, rotate);
 }
 
 // Prefill, step 1: token i of a batch at position pos0 + i (one workgroup per token). RoPE of every query head
@@ -495,8 +361,10 @@ __global__ void prefill_state_kernel(int *state, int *seq, const int *prompt, in
 // pos + 1 of the sequence, the position advances, and x becomes the next token's embedding row.
 __global__ __launch_bounds__(1024) void sample_kernel(const float *part_v, const int *part_i, int n_part, int *state,
                                                       const int *prompt, int *seq, int seq_len, const int8_t *emb,
-                                                      const float *emb_scale, float *x, int dim, int vocab)
+                                                      const float *emb_scale, float *x, int dim, int vocab, int *bar)
 {
+    // the persistent step's barrier words back to zero for the next step (that step ended before this launch)
+    if (bar && (int)threadIdx.x < eif::kPersistBarWords) bar[(size_t)eif::kPersistBarStride * threadIdx.x] = 0;
     __shared__ float bv[16];
     __shared__ int bi[16];
     __shared__ int next_l;
@@ -598,14 +466,25 @@ struct eif_hip_bitnet {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     hipStream_t cap = nullptr;       // the stream the step is captured on (the legacy stream cannot capture)
+    // the persistent step (persist.hip): made at the first step when the shapes allow it
+    eif::PersistPlan *plan = nullptr;
+    int plan_state = 0;              // 0 not tried, 1 made, -1 shapes outside the persistent step
+    int use_persist = 0;             // requested (eif_hip_bitnet_set_persistent); separate launches by default
 };
 
 namespace {
 
 int enqueue_head(eif_hip_bitnet *m, hipStream_t st);
 
+int enqueue_head_gemv(eif_hip_bitnet *m, hipStream_t st);
+
 int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
 {
+    if (m->plan && m->use_persist) {   // the layer stack and the head's prep as one launch, then head and sampler
+        const int rc = eif::persist_enqueue(m->plan, st);
+        if (rc) return rc;
+        return enqueue_head_gemv(m, st);
+    }
     const eif_hip_bitnet_config &c = m->c;
     const float inv_sqrt_hd = 1.0f / sqrtf((float)c.head_dim);
     for (int l = 0; l < c.n_layers; ++l) {
@@ -647,13 +526,58 @@ int enqueue_head(eif_hip_bitnet *m, hipStream_t st)
     const eif_hip_bitnet_config &c = m->c;
     eif_hip_prep_spec sp{};
     sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_final, sp.eps = c.rms_eps;
-    int rc = eif_hip_prep_spec_rows(&sp, c.dim, m->hq, m->head_kpad, m->hs, 1, st);
+    const int rc = eif_hip_prep_spec_rows(&sp, c.dim, m->hq, m->head_kpad, m->hs, 1, st);
     if (rc) return rc;
+    return enqueue_head_gemv(m, st);
+}
+
+// The head GEMV on the prepped row (hq, hs) with per-tile maxima, then the sampler.
+int enqueue_head_gemv(eif_hip_bitnet *m, hipStream_t st)
+{
+    const eif_hip_bitnet_config &c = m->c;
+    int rc;
     if ((rc = eif::qlinear_argmax(m->head, m->hq, m->head_kpad, m->hs, m->logits, m->amax_v, m->amax_i, st)))
         return rc;
     sample_kernel<<<1, 1024, 0, st>>>(m->amax_v, m->amax_i, m->head_tiles, m->state, m->prompt, m->seq, c.seq_len,
-                                      m->emb, m->emb_scale, m->x, c.dim, c.vocab);
+                                      m->emb, m->emb_scale, m->x, c.dim, c.vocab, eif::persist_bar(m->plan));
     EIF_HIP_LAUNCHED();
+    return EIF_HIP_OK;
+}
+
+// The persistent step's plan, made once all weights are set (or left unmade when the shapes are outside it).
+void ensure_plan(eif_hip_bitnet *m)
+{
+    if (m->plan_state != 0) return;
+    const eif_hip_bitnet_config &c = m->c;
+    eif::PersistModel pm{};
+    pm.n_layers = c.n_layers, pm.dim = c.dim, pm.hidden = c.hidden, pm.q_dim = m->q_dim, pm.kv_dim = m->kv_dim;
+    pm.n_heads = c.n_heads, pm.n_kv = c.n_kv_heads, pm.head_dim = c.head_dim, pm.seq_len = c.seq_len;
+    pm.rms_eps = c.rms_eps, pm.sub_eps = c.sub_eps;
+    pm.wht_dim = c.wht_dim, pm.wht_q = c.wht_q, pm.wht_hidden = c.wht_hidden;
+    pm.norm_dim = c.wht_norm_dim, pm.norm_q = c.wht_norm_q, pm.norm_hidden = c.wht_norm_hidden;
+    pm.signs_dim = m->signs_dim, pm.signs_q = m->signs_q, pm.signs_hidden = m->signs_hidden;
+    pm.wqkv = m->wqkv.data(), pm.wo = m->wo.data(), pm.w13 = m->w13.data(), pm.w2 = m->w2.data();
+    pm.rms_att = m->rms_att.data(), pm.rms_ffn = m->rms_ffn.data();
+    pm.rms_sub_att = m->rms_sub_att.data(), pm.rms_sub_ffn = m->rms_sub_ffn.data();
+    pm.x = m->x, pm.qkv = m->qkv, pm.hb = m->hb, pm.sh_o = m->sh_o, pm.sh_ml = m->sh_ml;
+    pm.kc = m->kc, pm.vc = m->vc, pm.rope = m->rope, pm.state = m->state;
+    pm.rms_final = m->rms_final, pm.hq = m->hq, pm.hs = m->hs, pm.head_kpad = m->head_kpad;
+    eif::PersistPlan *p = nullptr;
+    if (eif::persist_create(&p, pm) == EIF_HIP_OK) {
+        m->plan = p;
+        m->plan_state = 1;
+    } else {
+        m->plan_state = -1;
+    }
+}
+
+// EIF_HIP_E_DEVICE when a persistent step gave up at a barrier (synchronous; clears nothing).
+int check_plan(eif_hip_bitnet *m, hipStream_t st)
+{
+    if (m->plan && eif::persist_failed(m->plan, st)) {
+        fprintf(stderr, "libbitllm_hip: a persistent decode step gave up waiting at a grid barrier\n");
+        return EIF_HIP_E_DEVICE;
+    }
     return EIF_HIP_OK;
 }
 
@@ -971,6 +895,7 @@ int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, voi
     EIF_HIP_LAUNCHED();
     fill_half_kernel<<<1024, 256, 0, st>>>(m->vc, cache);
     EIF_HIP_LAUNCHED();
+    if (m->plan && eif::persist_reset(m->plan, st)) return EIF_HIP_E_DEVICE;
     start_kernel<<<1, 1, 0, st>>>(m->state, m->seq, m->prompt, n_prompt);
     EIF_HIP_LAUNCHED();
     embed_kernel<<<1, 256, 0, st>>>(m->emb, m->emb_scale, m->state, m->x, c.dim, c.vocab);   // each step
@@ -989,6 +914,7 @@ int eif_hip_bitnet_steps(eif_hip_bitnet *m, int n, int use_graph, void *stream)
         if (!m->wqkv[l]) return EIF_HIP_E_ARG;
     if (m->hpos + n > m->c.seq_len) return EIF_HIP_E_LIMIT;
     hipStream_t st = (hipStream_t)stream;
+    ensure_plan(m);
     if (use_graph && !m->exec) {   // capture once, on the model's own stream; replay on the caller's
         if (!m->cap) EIF_HIP_TRY(hipStreamCreateWithFlags(&m->cap, hipStreamNonBlocking));
         EIF_HIP_TRY(hipStreamBeginCapture(m->cap, hipStreamCaptureModeRelaxed));
@@ -1031,6 +957,7 @@ int eif_hip_bitnet_prefill(eif_hip_bitnet *m, int n, void *stream)
 int eif_hip_bitnet_tokens(eif_hip_bitnet *m, int *out, int n, void *stream)
 {
     if (!m || !out || n < 0 || n > m->c.seq_len) return EIF_HIP_E_ARG;
+    if (const int rc = check_plan(m, (hipStream_t)stream)) return rc;
     EIF_HIP_TRY(hipMemcpyAsync(out, m->seq, sizeof(int) * n, hipMemcpyDeviceToHost, (hipStream_t)stream));
     EIF_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
     return EIF_HIP_OK;
@@ -1039,6 +966,7 @@ int eif_hip_bitnet_tokens(eif_hip_bitnet *m, int *out, int n, void *stream)
 int eif_hip_bitnet_logits(eif_hip_bitnet *m, float *out, void *stream)
 {
     if (!m || !out) return EIF_HIP_E_ARG;
+    if (const int rc = check_plan(m, (hipStream_t)stream)) return rc;
     EIF_HIP_TRY(hipMemcpyAsync(out, m->logits, sizeof(float) * m->c.vocab, hipMemcpyDeviceToHost, (hipStream_t)stream));
     EIF_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
     return EIF_HIP_OK;
@@ -1047,6 +975,7 @@ int eif_hip_bitnet_logits(eif_hip_bitnet *m, float *out, void *stream)
 int eif_hip_bitnet_position(eif_hip_bitnet *m, void *stream)
 {
     if (!m) return EIF_HIP_E_ARG;
+    if (const int rc = check_plan(m, (hipStream_t)stream)) return rc;
     int s[4];
     EIF_HIP_TRY(hipMemcpyAsync(s, m->state, sizeof(s), hipMemcpyDeviceToHost, (hipStream_t)stream));
     EIF_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
@@ -1077,6 +1006,24 @@ int eif_hip_bitnet_kv_cache(eif_hip_bitnet *m, int layer, int pos0, int n, float
     return EIF_HIP_OK;
 }
 
+int eif_hip_bitnet_set_persistent(eif_hip_bitnet *m, int on)
+{
+    if (!m || on < -1 || on > 1) return EIF_HIP_E_ARG;
+    for (int l = 0; l < m->c.n_layers; ++l)
+        if (!m->wqkv[l]) return EIF_HIP_E_ARG;
+    if (!m->head) return EIF_HIP_E_ARG;
+    ensure_plan(m);
+    if (on >= 0 && on != m->use_persist) {
+        m->use_persist = on;
+        if (m->exec) {   // the captured step holds the other path: capture again at the next graph step
+            (void)hipGraphExecDestroy(m->exec);
+            (void)hipGraphDestroy(m->graph);
+            m->exec = nullptr, m->graph = nullptr;
+        }
+    }
+    return m->plan && m->use_persist ? 1 : 0;
+}
+
 int eif_hip_bitnet_get_config(const eif_hip_bitnet *m, eif_hip_bitnet_config *out)
 {
     if (!m || !out) return EIF_HIP_E_ARG;
@@ -1098,6 +1045,7 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
     if (m->cap) (void)hipStreamDestroy(m->cap);
+    eif::persist_destroy(m->plan);
     free_prefill(m);
     for (auto *v : {&m->wqkv, &m->wo, &m->w13, &m->w2})
         for (eif_hip_qweight *q : *v) eif_hip_qweight_destroy(q);

@@ -79,6 +79,14 @@ int launch_quant_rows(const float *x, int ldx, int M, int K, int8_t *xq, int ldq
 int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *xq, int ldq, const float *xs,
                    const float *bias, float *y, int ldy, int M, int path, hipStream_t st);
 int qweight_row_tiles(const eif_hip_qweight *w);
+// The GPU layout of a resident weight (qlinear.hip): codes W (rows padded to 64, wld bytes per row), scales
+// ([rows, G] grouped, [rows] row-scaled or NULL), format, group (0: row-scaled), steps of the layout along K.
+struct QView {
+    const uint8_t *W;
+    const float *scales;
+    int fmt, rows, cols, group, ud, kpad, rows_pad, nsteps, wld, G;
+};
+int qweight_view(const eif_hip_qweight *w, QView *v);
 // The fused-prep linear of one token row (M = 1) whose input row is combined from attention shares in the prep:
 // column c = h hd + d is sum_s e^(M_s - M) O_s[d] / sum_s e^(M_s - M) L_s over the shares s of head h, M = max_s M_s,
 // with sh_o [K / hd][kAttnShares][hd] the outputs O_s and sh_ml [K / hd][2 kAttnShares] the maxima M_s, then the

@@ -76,6 +76,20 @@ int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *
  * must be set.                                                                                          */
 int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, void *stream);
 
+/* How a token step runs: on = 0 (the default) as separate launches per linear and attention, replayed as a HIP
+ * graph; on = 1 the layer stack as one persistent kernel (one workgroup per CU, grid barriers between the stages,
+ * the next layer's weight tiles streamed into LDS while the current layer computes; src/eif_tinyllm.c:371-857's
+ * layer loop), then the head GEMV and the sampler. Both give the same bits. The persistent form is slower on
+ * MI355X at the BitNet-2B shape (1.72 against 1.14 ms per token): every stage's fused activation prep is a
+ * dependent chain of 1.8-4.5 us that the separate launches overlap with their weight loads, while the persistent
+ * kernel, whose weights are already in LDS, waits for it and for a grid barrier of about 1.8 us per stage.
+ * Shapes outside the persistent kernel (head_dim other than 128, row-scaled ternary matrices, ...) always take
+ * the separate launches. on = -1 only queries. Returns 1 when steps run persistent, 0 when not, or a negative
+ * error (all layers and the globals must be set). A persistent step that gives up waiting at a grid barrier (all
+ * workgroups could not run at once) makes the next eif_hip_bitnet_tokens / _logits / _position return
+ * EIF_HIP_E_DEVICE.                                                                                     */
+int eif_hip_bitnet_set_persistent(eif_hip_bitnet *m, int on);
+
 /* Runs n token steps from the current position. The step at position p consumes the current token and
  * makes the next: the prompt's token p + 1 while the prompt lasts, the argmax of the logits after. Each
  * made token is stored at index p + 1 of the sequence. Steps past seq_len return EIF_HIP_E_LIMIT.

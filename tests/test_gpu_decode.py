@@ -347,6 +347,79 @@ def test_decode_bitnet2b_full_size(gpu, oracle):
         m.close()
 
 
+def run_path(m, prompt, prefill, n_steps, persistent, graph):
+    """Prefill, then n_steps token steps on one path; the sequence, last logits and every layer's KV cache."""
+    L = m.cfg["n_layers"]
+    m.set_persistent(persistent)
+    m.reset(prompt)
+    if prefill:
+        m.prefill(prefill)
+    m.steps(n_steps, graph=graph)
+    n = prefill + n_steps
+    return m.tokens(n + 1), m.logits(), [m.kv_cache(layer, 0, n) for layer in range(L)]
+
+
+def assert_same_bits(a, b):
+    ta, la, kva = a
+    tb, lb, kvb = b
+    assert np.array_equal(ta, tb)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    for (ka, va), (kb, vb) in zip(kva, kvb):
+        assert np.array_equal(ka.view(np.uint32), kb.view(np.uint32))
+        assert np.array_equal(va.view(np.uint32), vb.view(np.uint32))
+
+
+def test_persistent_step_same_bits(gpu):
+    """The persistent token step (one launch for the layer stack) against the separate launches: the same tokens,
+    logits and KV cache bits, eagerly and replayed as a graph, over attention chunks of 128 positions and across
+    the change to 256 at position 1024 (head_dim 128, g128 inputs, g96 down, WHT-128, 8/2 heads)."""
+    cfg = synth.bitnet_config(512, 768, 3, 8, 2, 128, 1000, 1280, 128, 96, 128, 128, 128)
+    w = synth.bitnet_model((41,), cfg)
+    prompt = list(np.random.default_rng(42).integers(0, cfg["vocab"], 1020))
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        assert m.set_persistent(True)
+        sep = run_path(m, prompt, 1000, 40, False, graph=False)
+        per = run_path(m, prompt, 1000, 40, True, graph=False)
+        assert_same_bits(sep, per)
+        per_g = run_path(m, prompt, 1000, 40, True, graph=True)
+        assert_same_bits(sep, per_g)
+        short = run_path(m, prompt[:5], 0, 30, True, graph=True)   # from position 0, one chunk
+        assert_same_bits(run_path(m, prompt[:5], 0, 30, False, graph=False), short)
+    finally:
+        m.close()
+
+
+def test_persistent_step_bitnet2b_same_bits(gpu):
+    """The persistent step of the 30-layer BitNet-b1.58-2B-shaped model (dim 2560, FFN 6912, 20/5 heads x 128,
+    g128 / g96 down, 128256-row INT8 head, context 2048) gives the separate launches' bits after a 512-token
+    prefill: 16 greedy tokens, the last logits and all 30 layers' KV caches."""
+    cfg = synth.bitnet_config(**synth.BITNET_2B_DECODE)
+    w = synth.bitnet_model((31,), cfg)
+    prompt = [int(t) for t in np.random.default_rng(32).integers(0, cfg["vocab"], 513)]
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        assert m.set_persistent(True)
+        sep = run_path(m, prompt, 512, 16, False, graph=True)
+        per = run_path(m, prompt, 512, 16, True, graph=True)
+        assert_same_bits(sep, per)
+    finally:
+        m.close()
+
+
+def test_persistent_unsupported_shapes_fall_back(gpu):
+    """Shapes outside the persistent kernel (head_dim 32, g32) keep the separate launches."""
+    cfg, w = tiny()
+    m = gpu.BitnetModel(cfg, w)
+    try:
+        assert not m.set_persistent(True)
+        m.reset([3])
+        m.steps(3)
+        assert m.position() == 3
+    finally:
+        m.close()
+
+
 def check_prefill(gpu, oracle, cfg, w, prompt, chunks):
     """Prefill in the given chunks; every prompt position checked one step at a time against the oracle given
     the GPU's cache of the positions before it: that position's keys and values in every layer and, at the
