@@ -17,12 +17,20 @@ GOLD = os.path.join(ROOT, "tests", "golden", "reference_vectors.npz")
 
 @pytest.fixture(scope="module")
 def gold():
-    return np.load(GOLD)
+    # Every array materialized once and kept for the module: the host API keeps device copies of weight buffers
+    # keyed by their host address (weights live in stable pools, as in the reference), so a weight array must not
+    # be freed and another allocated at its address while its copy is cached. An NpzFile makes a new array on
+    # every access.
+    with np.load(GOLD) as z:
+        return {k: z[k] for k in z.files}
 
 
 @pytest.fixture(scope="module")
 def lib(gpu):
-    return gpu.load()
+    lib = gpu.load()
+    lib.eif_hip_forget_host_weights(None)   # no copies left by earlier tests' freed buffers
+    yield lib
+    lib.eif_hip_forget_host_weights(None)
 
 
 def bits(a):
