@@ -100,6 +100,8 @@ _SIGS = {
                                   C.POINTER(_sz)]),
     "eif_hip_qlinear": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_ex": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "eif_hip_qlinear_ex_noalloc": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp]),
+    "eif_hip_qlinear_noalloc_max_bytes": (C.c_size_t, []),
     "eif_hip_qlinear_acc": (_i, [_vp, _vp, _i, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_f32": (_i, [_vp, _vp, _i, _vp, _i, _f, _vp, _vp, _i, _i, _vp]),
     "eif_hip_qlinear_f32_acc": (_i, [_vp, _vp, _i, _vp, _i, _f, _vp, _i, _vp]),

@@ -217,7 +217,8 @@ int eif_hip_init(int device)
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, device) != hipSuccess || strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return EIF_HIP_E_DEVICE;
-    return hipSetDevice(device) == hipSuccess ? EIF_HIP_OK : EIF_HIP_E_DEVICE;
+    if (hipSetDevice(device) != hipSuccess) return EIF_HIP_E_DEVICE;
+    return eif::scratch_init(device, nullptr);   // the no-alloc entry point's scratch address on this device
 }
 
 const char *eif_hip_strerror(int code)

@@ -706,13 +706,11 @@ int g_gemm_split = 0;   // splits along K of the GEMM, 0 = chosen from the shape
 // rounds of workgroups per unit of work, ceil(tiles s / CUs) / s, the smallest of equal ones. One round or
 // more: 2 when a long K (24 steps or more) leaves the last round under 70% full (e.g. 320 tiles on 256 CUs).
 // 1 for the parity outputs and when no workspace can be had (first use of a stream inside a graph capture).
-template <bool ACC>
-int pick_split(QArgs &a, int tiles, hipStream_t st)
+int choose_split(int nsteps, int tiles)
 {
-    if (ACC) return 1;
     int ks = g_gemm_split;
     if (ks == 0) {
-        const int C = device_cus(), smax = std::min(16, std::max(1, a.nsteps / 3));
+        const int C = device_cus(), smax = std::min(16, std::max(1, nsteps / 3));
         if (tiles < C) {
             ks = 1;
             double best = 1.0;
@@ -722,12 +720,46 @@ int pick_split(QArgs &a, int tiles, hipStream_t st)
             }
         } else {
             const int rounds = eif_ceil_div(tiles, C);
-            ks = a.nsteps >= 24 && (double)tiles < 0.7 * rounds * C ? 2 : 1;
+            ks = nsteps >= 24 && (double)tiles < 0.7 * rounds * C ? 2 : 1;
         }
     }
-    ks = std::min(ks, std::min(16, std::max(1, a.nsteps / 3)));
+    return std::min(ks, std::min(16, std::max(1, nsteps / 3)));
+}
+
+// The fixed scratch of eif_hip_qlinear_ex_noalloc: the GEMM's split-along-K partials, kScratchFloats floats in the
+// code object's device memory (every device the library runs on holds one until the process ends). Host code
+// uses its address per device from hipGetSymbolAddress (g_scratch_dev), never the array's name.
+constexpr size_t kScratchFloats = (size_t)8 << 20;   // 32 MiB
+static __device__ __align__(256) float scratch[kScratchFloats];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_dev[kMaxDevices];
+
+// Token tile of the GEMM (16 x TT tokens, see launch_gemm) and its row tiles x token tiles for M tokens.
+int gemm_tt(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+int gemm_tiles(int rows_pad, int M) { return rows_pad / 64 * eif_ceil_div(M, 16 * gemm_tt(M)); }
+
+// A caller-provided split workspace (eif_hip_qlinear_ex_noalloc): while set on this thread, the GEMM takes its
+// split partials from it instead of the per-stream workspace.
+struct FixedWs {
+    float *ptr = nullptr;
+    size_t bytes = 0;
+};
+thread_local FixedWs tl_fixed_ws;
+
+template <bool ACC>
+int pick_split(QArgs &a, int tiles, hipStream_t st)
+{
+    if (ACC) return 1;
+    const int ks = choose_split(a.nsteps, tiles);
     if (ks <= 1) return 1;
-    a.part = split_ws(st, (size_t)ks * a.M * a.N * sizeof(float));
+    const size_t bytes = (size_t)ks * a.M * a.N * sizeof(float);
+    if (tl_fixed_ws.ptr) {   // a fixed workspace too small for this split: -1, nothing is launched
+        if (bytes > tl_fixed_ws.bytes) return -1;
+        a.part = tl_fixed_ws.ptr;
+        return ks;
+    }
+    a.part = split_ws(st, bytes);
     return a.part ? ks : 1;
 }
 
@@ -737,7 +769,9 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     // the kernel addresses the batch rows and the weights with 32-bit offsets
     if ((size_t)a.M * a.ldq >= ((size_t)1 << 32) || (size_t)rows_pad * a.wld >= ((size_t)1 << 32)) return EIF_HIP_E_LIMIT;
     const int tm = eif_ceil_div(a.M, 16 * TT), tiles = rows_pad / 64 * tm;
+    static_assert(TT == 1 || TT == 2 || TT == 4, "token tiles of gemm_tt");
     const int ks = pick_split<ACC>(a, tiles, st);
+    if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
     qgemm_kernel<FMT, UD, GROUPED, ACC, TT><<<grid, kGemmThreads, 0, st>>>(a);
     EIF_HIP_LAUNCHED();
@@ -753,9 +787,11 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemm(const QArgs &a, int rows_pad, hipStream_t st)
 {
-    if (a.M <= 16) return launch_gemm_t<FMT, UD, GROUPED, ACC, 1>(a, rows_pad, st);
-    if (a.M <= 32) return launch_gemm_t<FMT, UD, GROUPED, ACC, 2>(a, rows_pad, st);
-    return launch_gemm_t<FMT, UD, GROUPED, ACC, 4>(a, rows_pad, st);
+    switch (gemm_tt(a.M)) {
+    case 1: return launch_gemm_t<FMT, UD, GROUPED, ACC, 1>(a, rows_pad, st);
+    case 2: return launch_gemm_t<FMT, UD, GROUPED, ACC, 2>(a, rows_pad, st);
+    default: return launch_gemm_t<FMT, UD, GROUPED, ACC, 4>(a, rows_pad, st);
+    }
 }
 
 // Waves per tile of the small-batch GEMV (measured on MI355X with graph-chained launches): two steps per wave
@@ -1064,6 +1100,25 @@ namespace eif {
 
 int qweight_row_tiles(const eif_hip_qweight *w) { return w ? w->rows_pad / 16 : 0; }
 
+// The address of this device's scratch (device current), made once per device at eif_hip_init or at the first
+// eif_hip_qlinear_ex_noalloc call on the device.
+int scratch_init(int device, float **out)
+{
+    if (device < 0 || device >= kMaxDevices) return EIF_HIP_E_DEVICE;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_dev[device]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            fprintf(stderr, "libbitllm_hip: hipGetSymbolAddress(scratch) failed: %s\n", hipGetErrorString(e));
+            return EIF_HIP_E_DEVICE;
+        }
+        g_scratch_dev[device] = static_cast<float *>(ptr);
+    }
+    if (out) *out = g_scratch_dev[device];
+    return EIF_HIP_OK;
+}
+
 int qweight_view(const eif_hip_qweight *w, QView *v)
 {
     if (!w || !v) return EIF_HIP_E_ARG;
@@ -1363,6 +1418,23 @@ int eif_hip_qlinear_ex(const eif_hip_qweight *w, const int8_t *xq, int ldq, cons
     if (!w) return EIF_HIP_E_ARG;
     return eif::qlinear_scaled(w, w->scales, xq, ldq, xs, bias, y, ldy, M, path, (hipStream_t)stream);
 }
+
+int eif_hip_qlinear_ex_noalloc(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs,
+                               const float *bias, float *y, int ldy, int M, int path, void *stream)
+{
+    if (!w) return EIF_HIP_E_ARG;
+    int dev = 0;
+    float *ws = nullptr;
+    if (hipGetDevice(&dev) != hipSuccess) return EIF_HIP_E_DEVICE;
+    const int rc = eif::scratch_init(dev, &ws);
+    if (rc) return rc;
+    tl_fixed_ws = FixedWs{ws, kScratchFloats * sizeof(float)};
+    const int r = eif::qlinear_scaled(w, w->scales, xq, ldq, xs, bias, y, ldy, M, path, (hipStream_t)stream);
+    tl_fixed_ws = FixedWs{};
+    return r;
+}
+
+size_t eif_hip_qlinear_noalloc_max_bytes(void) { return kScratchFloats * sizeof(float); }
 
 int eif_hip_qlinear(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, const float *bias,
                     float *y, int ldy, int M, void *stream)

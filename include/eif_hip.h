@@ -88,6 +88,17 @@ int eif_hip_qlinear(const eif_hip_qweight *w, const int8_t *xq, int ldq, const f
 int eif_hip_qlinear_ex(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, const float *bias,
                        float *y, int ldy, int M, int path, void *stream);
 
+/* eif_hip_qlinear_ex that allocates nothing (no counterpart in the reference; for callers that cannot call
+ * hipMalloc: code under HIP graph capture, tight serving loops, harnesses that forbid allocation). The GEMM's
+ * split-along-K partials go to a fixed scratch in the library's device memory, eif_hip_qlinear_noalloc_max_bytes()
+ * bytes (32 MiB) per device, instead of a per-stream workspace allocated on first use; a call whose split needs more
+ * returns EIF_HIP_E_LIMIT and launches nothing. Results are those of eif_hip_qlinear_ex (the same split, the same
+ * bits). Every call on a device shares that device's scratch, which keeps the last call's contents: calls that
+ * overlap on one device (other streams, other threads) race and must be serialized by the caller.       */
+int eif_hip_qlinear_ex_noalloc(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs,
+                               const float *bias, float *y, int ldy, int M, int path, void *stream);
+size_t eif_hip_qlinear_noalloc_max_bytes(void);
+
 /* Exact int32 accumulators of the same kernels: grouped ternary -> acc [M, rows, ngroups]; row-scaled -> acc
  * [M, rows]. For parity tests.                                                                          */
 int eif_hip_qlinear_acc(const eif_hip_qweight *w, const int8_t *xq, int ldq, int32_t *acc, int M, int path,
