@@ -284,6 +284,46 @@ def test_fp32_gemvs_vs_ref(oracle, ref):
         assert rel_err(y, want, mag * sc) < 1e-5
 
 
+GROUPED_SHAPES = [
+    # N, K, group, M: the single BitNet linear (one token and a batch), then the BitNet-2B layer's linears
+    (6912, 2560, 128, 1),
+    (6912, 2560, 128, 3),
+] + [(N, K, g, 2) for _, N, K, g in synth.BITNET_2B_LAYER if _ != "up"] + [
+    (130, 200, 32, 2),   # ragged: a short last group and a row count off the tiles
+]
+
+
+@pytest.mark.parametrize("N,K,g,M", GROUPED_SHAPES)
+def test_ternary_gemv_grouped_vs_double(oracle, N, K, g, M):
+    # orc_ternary_gemv_grouped (the GPU linear's FP32 contract) against the float64 closed form
+    #   y[m, r] = xs[m] * sum_g s[r, g] * sum_{k in g} code[r, k] * xq[m, k] + bias[r],
+    # built from unpacked codes, per-group slices and a matrix product, to 1e-5 of sum_g |s * acc_g| * xs + |bias|.
+    # Planted mistakes it catches (each checked on the CPU): a dropped last group, scales indexed [g, r], xs of
+    # token 0 for every token, the bias added before the xs multiply.
+    w, s = synth.ternary_weight((60, N, K, g), N, K, g)
+    x = synth.activations((61, M, K), M, K)
+    kpad = -(-K // 128) * 128
+    xq = np.zeros((M, kpad), np.int8)
+    xs = np.zeros(M, np.float32)
+    assert oracle.orc_prep_rows(P(x), K, None, M, K, 0, 1.0, P(xq), kpad, P(xs), None, 0) == 0
+    bias = synth.rng(62, N).standard_normal(N).astype(np.float32)
+    codes = synth.unpack_ternary(w, K).astype(np.float64)
+    ng = -(-K // g)
+    want = np.zeros((M, N))
+    mag = np.zeros((M, N))
+    for gi in range(ng):
+        a = xq[:, gi * g:min(K, (gi + 1) * g)].astype(np.float64) @ codes[:, gi * g:min(K, (gi + 1) * g)].T
+        want += a * s[None, :, gi]
+        mag += np.abs(a) * s[None, :, gi]
+    want = want * xs[:, None].astype(np.float64) + bias[None, :]
+    mag = mag * xs[:, None].astype(np.float64) + np.abs(bias)[None, :]
+    for b in (None, bias):
+        y = np.full((M, N), np.nan, np.float32)
+        oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), kpad, P(xs), P(b), P(y), N, M, N, K)
+        wb = want if b is not None else want - bias[None, :]
+        assert rel_err(y, wb, mag) <= 1e-5, (N, K, g, M, b is not None)
+
+
 def test_int8_int4_fp32_bounds_vs_ref(oracle, ref):
     # tests/test_int8_gemv.c:10-56 and tests/test_q35_int4.c:5-51: FP32-activation paths exact to rounding
     r = rng(4)
