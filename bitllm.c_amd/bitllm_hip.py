@@ -109,6 +109,7 @@ _SIGS = {
     "eif_hip_gemm_min_tokens": (_i, []),
     "eif_hip_set_gemv_ksplit": (_i, [_i]),
     "eif_hip_set_gemv_row_tiles": (_i, [_i]),
+    "eif_hip_set_gemv_token_chunk": (_i, [_i]),
     "eif_hip_set_gemv_prep_cols": (_i, [_i]),
     "eif_hip_set_gemm_split": (_i, [_i]),
     "eif_hip_forget_host_weights": (None, [_vp]),

@@ -56,6 +56,8 @@ struct QArgs {
     float *part;           // GEMM split along K: partial sums [split][M][N]
     float *amax_v;         // row-scaled GEMV, M = 1: per 16-row tile, the largest output and its row
     int *amax_i;           //   (first of equal maxima; NaN never wins), or NULL
+    int mw;                // GEMV: token rows per workgroup (0: all M in one workgroup)
+    int nrb;               // GEMV with token chunks: row blocks (workgroups along the rows per chunk)
 };
 
 // ---- tiled GEMM (token batches above the small-batch GEMV) ----
@@ -270,6 +272,12 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(QArgs a, int ks)
 
 // ---- small-batch GEMV (M <= kGemvMaxM): RT 16-row tiles per workgroup, ks waves per tile ----
 //
+// One MFMA covers 16 token rows (a token tile); a workgroup takes TT token tiles, each decoded weight step
+// feeding TT MFMAs. A batch larger than the workgroup's rows (mw) is cut into token chunks, one workgroup per
+// (row block, chunk). The workgroups of one row block are given ids 8 apart, which the dispatcher places on
+// the same XCD one after another, so they read the same weight tile at about the same time through that XCD's
+// L2. Each chunk's outputs are those of the whole batch (every token row is computed on its own).
+//
 // Each wave owns some steps of one tile. Order of work, chosen so no load waits on another:
 //   1. the activation loads (the FP32 row slice of the fused prep, or the int8 row pieces to stage) and the
 //      workgroup's group scales (one contiguous block of the scale array),
@@ -284,7 +292,14 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(QArgs a, int ks)
 // instruction of a wave is on its critical path (one or two waves per SIMD), so the prep is written for a
 // short per-thread chain: few columns per thread, the WHT block fixed at compile time, DPP butterflies.
 
-constexpr int kGemvMaxM = 8;
+constexpr int kGemvMaxM = 63;    // token rows of the GEMV path (the GEMM takes 64 and more)
+constexpr int kGemvTileM = 16;   // token rows of one MFMA (a token tile)
+constexpr int kGemvMaxTT = 4;    // token tiles per workgroup
+// Default token rows per workgroup above kFusedMaxM: two tiles. Four tiles staged at once (up to 64 rows of
+// activations and their sums) hold a workgroup to one per CU with nothing to overlap its staging; measured
+// slower than 32-row chunks on every shape tried.
+constexpr int kGemvDefaultWgM = 32;
+constexpr int kFusedMaxM = 8;    // token rows of the fused-prep GEMV (each workgroup preps them one by one)
 constexpr int kMaxPieces = 4;
 constexpr int kMaxScLoads = 8;
 
@@ -292,24 +307,41 @@ constexpr int kMaxScLoads = 8;
 // RT row tiles of 16 rows per workgroup; wave w works on tile w % RT and on steps w / RT, w / RT + ks, ... of
 // it (ks = waves / RT). SPW: steps per wave held in registers at once; the first SPW are loaded unconditionally
 // (a wave with fewer steps loads its last step again and skips the copies), later chunks only when a row has
-// more steps. SH: one token row combined from attention shares (PrepArgs::sh_o) in the prep.
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, bool SH = false>
+// more steps. TT: token tiles (E = 0 only). SH: one token row combined from attention shares (PrepArgs::sh_o)
+// in the prep.
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT = 1, bool SH = false>
 __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 {
+    static_assert(TT == 1 || E == 0, "token tiles with staged activations only");
     using GE = Geo<FMT, UD>;
     constexpr int NW = GE::SB / 4;
     constexpr int EV = E > 0 ? E : 4;
     constexpr int MS = SPW;
     constexpr int TR = 16 * RT;   // rows per workgroup
     extern __shared__ __align__(16) int8_t smem[];
-    __shared__ float xs_l[kGemvMaxM];
+    __shared__ float xs_l[kGemvTileM * TT];
     __shared__ float red_max[16], red_ss[16];
+    // token chunks: workgroup id -> (row block, chunk); ids 8 apart share the XCD (see above)
+    int rb = blockIdx.x;
+    if (a.mw > 0 && a.mw < a.M) {   // uniform
+        const int nch = (a.M + a.mw - 1) / a.mw;
+        const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+        const int ch = k % nch;
+        rb = (k / nch) * 8 + xcd;
+        if (rb >= a.nrb) return;   // the grid is rounded up to whole XCD rounds
+        const int m0 = ch * a.mw;
+        a.M = min(a.mw, a.M - m0);
+        a.xq += (size_t)m0 * a.ldq;
+        a.xs += m0;
+        a.y += (size_t)m0 * a.ldy;
+        if (a.acc) a.acc += (size_t)m0 * a.N * (GROUPED ? a.G : 1);
+    }
     const int ks = (blockDim.x >> 6) / RT;
     // the wave index through readfirstlane: a scalar, so the per-wave step bounds below are scalar branches
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rt = wv % RT, kw = wv / RT;
     const int r16 = lane & 15, s = lane >> 4;
-    const int row0 = blockIdx.x * TR;
+    const int row0 = rb * TR;
     const int row = row0 + 16 * rt + r16;
     const bool row_ok = row < a.N;
     const int kpad = a.nsteps * GE::SC;
@@ -426,12 +458,11 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         }
     }
 
-    // 4. MFMAs. A lane's accumulator holds tokens 4s .. 4s+3 (ntok of them live) of row r16.
-    const bool tok_ok = r16 < a.M;
-    const int8_t *xl = lds_x + (tok_ok ? r16 : 0) * p.ldl;
-    const int ntok = min(4, a.M - 4 * s);
-    int32_t *accp = acc_l + ((4 * s) * TR + 16 * rt + r16) * gld;
-    v4i C = {0, 0, 0, 0};
+    // 4. MFMAs. Token tile t: a lane's accumulator C[t] holds tokens 16t + 4s .. 16t + 4s + 3 (ntok of them live)
+    // of row r16; tiles past the batch are skipped (a uniform bound).
+    v4i C[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) C[t] = v4i{0, 0, 0, 0};
     for (int j0 = 0; j0 < nj; j0 += MS) {
         if (j0 > 0) load_chunk(j0);
 #pragma unroll
@@ -440,48 +471,58 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
             const int st = kw + (j0 + j) * ks;
             long bop[GE::NMF];
             decode<FMT, UD>(wq[j], bop);
-            if constexpr (FMT == kTern) {
-                auto group = [&](auto grp_c) __attribute__((always_inline)) {
-                    constexpr int grp = decltype(grp_c)::value;
-                    long aop[UD];
-                    if (tok_ok) {
-                        load_ops<UD, (UD % 2 == 0)>(xl + st * GE::SC + 32 * UD * grp + 8 * UD * s, aop);
-                    } else {
 #pragma unroll
-                        for (int i = 0; i < UD; ++i) aop[i] = 0;
-                    }
-                    const v4i c = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C);
-                    if constexpr (GROUPED) {
-                        const int gi = 2 * st + grp;
-                        if (gi < a.G && ntok > 0) {
-                            if constexpr (ACC) {
-                                if (row_ok) {
+            for (int t = 0; t < TT; ++t) {
+                if (t > 0 && 16 * t >= a.M) break;
+                const int tb = 16 * t;
+                const bool tok_ok = tb + r16 < a.M;
+                const int8_t *xl = lds_x + (tok_ok ? tb + r16 : 0) * p.ldl;
+                if constexpr (FMT == kTern) {
+                    const int ntok = min(4, a.M - tb - 4 * s);
+                    int32_t *accp = acc_l + ((tb + 4 * s) * TR + 16 * rt + r16) * gld;
+                    auto group = [&](auto grp_c) __attribute__((always_inline)) {
+                        constexpr int grp = decltype(grp_c)::value;
+                        long aop[UD];
+                        if (tok_ok) {
+                            load_ops<UD, (UD % 2 == 0)>(xl + st * GE::SC + 32 * UD * grp + 8 * UD * s, aop);
+                        } else {
 #pragma unroll
-                                    for (int vv = 0; vv < 4; ++vv)
-                                        if (vv < ntok) a.acc[((size_t)(4 * s + vv) * a.N + row) * a.G + gi] = c[vv] >> GE::SHIFT;
-                                }
-                            } else {
-                                accp[gi] = c[0] >> GE::SHIFT;
-#pragma unroll
-                                for (int vv = 1; vv < 4; ++vv)
-                                    if (vv < ntok) accp[vv * TR * gld + gi] = c[vv] >> GE::SHIFT;
-                            }
+                            for (int i = 0; i < UD; ++i) aop[i] = 0;
                         }
-                    } else {
-                        C = c;
-                    }
-                };
-                group(std::integral_constant<int, 0>{});
-                group(std::integral_constant<int, 1>{});
-            } else {
-                long aop[GE::NMF];
-                if (tok_ok) {
-                    load_ops<GE::NMF, true>(xl + st * GE::SC + (GE::SC / 4) * s, aop);
-                } else {
+                        const v4i c = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C[t]);
+                        if constexpr (GROUPED) {
+                            const int gi = 2 * st + grp;
+                            if (gi < a.G && ntok > 0) {
+                                if constexpr (ACC) {
+                                    if (row_ok) {
 #pragma unroll
-                    for (int i = 0; i < GE::NMF; ++i) aop[i] = 0;
+                                        for (int vv = 0; vv < 4; ++vv)
+                                            if (vv < ntok)
+                                                a.acc[((size_t)(tb + 4 * s + vv) * a.N + row) * a.G + gi] = c[vv] >> GE::SHIFT;
+                                    }
+                                } else {
+                                    accp[gi] = c[0] >> GE::SHIFT;
+#pragma unroll
+                                    for (int vv = 1; vv < 4; ++vv)
+                                        if (vv < ntok) accp[vv * TR * gld + gi] = c[vv] >> GE::SHIFT;
+                                }
+                            }
+                        } else {
+                            C[t] = c;
+                        }
+                    };
+                    group(std::integral_constant<int, 0>{});
+                    group(std::integral_constant<int, 1>{});
+                } else {
+                    long aop[GE::NMF];
+                    if (tok_ok) {
+                        load_ops<GE::NMF, true>(xl + st * GE::SC + (GE::SC / 4) * s, aop);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < GE::NMF; ++i) aop[i] = 0;
+                    }
+                    C[t] = mfma_ops<0>(aop, bop, C[t]);
                 }
-                C = mfma_ops<0>(aop, bop, C);
             }
         }
     }
@@ -516,29 +557,36 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
         if (ks > 1) {
             if (kw > 0) {
 #pragma unroll
-                for (int vv = 0; vv < 4; ++vv) red[(((kw - 1) * RT + rt) * 4 + vv) * 64 + lane] = C[vv];
+                for (int t = 0; t < TT; ++t)
+#pragma unroll
+                    for (int vv = 0; vv < 4; ++vv) red[((((kw - 1) * RT + rt) * TT + t) * 4 + vv) * 64 + lane] = C[t][vv];
             }
             __syncthreads();
             if (kw > 0) return;
             for (int k = 0; k < ks - 1; ++k)
 #pragma unroll
-                for (int vv = 0; vv < 4; ++vv) C[vv] += red[((k * RT + rt) * 4 + vv) * 64 + lane];
+                for (int t = 0; t < TT; ++t)
+#pragma unroll
+                    for (int vv = 0; vv < 4; ++vv) C[t][vv] += red[(((k * RT + rt) * TT + t) * 4 + vv) * 64 + lane];
         }
         const float rs = a.scales ? rs_raw : 1.0f;
         float out0 = -INFINITY;
 #pragma unroll
-        for (int vv = 0; vv < 4; ++vv) {
-            const int tok = 4 * s + vv;
-            if (tok >= a.M || !row_ok) continue;
-            const int isum = C[vv] >> GE::SHIFT;
-            if constexpr (ACC) {
-                a.acc[(size_t)tok * a.N + row] = isum;
-                continue;
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int tok = 16 * t + 4 * s + vv;
+                if (tok >= a.M || !row_ok) continue;
+                const int isum = C[t][vv] >> GE::SHIFT;
+                if constexpr (ACC) {
+                    a.acc[(size_t)tok * a.N + row] = isum;
+                    continue;
+                }
+                float out = ((float)isum * xs_l[tok]) * rs;
+                if (a.bias) out = out + bb_raw;
+                a.y[(size_t)tok * a.ldy + row] = out;
+                if (t == 0 && vv == 0) out0 = out;
             }
-            float out = ((float)isum * xs_l[tok]) * rs;
-            if (a.bias) out = out + bb_raw;
-            a.y[(size_t)tok * a.ldy + row] = out;
-            if (vv == 0) out0 = out;
         }
         if constexpr (!ACC) {
             if (a.amax_v) {   // M = 1: lanes 0..15 (s = 0) hold the tile's rows; the tile's first largest
@@ -551,8 +599,8 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
                     if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
                 }
                 if (lane == 0) {
-                    a.amax_v[blockIdx.x * RT + rt] = bv;
-                    a.amax_i[blockIdx.x * RT + rt] = bi;
+                    a.amax_v[rb * RT + rt] = bv;
+                    a.amax_i[rb * RT + rt] = bi;
                 }
             }
         }
@@ -647,9 +695,10 @@ struct eif_hip_qweight {
 
 namespace {
 
-int g_gemm_min_tokens = 16;
+int g_gemm_min_tokens = 64;
 int g_gemv_ksplit = 0;   // waves per row tile of the GEMV, 0 = pick_ks_gemv()
 int g_gemv_rt = 0;       // row tiles per workgroup of the GEMV, 0 = chosen from the shape
+int g_gemv_chunk = 0;    // token rows per GEMV workgroup above kFusedMaxM (1 .. 64, powers of 2), 0 = what fits
 int g_gemv_prep_cols = 0;   // fewest columns per thread of the fused prep (4, 8, 16), 0 = chosen from the shape
 
 int ud_supported(int ud) { return ud == 1 || ud == 2 || ud == 3 || ud == 4 || ud == 8; }
@@ -809,13 +858,33 @@ int pick_ks_gemv(int row_tiles, int nsteps)
     return ks > 16 ? 16 : (ks < 1 ? 1 : ks);
 }
 
+// Token rows one GEMV workgroup takes: the chunk size, or the whole batch.
+int gemv_wg_m(const QArgs &a) { return a.mw > 0 && a.mw < a.M ? a.mw : a.M; }
+// Token tiles of a GEMV workgroup (the kernel's TT): 1, 2 or 4.
+int gemv_tt(const QArgs &a)
+{
+    const int t = eif_ceil_div(gemv_wg_m(a), kGemvTileM);
+    return t <= 1 ? 1 : (t == 2 ? 2 : 4);
+}
+
 // Dynamic LDS of qgemv_kernel: the staged int8 rows, then the group sums and scales (grouped) or the K-split
 // partials (row-scaled).
 size_t gemv_lds_bytes(bool grouped, const QArgs &a, int ldl, int rt, int ks)
 {
-    const size_t tr = 16 * (size_t)rt, gld = (size_t)((a.G + 3) & ~3);
-    const size_t tail = grouped ? ((size_t)a.M * tr * gld + tr * (size_t)a.G) * 4 : (size_t)(ks - 1) * rt * 4 * 64 * 4;
-    return (size_t)a.M * ldl + tail;
+    const size_t tr = 16 * (size_t)rt, gld = (size_t)((a.G + 3) & ~3), m = (size_t)gemv_wg_m(a);
+    const size_t tail = grouped ? (m * tr * gld + tr * (size_t)a.G) * 4
+                                : (size_t)(ks - 1) * rt * gemv_tt(a) * 4 * 64 * 4;
+    return m * ldl + tail;
+}
+
+// Grid of a GEMV launch with nrb row blocks: one workgroup per row block, or with token chunks one per
+// (row block, chunk) over whole rounds of the 8 XCDs (the kernel's id mapping; surplus ids return at once).
+int gemv_grid(QArgs &a, int nrb)
+{
+    a.nrb = nrb;
+    if (!(a.mw > 0 && a.mw < a.M)) return nrb;
+    const int nch = eif_ceil_div(a.M, a.mw);
+    return eif_ceil_div(nrb, 8) * 8 * nch;
 }
 // LDS a workgroup may allocate on the current device (160 KiB on gfx950), read once per process.
 size_t gemv_max_lds()
@@ -835,11 +904,13 @@ size_t gemv_max_lds()
 template <int FMT, int UD, bool GROUPED>
 constexpr bool gemv_tuned() { return FMT != kTern || (GROUPED && (UD == 3 || UD == 4)); }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT>
 int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
     const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
-    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT><<<rows_pad / (16 * RT), 64 * RT * ks, lds, st>>>(a, p);
+    QArgs ag = a;
+    const int grid = gemv_grid(ag, rows_pad / (16 * RT));
+    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT, TT><<<grid, 64 * RT * ks, lds, st>>>(ag, p);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
@@ -851,7 +922,7 @@ int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipS
 {
     if constexpr (FMT == kTern && !ACC && (E == 4 || E == 8) && RT == 1) {
         const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
-        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, true><<<rows_pad / 16, 64 * ks, lds, st>>>(a, p);
+        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true><<<rows_pad / 16, 64 * ks, lds, st>>>(a, p);
         EIF_HIP_LAUNCHED();
         return EIF_HIP_OK;
     } else {
@@ -859,28 +930,28 @@ int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipS
     }
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT, int TT = 1>
 int launch_gemv_e(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
     if (p.sh_ml) return launch_gemv_sh<FMT, UD, GROUPED, ACC, E, LB, RT>(a, p, rows_pad, ks, st);
     constexpr int SMAX = Geo<FMT, UD>::SB >= 32 ? 4 : 8;   // 8-dword steps: half the registers per chunk
     const int steps = eif_ceil_div(a.nsteps, ks);
     if constexpr (ACC || !gemv_tuned<FMT, UD, GROUPED>()) {
-        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT>(a, p, rows_pad, ks, st);
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT, TT>(a, p, rows_pad, ks, st);
     } else {
-        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1, LB, RT>(a, p, rows_pad, ks, st);
-        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2, LB, RT>(a, p, rows_pad, ks, st);
-        if (steps <= 4 || SMAX == 4) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4, LB, RT>(a, p, rows_pad, ks, st);
-        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT>(a, p, rows_pad, ks, st);
+        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1, LB, RT, TT>(a, p, rows_pad, ks, st);
+        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2, LB, RT, TT>(a, p, rows_pad, ks, st);
+        if (steps <= 4 || SMAX == 4) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4, LB, RT, TT>(a, p, rows_pad, ks, st);
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT, TT>(a, p, rows_pad, ks, st);
     }
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int TT = 1>
 int launch_gemv_rt(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int ks, hipStream_t st)
 {
     if constexpr (gemv_tuned<FMT, UD, GROUPED>())
-        if (rt == 4) return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 4>(a, p, rows_pad, ks, st);
-    return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 1>(a, p, rows_pad, ks, st);
+        if (rt == 4) return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 4, TT>(a, p, rows_pad, ks, st);
+    return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 1, TT>(a, p, rows_pad, ks, st);
 }
 
 // Fused prep: E columns per thread. The WHT-128 of the BitNet configurations and no rotation (the INT8 head)
@@ -930,9 +1001,15 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
         }
         return EIF_HIP_E_LIMIT;
     }
-    while (ks < maxks && (a.M * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks))) ++ks;
-    if (a.M * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks) || !lds_fit(ks)) return 1;
-    return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0>(a, p, rows_pad, rt, ks, st);
+    const int wm = gemv_wg_m(a);
+    if (wm > kGemvTileM * kGemvMaxTT) return 1;
+    while (ks < maxks && (wm * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks))) ++ks;
+    if (wm * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks) || !lds_fit(ks)) return 1;
+    switch (gemv_tt(a)) {
+    case 1: return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0, 1>(a, p, rows_pad, rt, ks, st);
+    case 2: return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0, 2>(a, p, rows_pad, rt, ks, st);
+    default: return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0, 4>(a, p, rows_pad, rt, ks, st);
+    }
 }
 
 // Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses the GEMM).
@@ -941,17 +1018,45 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
 // the row (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
 // A shape that does not fit with four tiles is launched with one.
 template <int FMT, int UD, bool GROUPED, bool ACC>
-int launch_gemv(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
+int launch_gemv_m(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
 {
     p.ldl = a.nsteps * Geo<FMT, UD>::SC + 16;
     int rt = 1;
     if constexpr (gemv_tuned<FMT, UD, GROUPED>())
-        if (!p.sh_ml) rt = g_gemv_rt > 0 ? g_gemv_rt : (rows_pad / 16 >= 768 && (GROUPED || p.x || rows_pad / 16 < kBigTiles) ? 4 : 1);
+        if (!p.sh_ml) {
+            const int tiles = rows_pad / 16;
+            const bool chunked = a.M > kFusedMaxM && !p.x;
+            // more than kFusedMaxM tokens: four tiles once the workgroups (row tiles x token chunks) reach 768
+            const bool four = chunked ? tiles * eif_ceil_div(a.M, gemv_wg_m(a)) >= 768
+                                      : tiles >= 768 && (GROUPED || p.x || tiles < kBigTiles);
+            rt = g_gemv_rt > 0 ? g_gemv_rt : (four ? 4 : 1);
+        }
     if (rt > 1) {
         const int rc = launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, rt, st);
         if (rc == EIF_HIP_OK || rc == EIF_HIP_E_DEVICE) return rc;
     }
     return launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, 1, st);
+}
+
+// The batch in one workgroup when the fused prep or the shares are in (at most kFusedMaxM rows) or it is at
+// most kFusedMaxM rows; else workgroups of mw token rows (token tiles, then chunks), mw from kGemvDefaultWgM
+// (or the knob) halved until the staged rows and sums fit.
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_gemv(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
+{
+    if (p.x || p.sh_ml || a.M <= kFusedMaxM) {
+        if (a.M > (p.x ? kFusedMaxM : kGemvTileM)) return 1;
+        QArgs a1 = a;
+        a1.mw = 0;
+        return launch_gemv_m<FMT, UD, GROUPED, ACC>(a1, p, rows_pad, st);
+    }
+    for (int mw = g_gemv_chunk > 0 ? g_gemv_chunk : kGemvDefaultWgM; mw >= 1; mw /= 2) {
+        QArgs a1 = a;
+        a1.mw = mw;
+        const int rc = launch_gemv_m<FMT, UD, GROUPED, ACC>(a1, p, rows_pad, st);
+        if (rc != 1) return rc;
+    }
+    return 1;
 }
 
 template <int FMT, int UD, bool GROUPED, bool ACC>
@@ -999,12 +1104,12 @@ int make_prep_cols(int K, const float *x, int ldx, const float *signs, int block
     return EIF_HIP_OK;
 }
 
-// Fused-prep arguments of a linear: K == cols, at most kGemvMaxM token rows.
+// Fused-prep arguments of a linear: K == cols, at most kFusedMaxM token rows.
 int make_prep(const eif_hip_qweight *w, const float *x, int ldx, const float *signs, int block, float norm, int M,
               PrepArgs *p)
 {
     *p = PrepArgs{};
-    if (!w || !x || M < 1 || M > kGemvMaxM) return M > kGemvMaxM ? EIF_HIP_E_LIMIT : EIF_HIP_E_ARG;
+    if (!w || !x || M < 1 || M > kFusedMaxM) return M > kFusedMaxM ? EIF_HIP_E_LIMIT : EIF_HIP_E_ARG;
     return make_prep_cols(w->cols, x, ldx, signs, block, norm, p);
 }
 
@@ -1073,10 +1178,28 @@ int check_linear_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M
     return EIF_HIP_OK;
 }
 
-int resolve_path(int path, int M)
+// Whether one GEMV workgroup can stage a full token tile (16 rows) of the weight's activations and sums.
+bool gemv_fits_tile(const eif_hip_qweight *w)
 {
-    if (path == EIF_HIP_PATH_AUTO) return M >= g_gemm_min_tokens ? EIF_HIP_PATH_GEMM : EIF_HIP_PATH_GEMV;
-    return path;
+    const bool grouped = w->fmt == kTern && w->group > 0;
+    const size_t m = kGemvTileM, ldl = (size_t)w->kpad + 16, gld = (size_t)((w->ngroups + 3) & ~3);
+    const size_t lds = m * ldl + (grouped ? (m * 16 * gld + 16 * (size_t)w->ngroups) * 4 : 0);
+    return m * (size_t)(w->kpad / 16) <= (size_t)kMaxPieces * 1024 && lds <= gemv_max_lds();
+}
+
+// Auto path: the GEMV up to kFusedMaxM tokens; below eif_hip_gemm_min_tokens() also where a token tile fits one
+// workgroup and the batch is at most two tiles or the weights at most kGemvSmallBytes (the GEMV streams the
+// weights once per workgroup chunk, the GEMM once per 64 tokens); else the GEMM.
+constexpr size_t kGemvSmallBytes = (size_t)4 << 20;
+
+int resolve_path(const eif_hip_qweight *w, int path, int M)
+{
+    if (path != EIF_HIP_PATH_AUTO) return path;
+    if (M >= g_gemm_min_tokens) return EIF_HIP_PATH_GEMM;
+    if (M <= kFusedMaxM) return EIF_HIP_PATH_GEMV;
+    const size_t bytes = (size_t)w->rows_pad * w->wld + (size_t)w->rows * (w->ngroups > 0 ? w->ngroups : 1) * 4;
+    return gemv_fits_tile(w) && (M <= 2 * kGemvTileM || bytes <= kGemvSmallBytes) ? EIF_HIP_PATH_GEMV
+                                                                                   : EIF_HIP_PATH_GEMM;
 }
 
 QArgs make_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
@@ -1181,7 +1304,7 @@ int qlinear_scaled(const eif_hip_qweight *w, const float *scales, const int8_t *
     a.bias = bias;
     a.y = y;
     a.ldy = ldy;
-    return dispatch<false>(w, a, PrepArgs{}, resolve_path(path, M), st);
+    return dispatch<false>(w, a, PrepArgs{}, resolve_path(w, path, M), st);
 }
 
 }  // namespace eif
@@ -1300,6 +1423,13 @@ int eif_hip_set_gemv_row_tiles(int rt)
 {
     int old = g_gemv_rt;
     if (rt == 0 || rt == 1 || rt == 4) g_gemv_rt = rt;
+    return old;
+}
+
+int eif_hip_set_gemv_token_chunk(int m)
+{
+    const int old = g_gemv_chunk;
+    if (m >= 0 && m <= 64 && (m & (m - 1)) == 0) g_gemv_chunk = m;
     return old;
 }
 
@@ -1451,7 +1581,7 @@ int eif_hip_qlinear_acc(const eif_hip_qweight *w, const int8_t *xq, int ldq, int
     if (!acc) return EIF_HIP_E_ARG;
     QArgs a = make_args(w, xq, ldq, M);
     a.acc = acc;
-    return dispatch<true>(w, a, PrepArgs{}, resolve_path(path, M), (hipStream_t)stream);
+    return dispatch<true>(w, a, PrepArgs{}, resolve_path(w, path, M), (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -175,7 +175,10 @@ int eif_hip_qweight_from_gguf_ternary(eif_hip_qweight **out, int gguf_type, cons
  * Call it after rewriting a weight buffer in place or before freeing it.                                 */
 void eif_hip_forget_host_weights(const void *host_ptr);
 
-/* Token count from which the auto path uses the MFMA GEMM (default 16); returns the previous value.     */
+/* Token count from which the auto path uses the MFMA GEMM (default 64); returns the previous value. Below it
+ * the auto path takes the streaming GEMV for up to 8 tokens, and for more where one workgroup stages 16
+ * token rows of the weight's columns and the batch is at most 32 tokens or the weights at most 4 MiB
+ * (the GEMM otherwise: it reads the weights once per 64 tokens).                                       */
 int eif_hip_set_gemm_min_tokens(int m);
 int eif_hip_gemm_min_tokens(void);
 
@@ -186,6 +189,12 @@ int eif_hip_set_gemv_ksplit(int k);
 /* 16-row tiles per workgroup of the GEMV (1 or 4; 0 = chosen from the shape, the default); returns the
  * previous setting. A tuning knob: results do not depend on it.                                          */
 int eif_hip_set_gemv_row_tiles(int rt);
+
+/* Token rows per GEMV workgroup for batches above 8 tokens (1, 2, 4, 8, 16, 32 or 64; 0 = 32, halved until the
+ * shape's staged rows fit, the default): a workgroup decodes each weight step once for all its rows (up to 4
+ * MFMA token tiles of 16), and a larger batch is cut into chunks of that many rows, whose workgroups share
+ * each weight tile through L2. Returns the previous setting. A tuning knob: results do not depend on it.   */
+int eif_hip_set_gemv_token_chunk(int m);
 
 /* Fewest columns per thread of the prep fused into the GEMV (4, 8 or 16; 0 = chosen from the shape, the
  * default): more columns, fewer waves per workgroup. Returns the previous setting. A tuning knob: results do

@@ -51,6 +51,11 @@ TERN_GROUPED = [
     (130, 200, 32, 3, GEMV),        # ragged rows and columns
     (70, 640, 64, 5, GEMV),
     (64, 512, 256, 2, GEMV),
+    (6912, 2560, 128, 16, GEMV),    # 9 .. 63 tokens: the GEMV in token chunks
+    (3840, 2560, 128, 32, GEMV),
+    (2560, 6912, 96, 63, GEMV),     # g96 down: 8-row chunks (16 rows of sums do not fit the LDS)
+    (130, 200, 32, 63, GEMV),
+    (70, 640, 64, 17, GEMV),
     (70, 640, 64, 17, GEMM),
     (6912, 2560, 128, 64, GEMM),
     (2560, 6912, 96, 64, GEMM),
@@ -226,8 +231,10 @@ def test_ternary_rowscale_bit_exact(gpu, oracle, N, K, M, path, with_bias):
 @pytest.mark.parametrize("fmt,N,K,M,path", [
     ("int8", 4864, 896, 1, GEMV), ("int8", 896, 4864, 1, GEMV), ("int8", 128, 896, 3, GEMV),
     ("int8", 4864, 896, 128, GEMM), ("int8", 77, 100, 20, GEMM),
+    ("int8", 4864, 896, 32, GEMV), ("int8", 896, 4864, 63, GEMV), ("int8", 77, 100, 20, GEMV),
     ("int4", 3584, 1024, 1, GEMV), ("int4", 1024, 3584, 1, GEMV), ("int4", 3584, 1024, 32, GEMM),
-    ("int4", 50, 333, 4, GEMV), ("int4", 50, 333, 40, GEMM),
+    ("int4", 3584, 1024, 32, GEMV), ("int4", 1024, 3584, 16, GEMV),
+    ("int4", 50, 333, 4, GEMV), ("int4", 50, 333, 40, GEMM), ("int4", 50, 333, 40, GEMV),
 ])
 def test_int_rowscale_bit_exact(gpu, oracle, fmt, N, K, M, path):
     if fmt == "int8":
@@ -251,18 +258,71 @@ def test_int_rowscale_bit_exact(gpu, oracle, fmt, N, K, M, path):
 
 
 def test_int4_tied_head_full_size(gpu, oracle):
-    # the 151936 x 1024 INT4 head at M = 1 (GEMV) and M = 32 (GEMM): int32 sums against an exact integer product
+    # the 151936 x 1024 INT4 head at M = 1 and 32 (GEMV) and M = 32 (GEMM): int32 sums against an exact integer
+    # product
     N, K = synth.QWEN35_INT4_HEAD[1:]
     w, s = synth.int4_weight((49,), N, K)
     qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
     vals = synth.unpack_int4(w, K).astype(np.float64)
-    for M, path in ((1, GEMV), (32, GEMM)):
+    for M, path in ((1, GEMV), (32, GEMV), (32, GEMM)):
         x = synth.activations((50, M), M, K)
         xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
         acc = run_acc(gpu, qw, xq_d, M, (M, N), path)
         exact = xq[:, :K].astype(np.float64) @ vals.T          # integer-valued, |sums| < 2^53
         assert np.array_equal(acc.astype(np.float64), exact)
+        if M > 1 and path == GEMV:
+            y = run_linear(gpu, qw, xq_d, xs_d, M, path)
+            oy = np.zeros((M, N), np.float32)
+            oracle.orc_int4_gemv_i8act(P(w), P(s), P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
+            assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
     qw.close()
+
+
+@pytest.mark.parametrize("fmt,N,K,g", [("tern", 3840, 2560, 128), ("tern", 2560, 6912, 96), ("int8", 896, 4864, 0),
+                                       ("int4", 3000, 1024, 0)])
+def test_gemv_token_chunks(gpu, oracle, fmt, N, K, g):
+    """Token rows per workgroup and row tiles per workgroup change the launch of a 40-token GEMV, never the
+    result (y and the integer sums, bit for bit against the oracle)."""
+    lib = gpu.load()
+    M = 40
+    if fmt == "tern":
+        w, s = synth.ternary_weight((63, N, K, g), N, K, g)
+        qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+    elif fmt == "int8":
+        w, s = synth.int8_weight((64, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+    else:
+        w, s = synth.int4_weight((65, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+    x = synth.activations((66, M, K), M, K)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    oy = np.zeros((M, N), np.float32)
+    if fmt == "tern":
+        ng = -(-K // g)
+        oacc = np.zeros((M, N, ng), np.int32)
+        oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+        oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
+        shape = (M, N, ng)
+    else:
+        oacc = np.zeros((M, N), np.int32)
+        acc_fn = oracle.orc_int8_acc_i32 if fmt == "int8" else oracle.orc_int4_acc_i32
+        acc_fn(P(w), P(xq), qw.kpad, M, N, K, P(oacc))
+        fn = oracle.orc_int8_gemv_i8act if fmt == "int8" else oracle.orc_int4_gemv_i8act
+        fn(P(w), P(s), P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
+        shape = (M, N)
+    try:
+        for ch in (0, 16, 8, 4, 2, 1):
+            for rt in (0, 1, 4):
+                lib.eif_hip_set_gemv_token_chunk(ch)
+                lib.eif_hip_set_gemv_row_tiles(rt)
+                y = run_linear(gpu, qw, xq_d, xs_d, M, GEMV)
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (ch, rt)
+                acc = run_acc(gpu, qw, xq_d, M, shape, GEMV)
+                assert np.array_equal(acc, oacc), (ch, rt)
+    finally:
+        lib.eif_hip_set_gemv_token_chunk(0)
+        lib.eif_hip_set_gemv_row_tiles(0)
+        qw.close()
 
 
 def test_bitnet_layer_prefill_512(gpu, oracle):
