@@ -127,6 +127,7 @@ REF_TINYLLM_SIGS = {
     "ref_bitnet_create": (_vp, [_vp, _vp, _i]),
     "ref_bitnet_forward": (C.POINTER(_f), [_vp, _i, _i]),
     "ref_bitnet_destroy": (None, [_vp]),
+    "ref_bitnet_fill_cache": (C.c_int, [_vp, _i]),
     "ref_svlm_create": (_vp, [C.c_char_p]),
     "ref_ttml_create": (_vp, [C.c_char_p]),
     "ref_gguf_create": (_vp, [C.c_char_p]),

@@ -69,6 +69,31 @@ void *ref_bitnet_create(const orc_bitnet_cfg *c, const orc_bitnet_weights *w, in
 
 float *ref_bitnet_forward(void *h, int token, int pos) { return tinyllm_forward(&((ref_bitnet *)h)->llm, token, pos); }
 
+/* Fills the FP32 KV cache of positions 0 .. npos - 1 of every layer with synthetic values (a fixed 32-bit LCG
+ * mapped to [-1, 1)), so that tinyllm_forward at position npos reads a full cache of that length without the
+ * npos steps before it. For timing only: the values are not those of a prompt. The cache layout is the one
+ * tinyllm_forward indexes, [layer][seq_len][n_kv_heads * head_dim] (src/eif_tinyllm.c:415-418). Returns 0, or
+ * -1 when npos is outside 0 .. seq_len or the model keeps an INT8 cache. */
+int ref_bitnet_fill_cache(void *h, int npos)
+{
+    ref_bitnet *r = (ref_bitnet *)h;
+    const tinyllm_config_t *p = &r->llm.config;
+    tinyllm_state_t *s = &r->llm.state;
+    if (npos < 0 || npos > p->seq_len || p->kv_type != 0 || !s->key_cache || !s->value_cache) return -1;
+    const size_t kv_dim = (size_t)p->n_kv_heads * (size_t)(p->head_dim > 0 ? p->head_dim : p->dim / p->n_heads);
+    uint32_t st = 12345u;
+    for (int l = 0; l < p->n_layers; l++) {
+        const size_t loff = (size_t)l * p->seq_len * kv_dim;
+        for (size_t i = 0; i < (size_t)npos * kv_dim; i++) {
+            st = st * 1664525u + 1013904223u;
+            s->key_cache[loff + i] = (float)(st >> 8) * (2.0f / 16777216.0f) - 1.0f;
+            st = st * 1664525u + 1013904223u;
+            s->value_cache[loff + i] = (float)(st >> 8) * (2.0f / 16777216.0f) - 1.0f;
+        }
+    }
+    return 0;
+}
+
 void ref_bitnet_destroy(void *h)
 {
     ref_bitnet *r = (ref_bitnet *)h;
