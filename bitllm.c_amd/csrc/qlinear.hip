@@ -116,12 +116,12 @@ void qgemm_kernel(QArgs a)
         for (int i = 0; i < PPT; ++i) r[i] = *reinterpret_cast<const v4i *>(a.xq + (xo[i] + (uint32_t)(st * GE::SC)));
         load_words<NW>(a.W + (wo + (uint32_t)(st * 4 * GE::SB)), w);
         if constexpr (GROUPED) {
-            // a group past the row's last one (a ragged final step) gets scale 0 and adds nothing: F + 0 * x == F
+            // the loaded scales are only moved here, so the step's loads stay in flight until the step that uses
+            // them (a select on a loaded value would wait for it, and loads complete in order: for all of them)
 #pragma unroll
             for (int grp = 0; grp < 2; ++grp) {
                 const int gi = 2 * st + grp;
-                const float v = a.scales[so + (uint32_t)(gi < a.G ? gi : a.G - 1)];
-                c[grp] = gi < a.G ? v : 0.0f;
+                c[grp] = a.scales[so + (uint32_t)(gi < a.G ? gi : a.G - 1)];
             }
         }
     };
@@ -173,7 +173,8 @@ void qgemm_kernel(QArgs a)
                                 }
                             }
                         } else {
-                            const float cu = c[grp] * kUnshift;
+                            // a group past the row's last one (a ragged final step) adds nothing: F + 0 * x == F
+                            const float cu = gi < a.G ? c[grp] * kUnshift : 0.0f;
 #pragma unroll
                             for (int v = 0; v < 4; ++v) F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
                         }
