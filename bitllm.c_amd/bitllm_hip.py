@@ -80,6 +80,7 @@ _SIGS = {
     "eif_hip_qwen35_get_layout": (_vp, [_vp]),
     "eif_hip_qwen35_linear": (_vp, [_vp, _i, _i]),
     "eif_hip_qwen35_head": (_vp, [_vp]),
+    "eif_hip_qwen35_linear_batch": (_i, [_vp, _i, _i, C.POINTER(PrepSpec), _vp, _vp, _i, _i, _vp]),
     "eif_hip_qwen35_vector": (_vp, [_vp, _sz]),
     "eif_hip_bitnet_get_config": (_i, [_vp, _vp]),
     "eif_hip_bitnet_tokens": (_i, [_vp, _vp, _i, _vp]),
@@ -487,6 +488,7 @@ def _host_array(ptr, dtype, shape):
 Q35_DN_QKV, Q35_DN_Z, Q35_DN_OUT, Q35_DN_B, Q35_DN_A, Q35_FA_Q, Q35_FA_K, Q35_FA_V, Q35_FA_O, Q35_FF_GATE, \
     Q35_FF_UP, Q35_FF_DOWN = range(12)
 Q35_KINDS = 12
+Q35_HEAD = -1   # the tied head's kind for Qwen35Model.linear_batch
 Q35_FP32, Q35_INT4, Q35_TERN2, Q35_TERN3, Q35_INT8 = range(5)
 
 
@@ -546,6 +548,13 @@ class Qwen35Model:
     def vector(self, offset):
         """Device address of an FP32 vector of the layout (0 if absent)."""
         return load().eif_hip_qwen35_vector(self.h, offset) or 0
+
+    def linear_batch(self, layer, kind, spec, y, M=None, bias=None, stream=None):
+        """The prefill's batched linear (eif_hip_qwen35_linear_batch): y [M, N] from the rows of spec; kind
+        Q35_HEAD for the tied head."""
+        M = y.shape[0] if M is None else M
+        check(load().eif_hip_qwen35_linear_batch(self.h, layer, kind, C.byref(spec), ptr(bias), ptr(y), y.stride(0), M,
+                                                 stream_ptr(stream)), "eif_hip_qwen35_linear_batch")
 
     def close(self):
         if self.h:

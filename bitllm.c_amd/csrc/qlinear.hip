@@ -1325,9 +1325,32 @@ extern "C" int eif_hip_qlinear_f32(const eif_hip_qweight *w, const float *x, int
     return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, (hipStream_t)stream);
 }
 
+// More than kFusedMaxM rows of a spec: the prep on its own into the stream's prep workspace (xq [M, kpad], then xs
+// [M]), then the linear on the auto path. EIF_HIP_E_LIMIT when the workspace cannot be had (a stream's first such
+// call inside a graph capture).
+static int qlinear_prep_rows(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias, float *y,
+                             int ldy, int32_t *acc, int M, hipStream_t st)
+{
+    PrepArgs p;
+    int rc = make_prep_cols(w->cols, spec->x, spec->ldx, spec->signs, spec->wht_block, spec->wht_norm, &p);
+    if (rc) return rc;
+    if ((rc = apply_pre(spec, &p))) return rc;
+    const size_t qb = (size_t)M * w->kpad, bytes = qb + 4 * (size_t)M + 16;
+    int8_t *xq = reinterpret_cast<int8_t *>(split_ws(st, bytes, 1));
+    if (!xq) return EIF_HIP_E_LIMIT;
+    float *xs = reinterpret_cast<float *>(xq + ((qb + 15) & ~(size_t)15));
+    if ((rc = launch_prep_spec(p, xq, w->kpad, xs, M, st))) return rc;
+    if (acc) return eif_hip_qlinear_acc(w, xq, w->kpad, acc, M, EIF_HIP_PATH_AUTO, st);
+    return eif::qlinear_scaled(w, w->scales, xq, w->kpad, xs, bias, y, ldy, M, EIF_HIP_PATH_AUTO, st);
+}
+
 extern "C" int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias,
                                     float *y, int ldy, int M, void *stream)
 {
+    if (w && spec && y && M > kFusedMaxM) {
+        if (ldy < w->rows || (bias && bias + w->rows > y && bias < y + (size_t)M * ldy)) return EIF_HIP_E_ARG;
+        return qlinear_prep_rows(w, spec, bias, y, ldy, nullptr, M, (hipStream_t)stream);
+    }
     PrepArgs p;
     int rc = make_prep_spec(w, spec, M, &p);
     if (rc) return rc;
@@ -1367,6 +1390,7 @@ extern "C" int eif_hip_prep_spec_rows(const eif_hip_prep_spec *spec, int K, int8
 extern "C" int eif_hip_qlinear_prep_acc(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, int32_t *acc, int M,
                                         void *stream)
 {
+    if (w && spec && acc && M > kFusedMaxM) return qlinear_prep_rows(w, spec, nullptr, nullptr, 0, acc, M, (hipStream_t)stream);
     PrepArgs p;
     int rc = make_prep_spec(w, spec, M, &p);
     if (rc) return rc;

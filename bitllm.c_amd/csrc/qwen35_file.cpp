@@ -408,6 +408,16 @@ extern "C" const eif_hip_qweight *eif_hip_qwen35_head(const eif_hip_qwen35 *m)
     return m ? m->head : nullptr;
 }
 
+// The batched linear of the engine's prefill (linear_gemm, src/eif_qwen35.c:1034-1065, as prefill_chunk calls it,
+// :1067-1153) on a resident matrix: eif_hip_qlinear_prep over the batch's rows.
+extern "C" int eif_hip_qwen35_linear_batch(const eif_hip_qwen35 *m, int layer, int kind, const eif_hip_prep_spec *spec,
+                                           const float *bias, float *y, int ldy, int M, void *stream)
+{
+    const eif_hip_qweight *w = kind == EIF_Q35_HEAD ? eif_hip_qwen35_head(m) : eif_hip_qwen35_linear(m, layer, kind);
+    if (!w || !spec || M < 1) return EIF_HIP_E_ARG;
+    return eif_hip_qlinear_prep(w, spec, bias, y, ldy, M, stream);
+}
+
 extern "C" const float *eif_hip_qwen35_vector(const eif_hip_qwen35 *m, size_t offset)
 {
     if (!m || !offset || !m->vec) return nullptr;

@@ -135,10 +135,13 @@ typedef struct eif_hip_prep_spec {
     float wht_norm;       /* the WHT scale, e.g. eif_hip_wht_norm(wht_block) */
 } eif_hip_prep_spec;
 
-/* eif_hip_qlinear_f32 with a pre-op: y = linear(prep(pre(x))) (+ bias) for M <= 8 rows, one launch (a
- * row-scaled matrix of 65536 rows or more at M = 1, e.g. a vocabulary head: a prep launch, then the GEMV of
- * the prepped row, with the same output bits). The bias may be the residual stream itself (y == bias: each
- * output reads its own bias element first).                                                            */
+/* eif_hip_qlinear_f32 with a pre-op: y = linear(prep(pre(x))) (+ bias). M <= 8 rows: one launch (a row-scaled
+ * matrix of 65536 rows or more at M = 1, e.g. a vocabulary head: a prep launch, then the GEMV of the prepped row,
+ * with the same output bits); the bias may then be the residual stream itself (y == bias: each output reads its
+ * own bias element first). More rows (a prompt batch): the prep of eif_hip_prep_spec_rows into a per-stream
+ * workspace, then eif_hip_qlinear on the auto path (the streaming GEMV below 64 rows, the int8-MFMA GEMM from 64),
+ * the same bits as those two calls; the bias must not overlap y, and a stream's first such call must be made
+ * outside graph capture (it allocates the workspace; inside a capture it returns EIF_HIP_E_LIMIT).      */
 int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias, float *y,
                          int ldy, int M, void *stream);
 

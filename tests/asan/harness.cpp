@@ -16,6 +16,7 @@ int eif_hip_bitnet_set_globals(eif_hip_bitnet *, const eif_hip_bitnet_globals *)
 void eif_hip_bitnet_destroy(eif_hip_bitnet *) {}
 int eif_hip_qweight_create(eif_hip_qweight **, int, int, int, int, const void *, const float *, int, void *) { return -2; }
 void eif_hip_qweight_destroy(eif_hip_qweight *) {}
+int eif_hip_qlinear_prep(const eif_hip_qweight *, const eif_hip_prep_spec *, const float *, float *, int, int, void *) { return -2; }
 int eif_hadamard_block_size(int n) { int b = 1; while (b < 1024 && n % (2 * b) == 0) b *= 2; return b; }
 int eif_bitnet_group_size(int n, int mx) { for (int g = mx / 32 * 32; g >= 32; g -= 32) if (n % g == 0) return g; return 0; }
 float eif_hip_wht_norm(int) { return 1.0f; }

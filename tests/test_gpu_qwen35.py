@@ -8,6 +8,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
+from conftest import P
 import synth
 import model_files
 from test_qwn5 import CASES, DN_KINDS, FA_KINDS, FF_KINDS, KIND_ID, make
@@ -159,3 +160,127 @@ def test_qwen35_gguf_loads_as_its_image(gpu, tmp_path):
     finally:
         mg.close()
         mi.close()
+
+
+# The reference's prefill runs every quantized linear of a layer on n token rows at once (linear_gemm inside
+# prefill_chunk, src/eif_qwen35.c:1034-1065, 1067-1153), the rows rotated by had_rows with the layer input's signs
+# (signs_dim for inputs of width dim, q_dim and val_dim; signs_hid for the down projection's input).
+C3 = model_files.qwen35_config(dim=1024, hidden=3584, layer_types=[0, 1], n_heads=8, n_kv_heads=2, head_dim=128,
+                               vocab=2048, lin_k_heads=4, lin_k_dim=128, lin_v_heads=8, lin_v_dim=128,
+                               quant_lm=model_files.Q35_INT4, quant_embed=model_files.Q35_EMBED_INT4)
+BATCH_KINDS = {0: ("qkv", "out", "gate", "down"), 1: ("q", "o", "up", "down")}
+EMB_QT = {model_files.Q35_EMBED_INT8: 4, model_files.Q35_EMBED_INT4: model_files.Q35_INT4,
+          model_files.Q35_EMBED_2BIT: model_files.Q35_TERN2, model_files.Q35_EMBED_DENSE: model_files.Q35_TERN3,
+          model_files.Q35_EMBED_FP32: model_files.Q35_FP32}
+
+
+def oracle_batch(oracle, qt, values, scales, group, x, signs, block, norm, kpad, bias):
+    """orc_prep_rows of the FP32 rows, then the oracle's linear of the weight's storage type:
+    (y [M, rows], |contributions| [M, rows] for the tolerance of a grouped K split, or None)."""
+    M, K = x.shape
+    rows = values.shape[0]
+    xq = np.zeros((M, kpad), np.int8)
+    xs = np.zeros(M, np.float32)
+    assert oracle.orc_prep_rows(P(np.ascontiguousarray(x)), K, P(signs), M, K, block, C.c_float(norm), P(xq), kpad,
+                                P(xs), None, 0) == 0
+    y = np.zeros((M, rows), np.float32)
+    mag = None
+    if qt == model_files.Q35_INT4:
+        oracle.orc_int4_gemv_i8act(P(np.ascontiguousarray(synth.pack_int4(values))), P(scales), P(xq), kpad, P(xs),
+                                   P(bias), P(y), rows, M, rows, K)
+    elif qt == 4:
+        oracle.orc_int8_gemv_i8act(P(np.ascontiguousarray(values)), P(scales), P(xq), kpad, P(xs), P(bias), P(y),
+                                   rows, M, rows, K)
+    else:
+        w = np.ascontiguousarray(synth.pack_ternary(values))
+        g = group if qt == model_files.Q35_TERN2 else 0
+        if g:
+            s = np.ascontiguousarray(scales.reshape(rows, -1))
+            oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), kpad, P(xs), P(bias), P(y), rows, M, rows, K)
+            acc = np.zeros((M, rows, s.shape[1]), np.int32)
+            oracle.orc_ternary_acc_i32(P(w), P(xq), kpad, M, rows, K, g, P(acc))
+            mag = np.einsum("mng,ng->mn", np.abs(acc).astype(np.float64), s.astype(np.float64)) * xs[:, None]
+            if bias is not None:
+                mag = mag + np.abs(bias)[None, :]
+        else:
+            oracle.orc_ternary_gemv_rowscale(P(w), P(scales), P(xq), kpad, P(xs), P(bias), P(y), rows, M, rows, K)
+    return y, mag
+
+
+def check_batch(gpu, oracle, m, cfg, layer, kind, w, values, scales, qt, M, key):
+    """eif_hip_qwen35_linear_batch on M FP32 rows (row stride K + 4) into y (row stride rows + 8): the oracle's
+    output bit for bit (row-scaled INT4 / INT8 / ternary; grouped ternary when the GEMM does not split), grouped
+    ternary within 1e-5 relative to the sum of |contributions| otherwise; y's padding columns untouched."""
+    import torch
+    dev = torch.device("cuda:0")
+    lay = m.layout
+    rows, K = values.shape
+    assert (w.rows, w.cols) == (rows, K)
+    block = lay.hadamard_block
+    sig_off = (lay.signs_hid if kind == KIND_ID["down"] else lay.signs_dim) if block else 0
+    signs = device_floats(m.vector(sig_off), K) if sig_off else None
+    norm = gpu.wht_norm(block) if block else 1.0
+    r = synth.rng(70, *key, M)
+    x = r.standard_normal((M, K)).astype(np.float32)
+    x[r.uniform(size=(M, K)) < 0.01] *= 20.0
+    bias = r.standard_normal(rows).astype(np.float32) if M % 2 else None
+    xd = torch.zeros((M, K + 4), device=dev)
+    xd[:, :K] = torch.from_numpy(x).to(dev)
+    yd = torch.full((M, rows + 8), 7.0, device=dev)
+    bd = torch.from_numpy(bias).to(dev) if bias is not None else None
+    sp = gpu.PrepSpec(x=gpu.ptr(xd).value, ldx=K + 4, x2=None, norm_w=None, eps=0.0, pre=gpu.PRE_NONE,
+                      signs=m.vector(sig_off) if sig_off else None, wht_block=block, wht_norm=norm)
+    m.linear_batch(layer, kind, sp, yd, M=M, bias=bd)
+    torch.cuda.synchronize()
+    yg = yd.cpu().numpy()
+    assert np.all(yg[:, rows:] == 7.0), key
+    yg = np.ascontiguousarray(yg[:, :rows])
+    g = cfg["group"] if qt == model_files.Q35_TERN2 else 0
+    want, mag = oracle_batch(oracle, qt, values, scales, g, x, signs, block, norm, w.kpad, bias)
+    if mag is None:
+        assert np.array_equal(yg.view(np.uint32), want.view(np.uint32)), key
+    else:
+        err = np.abs(yg.astype(np.float64) - want) / (mag + 1e-30)
+        assert np.all(np.isfinite(yg)) and err.max() <= 1e-5, (key, err.max())
+
+
+BATCH_FILES = ("int4_int8emb", "tern_rows_2bitemb", "tern_g32_hadamard", "dense_no_subln", "g64_plain_int8emb", "c3")
+
+
+@pytest.mark.parametrize("case", BATCH_FILES)
+def test_qwen35_linear_batch(gpu, oracle, tmp_path, case):
+    """The prefill's batched linear on a file's resident weights: M = 64 rows take the int8-MFMA GEMM, 20 the
+    streaming GEMV; every file's rotation (block and signs) as the file sets it. The c3 file has the layer shapes
+    of a 1024-wide INT4 model (FFN 3584) and its INT4 head, unrotated (a QWN5 rotation needs grouped ternary
+    linears and a 2-bit embedding, src/eif_qwen35.c:1273-1281). FP32 linears and bad indices are refused."""
+    import torch
+    if case == "c3":
+        cfg = C3
+        img, arrays = model_files.qwen35_image(cfg, (8,))
+    else:
+        cfg, img, arrays = make(case, key=(9,))
+    path = tmp_path / "m.eifm"
+    path.write_bytes(img)
+    m = gpu.Qwen35Model(str(path))
+    try:
+        g, qlm = cfg["group"], cfg["quant_lm"]
+        qt = EMB_QT[cfg["quant_embed"]]
+        for M in (64, 20):
+            for l, t in enumerate(cfg["layer_types"]):
+                for k in BATCH_KINDS[t]:
+                    _, values, scales, _ = arrays[f"L{l}.{k}"]
+                    check_batch(gpu, oracle, m, cfg, l, KIND_ID[k], m.linear(l, KIND_ID[k]), values, scales, qlm, M,
+                                (l, KIND_ID[k]))
+            _, values, scales, _ = arrays["embed"]
+            check_batch(gpu, oracle, m, cfg, 0, gpu.Q35_HEAD, m.head(), values, scales, qt, M, (99,))
+        M = 64
+        x = torch.zeros((M, cfg["dim"]), device="cuda:0")
+        y = torch.zeros((M, cfg["hidden"]), device="cuda:0")
+        sp = gpu.prep_spec(x)
+        if g:   # a grouped file's beta projection is FP32: no GPU weight
+            with pytest.raises(gpu.HipError):
+                m.linear_batch(0, KIND_ID["pb"], sp, y, M=M)
+        with pytest.raises(gpu.HipError):
+            m.linear_batch(len(cfg["layer_types"]), KIND_ID["gate"], sp, y, M=M)
+    finally:
+        m.close()
