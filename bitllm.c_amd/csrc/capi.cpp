@@ -5,9 +5,10 @@
 // synchronous return, NULL scales = 1, NULL bias = 0, invalid sizes are a silent no-op. Re-entrancy: the
 // reference engines call these symbols from OpenMP worker threads (src/eif_tinyllm.c:1020,
 // src/eif_qwen35.c:139-140), so every thread owns its stream and staging buffers; the resident-weight cache is
-// shared under a mutex. Weight bytes are uploaded once per (host pointer, size, format) -- the reference's
-// weights live in long-lived pools or mmaps (src/eif_tinyllm.c:2565-2731, src/eif_qwen35.c:1229); a caller that
-// rewrites a buffer in place calls eif_hip_forget_host_weights(). GEMM operands are never cached (qwen35
+// shared under a mutex. Weight bytes (and the block scales of eif_matmul_bitnet_block_f32) are uploaded once per
+// (host pointer, size, format) and kept in the device layout the kernels read -- the reference's weights live in
+// long-lived pools or mmaps (src/eif_tinyllm.c:2565-2731, src/eif_qwen35.c:1229); a caller that rewrites a
+// buffer in place calls eif_hip_forget_host_weights(). GEMM operands are never cached (qwen35
 // dequantizes into reused temporaries, src/eif_qwen35.c:1038-1049).
 //
 // There is no CPU fallback: without a gfx950 device every compute entry point prints why and aborts.
@@ -130,7 +131,7 @@ void download_sync(ThreadCtx &c, void *host, const void *dev, size_t bytes, cons
 }
 
 // ---- resident weights ----
-enum Kind { kRaw = 0, kQTernRow = 1 };
+enum Kind { kRaw = 0, kQTernRow = 1, kBlockScales = 2, kTiles = 3 };   // kTiles + a reference layout (eif::kSrc*)
 
 struct WKey {
     const void *p;
@@ -167,6 +168,49 @@ const void *resident_raw(const void *host, size_t n, const char *fn)
     DIE_ON(hipMalloc(&e.raw, n ? n : 16), fn);
     DIE_ON(hipMemcpyAsync(e.raw, host, n, hipMemcpyHostToDevice, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
+    g_wcache.emplace(k, e);
+    return e.raw;
+}
+
+// The row-tile copy (f32linear.hip) of a weight buffer in reference layout src_fmt (n bytes): the bytes go up once,
+// are repacked on the device and dropped.
+const void *resident_tiles(const void *host, size_t n, int src_fmt, int rows, int cols, const char *fn)
+{
+    ThreadCtx &c = ctx(fn);
+    WKey k{host, n, kTiles + src_fmt, rows, cols};
+    std::lock_guard<std::mutex> lock(g_wmu);
+    auto it = g_wcache.find(k);
+    if (it != g_wcache.end()) return it->second.raw;
+    const int fmt = src_fmt == eif::kSrcInt4 ? eif::kF32Int4 : (src_fmt == eif::kSrcInt8 ? eif::kF32Int8 : eif::kF32Tern);
+    WEntry e;
+    void *tmp = nullptr;
+    DIE_ON(hipMalloc(&tmp, n ? n : 16), fn);
+    DIE_ON(hipMalloc(&e.raw, eif::f32_tiles_bytes(fmt, rows, cols)), fn);
+    DIE_ON(hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, c.st), fn);
+    DIE_RC(eif::launch_f32_repack(src_fmt, (const uint8_t *)tmp, e.raw, rows, cols, c.st), fn);
+    DIE_ON(hipStreamSynchronize(c.st), fn);
+    DIE_ON(hipFree(tmp), fn);
+    g_wcache.emplace(k, e);
+    return e.raw;
+}
+
+// The [tile][block][4 rows] copy of block scales [rows, ceil(cols / block)] (f32linear.hip), kept like weights.
+const void *resident_block_scales(const float *host, int rows, int cols, int block, const char *fn)
+{
+    ThreadCtx &c = ctx(fn);
+    const size_t n = sizeof(float) * (size_t)rows * (size_t)((cols + block - 1) / block);
+    WKey k{host, n, kBlockScales, rows, block};
+    std::lock_guard<std::mutex> lock(g_wmu);
+    auto it = g_wcache.find(k);
+    if (it != g_wcache.end()) return it->second.raw;
+    WEntry e;
+    void *tmp = nullptr;
+    DIE_ON(hipMalloc(&tmp, n), fn);
+    DIE_ON(hipMalloc(&e.raw, eif::f32_scales_bytes(rows, cols, block)), fn);
+    DIE_ON(hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, c.st), fn);
+    DIE_RC(eif::launch_f32_scales((const float *)tmp, e.raw, rows, cols, block, c.st), fn);
+    DIE_ON(hipStreamSynchronize(c.st), fn);
+    DIE_ON(hipFree(tmp), fn);
     g_wcache.emplace(k, e);
     return e.raw;
 }
@@ -411,12 +455,18 @@ static void tern_f32(const char *fn, const uint8_t *w, size_t wbytes, const floa
                      int block, const float *x, const float *bias, float *out, int rows, int cols, int il)
 {
     ThreadCtx &c = ctx(fn);
-    const uint8_t *dw = (const uint8_t *)resident_raw(w, wbytes, fn);
+    const bool tiles = eif::f32_tiles_fit(cols, mode ? block : 0);
+    const void *dw = tiles ? resident_tiles(w, wbytes, il ? eif::kSrcTernIl : eif::kSrcTernRow, rows, cols, fn)
+                           : resident_raw(w, wbytes, fn);
     const float *dx = (const float *)upload(c, 0, x, sizeof(float) * cols, fn);
-    const float *dsc = (const float *)upload(c, 1, scales, sizeof(float) * nsc, fn);
+    const float *dsc = tiles && mode && scales ? (const float *)resident_block_scales(scales, rows, cols, block, fn)
+                                               : (const float *)upload(c, 1, scales, sizeof(float) * nsc, fn);
     const float *db = (const float *)upload(c, 2, bias, sizeof(float) * rows, fn);
     float *dy = (float *)slot(c, 3, sizeof(float) * rows, fn);
-    DIE_RC(eif::launch_tern_f32(dw, dsc, mode, block, dx, db, dy, rows, cols, il, c.st), fn);
+    if (tiles)
+        DIE_RC(eif::launch_f32_tiles(eif::kF32Tern, dw, dsc, mode ? block : 0, dx, db, dy, rows, cols, c.st), fn);
+    else
+        DIE_RC(eif::launch_tern_f32((const uint8_t *)dw, dsc, mode, block, dx, db, dy, rows, cols, il, c.st), fn);
     download_sync(c, out, dy, sizeof(float) * rows, fn);
 }
 
@@ -465,12 +515,17 @@ void eif_matmul_bitnet_dense_f32(const uint8_t *weights, const float *scales, co
     static const char *fn = "eif_matmul_bitnet_dense_f32";
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
     ThreadCtx &c = ctx(fn);
-    const uint8_t *dw = (const uint8_t *)resident_raw(weights, (size_t)rows * ((cols + 4) / 5), fn);
+    const size_t wb = (size_t)rows * ((cols + 4) / 5);
+    const bool tiles = eif::f32_tiles_fit(cols, 0);
+    const void *dw = tiles ? resident_tiles(weights, wb, eif::kSrcDense, rows, cols, fn) : resident_raw(weights, wb, fn);
     const float *dx = (const float *)upload(c, 0, input, sizeof(float) * cols, fn);
     const float *dsc = (const float *)upload(c, 1, scales, sizeof(float) * rows, fn);
     const float *db = (const float *)upload(c, 2, bias, sizeof(float) * rows, fn);
     float *dy = (float *)slot(c, 3, sizeof(float) * rows, fn);
-    DIE_RC(eif::launch_dense_f32(dw, dsc, dx, db, dy, rows, cols, c.st), fn);
+    if (tiles)
+        DIE_RC(eif::launch_f32_tiles(eif::kF32Tern, dw, dsc, 0, dx, db, dy, rows, cols, c.st), fn);
+    else
+        DIE_RC(eif::launch_dense_f32((const uint8_t *)dw, dsc, dx, db, dy, rows, cols, c.st), fn);
     download_sync(c, output, dy, sizeof(float) * rows, fn);
 }
 
@@ -481,11 +536,16 @@ static void int_f32(const char *fn, bool int4, const void *w, const float *sc, c
 {
     ThreadCtx &c = ctx(fn);
     const size_t wb = int4 ? (size_t)rows * ((cols + 1) / 2) : (size_t)rows * cols;
-    const void *dw = resident_raw(w, wb, fn);
+    const bool tiles = eif::f32_tiles_fit(cols, 0);
+    const void *dw = tiles ? resident_tiles(w, wb, int4 ? eif::kSrcInt4 : eif::kSrcInt8, rows, cols, fn)
+                           : resident_raw(w, wb, fn);
     const float *dx = (const float *)upload(c, 0, x, sizeof(float) * cols, fn);
     const float *dsc = (const float *)upload(c, 1, sc, sizeof(float) * rows, fn);
     float *dy = (float *)slot(c, 2, sizeof(float) * rows, fn);
-    if (int4)
+    if (tiles)
+        DIE_RC(eif::launch_f32_tiles(int4 ? eif::kF32Int4 : eif::kF32Int8, dw, dsc, 0, dx, nullptr, dy, rows, cols, c.st),
+               fn);
+    else if (int4)
         DIE_RC(eif::launch_int4_f32((const uint8_t *)dw, dsc, dx, dy, rows, cols, c.st), fn);
     else
         DIE_RC(eif::launch_int8_f32((const int8_t *)dw, dsc, dx, dy, rows, cols, c.st), fn);

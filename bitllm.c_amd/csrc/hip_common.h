@@ -98,6 +98,25 @@ int qlinear_prep_shares(const eif_hip_qweight *w, const eif_hip_prep_spec *spec,
 int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y, float *amax_v,
                    int *amax_i, hipStream_t st);
 
+// FP32-activation GEMVs on the row-tile layout (f32linear.hip). Formats of the resident copy and the reference
+// layouts it is made from.
+constexpr int kF32Tern = 0, kF32Int4 = 1, kF32Int8 = 2;
+constexpr int kSrcTernRow = 0;   // 2-bit row-major, (cols + 3) / 4 bytes a row, 01 = +1, 10 = -1, 00 / 11 = 0
+constexpr int kSrcTernIl = 1;    // the same codes in the 4-row interleaved layout (src/eif_quantize_bitnet.c:1422-1456)
+constexpr int kSrcDense = 2;     // base 3, (cols + 4) / 5 bytes a row, trit i of a byte weighs 3^i, 1 = +1, 2 = -1
+constexpr int kSrcInt4 = 3;      // (cols + 1) / 2 bytes a row, even column in the high nibble, value nibble - 8
+constexpr int kSrcInt8 = 4;      // cols signed bytes a row
+size_t f32_tiles_bytes(int fmt, int rows, int cols);
+// Whether a matrix of cols columns and block scales of `block` columns (0: one scale a row) has the row-tile path.
+bool f32_tiles_fit(int cols, int block);
+// Bytes of the [tile][block][4 rows] copy of block scales [rows, ceil(cols / block)], and the launch making it.
+size_t f32_scales_bytes(int rows, int cols, int block);
+int launch_f32_scales(const float *scales, void *dst, int rows, int cols, int block, hipStream_t st);
+int launch_f32_repack(int src_fmt, const uint8_t *src, void *dst, int rows, int cols, hipStream_t st);
+// y = W x (+ bias) on the row-tile copy Wt: block > 0 (ternary only) with block scales in the copy of
+// launch_f32_scales, else scales [rows] (NULL = 1). x 16-byte aligned. EIF_HIP_E_LIMIT when f32_tiles_fit is false.
+int launch_f32_tiles(int fmt, const void *Wt, const float *scales, int block, const float *x, const float *bias,
+                     float *y, int rows, int cols, hipStream_t st);
 int launch_tern_f32(const uint8_t *W, const float *scales, int mode, int block, const float *x, const float *bias,
                     float *y, int rows, int cols, int il, hipStream_t st);
 int launch_dense_f32(const uint8_t *W, const float *scales, const float *x, const float *bias, float *y, int rows,

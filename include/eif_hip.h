@@ -174,8 +174,8 @@ int eif_gguf_ternary_rows(int gguf_type, const void *src, int rows, int cols, ui
 int eif_hip_qweight_from_gguf_ternary(eif_hip_qweight **out, int gguf_type, const void *src, int rows, int cols,
                                       void *stream);
 
-/* Drop the device copies the host-pointer ABI keeps for the weight buffer at host_ptr (NULL: all of them).
- * Call it after rewriting a weight buffer in place or before freeing it.                                 */
+/* Drop the device copies the host-pointer ABI keeps for the weight or block-scale buffer at host_ptr (NULL: all
+ * of them). Call it after rewriting such a buffer in place or before freeing it.                          */
 void eif_hip_forget_host_weights(const void *host_ptr);
 
 /* Token count from which the auto path uses the MFMA GEMM (default 64); returns the previous value. Below it
@@ -198,6 +198,15 @@ int eif_hip_set_gemv_row_tiles(int rt);
  * MFMA token tiles of 16), and a larger batch is cut into chunks of that many rows, whose workgroups share
  * each weight tile through L2. Returns the previous setting. A tuning knob: results do not depend on it.   */
 int eif_hip_set_gemv_token_chunk(int m);
+
+/* Row tiles (of 4 rows) a wave takes at a time in the FP32-activation GEMVs of the host-pointer ABI (1 or 2;
+ * 0 = chosen from the shape, the default); returns the previous setting. A tuning knob: results do not
+ * depend on it.                                                                                          */
+int eif_hip_set_f32_tiles_per_wave(int tw);
+
+/* Waves that split one row tile's columns in those GEMVs (1, 2, 3, 4 or 8; 0 = chosen from the shape, the default);
+ * returns the previous setting. A tuning knob: results depend on it only through the order of FP32 sums.   */
+int eif_hip_set_f32_ksplit(int ks);
 
 /* Fewest columns per thread of the prep fused into the GEMV (4, 8 or 16; 0 = chosen from the shape, the
  * default): more columns, fewer waves per workgroup. Returns the previous setting. A tuning knob: results do

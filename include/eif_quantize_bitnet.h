@@ -10,9 +10,9 @@
  *   - all pointers are caller-owned HOST memory; calls are synchronous and return when outputs are written;
  *   - scales == NULL means 1.0, bias == NULL means 0.0, invalid sizes are a silent no-op;
  *   - 2-bit code format: column c lives in byte c>>2 at bits 2*(c&3); 01 = +1, 10 = -1, 00 and 11 = 0.
- * What differs: the arithmetic runs as HIP kernels on the GPU. Weight buffers are uploaded once and kept
- * resident, keyed by (host pointer, size); call eif_hip_forget_host_weights() after rewriting a weight buffer
- * in place. Without a usable GPU the compute entry points print a diagnostic and abort(): there is no CPU path.
+ * What differs: the arithmetic runs as HIP kernels on the GPU. Weight buffers (and the block scales of
+ * eif_matmul_bitnet_block_f32) are uploaded once and kept resident, keyed by (host pointer, size); call
+ * eif_hip_forget_host_weights() after rewriting such a buffer in place. Without a usable GPU the compute entry points print a diagnostic and abort(): there is no CPU path.
  */
 #ifndef EIF_QUANTIZE_BITNET_H
 #define EIF_QUANTIZE_BITNET_H

@@ -169,6 +169,8 @@ def test_block_f32_full_size(lib, oracle):
     codes = synth.unpack_ternary(w, K).astype(np.float64)
     mag = (np.abs(codes) * np.repeat(s, g, axis=1)) @ np.abs(x.astype(np.float64))
     assert within(y, o, mag)
+    lib.eif_hip_forget_host_weights(P(w))
+    lib.eif_hip_forget_host_weights(P(s))
 
 
 def test_resident_weight_cache(lib, oracle):
@@ -213,3 +215,125 @@ def test_concurrent_callers(lib, oracle):
         oracle.orc_matmul_bitnet_block_f32(P(w), P(s), 128, P(xs[t]), None, P(o), rows, cols)
         mag = (np.abs(codes) * np.repeat(s, 128, axis=1)) @ np.abs(xs[t].astype(np.float64))
         assert within(outs[t], o, mag)
+    lib.eif_hip_forget_host_weights(P(w))
+    lib.eif_hip_forget_host_weights(P(s))
+
+
+def with_code3(packed, key):
+    """The reference's 2-bit rows may hold code 11 for a zero (read as 0): turn about half the zero codes into 11."""
+    p = packed.copy()
+    r = np.random.default_rng(key)
+    for i in range(4):
+        zero = ((p >> (2 * i)) & 3) == 0
+        p[zero & (r.uniform(size=p.shape) < 0.5)] |= np.uint8(3 << (2 * i))
+    return p
+
+
+# (rows, cols, block): the row-tile path (K <= 8192, blocks of whole 16-column chunks), ragged rows and columns,
+# and the row-major fallbacks (K > 8192, a block of 4 or 40 columns)
+TERN_BLOCK_SHAPES = [(6912, 2560, 128), (2560, 6912, 96), (37, 200, 32), (5, 48, 16), (130, 8192, 256),
+                     (1001, 1000, 64), (3, 8200, 128), (64, 640, 4), (50, 400, 40)]
+
+
+@pytest.mark.parametrize("rows,cols,block", TERN_BLOCK_SHAPES)
+def test_block_f32_shapes(lib, oracle, rows, cols, block):
+    w, s = synth.ternary_weight((80, rows, cols, block), rows, cols, block)
+    w = with_code3(w, (81, rows))
+    x = synth.activations((82, cols), 1, cols)[0]
+    bias = synth.rng(83, rows).standard_normal(rows).astype(np.float32) if rows % 2 else None
+    y = np.full(rows, np.nan, np.float32)
+    lib.eif_matmul_bitnet_block_f32(P(w), P(s), block, P(x), P(bias), P(y), rows, cols)
+    o = np.zeros(rows, np.float32)
+    oracle.orc_matmul_bitnet_block_f32(P(w), P(s), block, P(x), P(bias), P(o), rows, cols)
+    codes = synth.unpack_ternary(w, cols).astype(np.float64)
+    mag = (np.abs(codes) * np.repeat(s, block, axis=1)[:, :cols]) @ np.abs(x.astype(np.float64))
+    if bias is not None:
+        mag = mag + np.abs(bias)
+    assert np.all(np.isfinite(y)) and within(y, o, mag)
+    lib.eif_hip_forget_host_weights(P(w))
+    lib.eif_hip_forget_host_weights(P(s))
+
+
+@pytest.mark.parametrize("rows,cols", [(6912, 2560), (2561, 1000), (17, 33), (4099, 4096), (8, 9000)])
+def test_row_scaled_f32_layouts(lib, oracle, rows, cols):
+    """The same values in the three reference layouts (2-bit rows, 4-row interleaved, base 3) give outputs within
+    1e-5 of the oracle's for each."""
+    r = synth.rng(84, rows, cols)
+    v = r.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    w = with_code3(synth.pack_ternary(v), (85, rows))
+    il = np.zeros_like(w)
+    oracle.orc_interleave_weights_4rows(P(w), P(il), rows, cols)
+    dense = np.zeros((rows, (cols + 4) // 5), np.uint8)
+    for i in range(rows):
+        oracle.orc_pack_ternary_dense(P(np.ascontiguousarray(v[i])), P(dense[i]), cols)
+    s = (np.abs(r.standard_normal(rows)) * 0.02).astype(np.float32)
+    x = synth.activations((86, cols), 1, cols)[0]
+    bias = r.standard_normal(rows).astype(np.float32)
+    mag = (np.abs(v.astype(np.float64)) @ np.abs(x.astype(np.float64))) * s + np.abs(bias)
+    for fn, ofn, wt in ((lib.eif_matmul_bitnet_f32, oracle.orc_matmul_bitnet_f32, w),
+                        (lib.eif_matmul_bitnet_tmac_interleaved_f32, oracle.orc_matmul_bitnet_tmac_interleaved_f32, il),
+                        (lib.eif_matmul_bitnet_dense_f32, oracle.orc_matmul_bitnet_dense_f32, dense)):
+        y = np.full(rows, np.nan, np.float32)
+        fn(P(wt), P(s), P(x), P(bias), P(y), rows, cols)
+        o = np.zeros(rows, np.float32)
+        ofn(P(wt), P(s), P(x), P(bias), P(o), rows, cols)
+        assert np.all(np.isfinite(y)) and within(y, o, mag), fn
+        lib.eif_hip_forget_host_weights(P(wt))
+
+
+@pytest.mark.parametrize("rows,cols", [(151936, 1024), (4864, 896), (37, 1001), (40, 9000)])
+def test_int_f32_shapes(lib, oracle, rows, cols):
+    """INT4 (the tied vocabulary head's shape) and INT8 row-scaled GEMVs with FP32 activations against the
+    oracle, ragged and past the row-tile path's 8192 columns."""
+    w4, s4 = synth.int4_weight((87, rows, cols), rows, cols)
+    w8, s8 = synth.int8_weight((88, rows, cols), rows, cols)
+    x = synth.activations((89, cols), 1, cols)[0]
+    xa = np.abs(x.astype(np.float64))
+
+    def absdot(vals):   # sum_c |w[r][c]| |x[c]| over row blocks (bounded memory)
+        return np.concatenate([np.abs(vals(i, i + 8192).astype(np.float64)) @ xa for i in range(0, rows, 8192)])
+    y = np.full(rows, np.nan, np.float32)
+    lib.eif_int4_gemv_f32(P(y), P(w4), P(s4), P(x), rows, cols)
+    o = np.zeros(rows, np.float32)
+    oracle.orc_int4_gemv_f32(P(o), P(w4), P(s4), P(x), rows, cols)
+    mag = absdot(lambda a, b: synth.unpack_int4(w4[a:b], cols)) * s4
+    assert np.all(np.isfinite(y)) and within(y, o, mag)
+    y = np.full(rows, np.nan, np.float32)
+    lib.tinyllm_matmul_int8_rowscale(P(y), P(w8), P(x), cols, rows, P(s8))
+    o = np.zeros(rows, np.float32)
+    oracle.orc_int8_rowscale_f32(P(o), P(w8), P(x), cols, rows, P(s8))
+    mag = absdot(lambda a, b: w8[a:b]) * s8
+    assert np.all(np.isfinite(y)) and within(y, o, mag)
+    lib.eif_hip_forget_host_weights(P(w4))
+    lib.eif_hip_forget_host_weights(P(w8))
+
+
+def test_f32_tile_knobs(lib, oracle):
+    """Tiles per wave change the launch, never the bits; waves per tile (K split) change only the order of the FP32
+    sums: every setting within 1e-5 of the oracle."""
+    rows, cols, g = 6912, 2560, 128
+    w, s = synth.ternary_weight((90,), rows, cols, g)
+    w4, s4 = synth.int4_weight((91,), 20000, 1024)
+    x = synth.activations((92,), 1, cols)[0]
+    o = np.zeros(rows, np.float32)
+    oracle.orc_matmul_bitnet_block_f32(P(w), P(s), g, P(x), None, P(o), rows, cols)
+    codes = synth.unpack_ternary(w, cols).astype(np.float64)
+    mag = (np.abs(codes) * np.repeat(s, g, axis=1)) @ np.abs(x.astype(np.float64))
+    old_tw, old_ks = lib.eif_hip_set_f32_tiles_per_wave(0), lib.eif_hip_set_f32_ksplit(0)
+    try:
+        for ks in (1, 2, 3, 4, 8):
+            lib.eif_hip_set_f32_ksplit(ks)
+            outs = []
+            for tw in (1, 2):
+                lib.eif_hip_set_f32_tiles_per_wave(tw)
+                y, y4 = np.zeros(rows, np.float32), np.zeros(20000, np.float32)
+                lib.eif_matmul_bitnet_block_f32(P(w), P(s), g, P(x), None, P(y), rows, cols)
+                lib.eif_int4_gemv_f32(P(y4), P(w4), P(s4), P(x), 20000, 1024)
+                outs.append((bits(y), bits(y4)))
+                assert within(y, o, mag), (ks, tw)
+            assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1]), ks
+    finally:
+        lib.eif_hip_set_f32_tiles_per_wave(old_tw)
+        lib.eif_hip_set_f32_ksplit(old_ks)
+    for a in (w, s, w4):
+        lib.eif_hip_forget_host_weights(P(a))
