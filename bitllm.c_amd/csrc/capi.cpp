@@ -27,6 +27,7 @@
 
 #include "hip_common.h"
 #include "../../include/eif_gemm.h"
+#include "../../include/eif_gpu_bitnet.h"
 #include "../../include/eif_quant_linear.h"
 #include "../../include/eif_quantize_bitnet.h"
 
@@ -476,6 +477,16 @@ void eif_matmul_bitnet_f32(const uint8_t *weights, const float *scales, const fl
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
     tern_f32("eif_matmul_bitnet_f32", weights, (size_t)rows * ((cols + 3) / 4), scales, (size_t)rows, 0, 0, input,
              bias, output, rows, cols, 0);
+}
+
+bool eif_gpu_matmul_bitnet_f32(eif_gpu_context_t *ctx, const uint8_t *weights, const float *scales,
+                               const float *input, const float *bias, float *output, int rows, int cols)
+{
+    (void)ctx;
+    if (!weights || !input || !output || rows <= 0 || cols <= 0 || !dev_state().ok) return false;
+    tern_f32("eif_gpu_matmul_bitnet_f32", weights, (size_t)rows * ((cols + 3) / 4), scales, (size_t)rows, 0, 0,
+             input, bias, output, rows, cols, 0);
+    return true;
 }
 
 void eif_matmul_bitnet_block_f32(const uint8_t *weights, const float *block_scales, int block_size,

@@ -337,3 +337,23 @@ def test_f32_tile_knobs(lib, oracle):
         lib.eif_hip_set_f32_ksplit(old_ks)
     for a in (w, s, w4):
         lib.eif_hip_forget_host_weights(P(a))
+
+
+def test_gpu_seat(lib, oracle):
+    """The reference's GPU seat (include/eif_gpu.h:55-70) computes on the GPU and says so: the same bits as
+    eif_matmul_bitnet_f32, within 1e-5 of the oracle; invalid sizes return false and leave the output alone."""
+    rows, cols = 3001, 2560
+    w, s = synth.ternary_weight((93,), rows, cols, 0)
+    x = synth.activations((94,), 1, cols)[0]
+    bias = synth.rng(95).standard_normal(rows).astype(np.float32)
+    y, y1, o = np.zeros(rows, np.float32), np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+    assert lib.eif_gpu_matmul_bitnet_f32(None, P(w), P(s), P(x), P(bias), P(y), rows, cols)
+    lib.eif_matmul_bitnet_f32(P(w), P(s), P(x), P(bias), P(y1), rows, cols)
+    assert np.array_equal(bits(y), bits(y1))
+    oracle.orc_matmul_bitnet_f32(P(w), P(s), P(x), P(bias), P(o), rows, cols)
+    codes = synth.unpack_ternary(w, cols).astype(np.float64)
+    assert within(y, o, (np.abs(codes) @ np.abs(x.astype(np.float64))) * s + np.abs(bias))
+    z = np.full(4, 7.0, np.float32)
+    assert not lib.eif_gpu_matmul_bitnet_f32(None, P(w), P(s), P(x), None, P(z), 0, cols)
+    assert np.all(z == 7.0)
+    lib.eif_hip_forget_host_weights(P(w))
