@@ -609,6 +609,129 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 }
 
 
+// ---- streaming GEMV for vocabulary-sized row-scaled matrices (INT4, INT8) ----
+//
+// A workgroup of four waves stages the batch's int8 rows (M <= 16 TT) in LDS once, and each wave copies the MFMA
+// activation operands of every step into registers. Waves then stride over the matrix's 16-row tiles, one tile
+// per wave at a time, the next tile's codes (and the rows' scale and bias) loaded while the current one is
+// multiplied. A tile's steps, MFMAs and epilogue are those of qgemv_kernel with one wave per tile, so the
+// output bits are the same.
+constexpr int kStreamThreads = 256;
+
+template <int FMT, int UD, bool ACC, int NS, int TT>
+__global__ __launch_bounds__(kStreamThreads) void qstream_kernel(QArgs a, int ntiles)
+{
+    static_assert(FMT != kTern, "row-scaled INT4 / INT8 layouts");
+    using GE = Geo<FMT, UD>;
+    constexpr int NW = GE::SB / 4, NMF = GE::NMF;
+    constexpr int ldl = NS * GE::SC + 16;   // LDS row stride: 16-byte aligned rows, 16 bytes apart in bank
+    constexpr int PIECES = NS * GE::SC / 16;                                     // 16-byte pieces of a row
+    constexpr int MAXP = (16 * TT * PIECES + kStreamThreads - 1) / kStreamThreads;   // pieces per thread
+    extern __shared__ __align__(16) int8_t smem[];
+    __shared__ float xs_l[16 * TT];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, s = lane >> 4;
+    const int nw = gridDim.x * (kStreamThreads / 64);
+    int t = blockIdx.x * (kStreamThreads / 64) + wave;
+
+    // 1. the batch's int8 rows: loads first (they complete first), then the first tile's codes
+    v4i pc[MAXP];   // a native vector type: an array of it stays in registers
+    const int npc = a.M * PIECES;
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        const int idx = min((int)threadIdx.x + i * kStreamThreads, npc - 1);
+        const int m = idx / PIECES, c = idx - m * PIECES;
+        pc[i] = *reinterpret_cast<const v4i *>(a.xq + (size_t)m * a.ldq + 16 * c);
+    }
+    const float xs_v = a.xs[(int)threadIdx.x < a.M ? threadIdx.x : 0];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // a tile's loads: unconditional, the tile clamped into the matrix (rows are padded to whole tiles); the row's
+    // scale and bias from the codes' first word where absent (selected at use)
+    const float *w0 = reinterpret_cast<const float *>(a.W);
+    auto load = [&](uint32_t (&w)[NS][NW], float &rs, float &bb, int tile) {
+        const int row = min(tile, ntiles - 1) * 16 + r16;
+        const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) load_words<NW>(wp + (size_t)st * 4 * GE::SB, w[st]);
+        const int rc = min(row, a.N - 1);
+        rs = *(a.scales ? a.scales + rc : w0);
+        bb = *(a.bias ? a.bias + rc : w0);
+    };
+    uint32_t wA[NS][NW], wB[NS][NW];
+    float rsA, bbA, rsB, bbB;
+    load(wA, rsA, bbA, t);
+
+    // indices past the batch were clamped to its last piece: those threads store the same bytes to the same place
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        const int idx = min((int)threadIdx.x + i * kStreamThreads, npc - 1);
+        const int m = idx / PIECES, c = idx - m * PIECES;
+        *reinterpret_cast<v4i *>(smem + m * ldl + 16 * c) = pc[i];
+    }
+    if ((int)threadIdx.x < a.M) xs_l[threadIdx.x] = xs_v;
+    __syncthreads();
+
+    // 2. this lane's activation operands of every step and token tile, held in registers from here on (zeros
+    // past the batch)
+    long aop[TT][NS][NMF];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        const int tok = 16 * tt + r16;
+        const int8_t *xl = smem + (tok < a.M ? tok : 0) * ldl + (GE::SC / 4) * s;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            load_ops<NMF, true>(xl + st * GE::SC, aop[tt][st]);
+            if (tok >= a.M) {
+#pragma unroll
+                for (int i = 0; i < NMF; ++i) aop[tt][st][i] = 0;
+            }
+        }
+    }
+
+    // 3. tiles
+    auto work = [&](const uint32_t (&w)[NS][NW], float rs_raw, float bb_raw, int tile) {
+        v4i C[TT];
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) C[tt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            long bop[NMF];
+            decode<FMT, UD>(w[st], bop);
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) C[tt] = mfma_ops<0>(aop[tt][st], bop, C[tt]);
+        }
+        const int row = tile * 16 + r16;
+        if (tile >= ntiles || row >= a.N) return;
+        const float rs = a.scales ? rs_raw : 1.0f;
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int tok = 16 * tt + 4 * s + vv;
+                if (tok >= a.M) continue;
+                const int isum = C[tt][vv] >> GE::SHIFT;
+                if constexpr (ACC) {
+                    a.acc[(size_t)tok * a.N + row] = isum;
+                } else {
+                    float out = ((float)isum * xs_l[tok]) * rs;
+                    if (a.bias) out = out + bb_raw;
+                    a.y[(size_t)tok * a.ldy + row] = out;
+                }
+            }
+        }
+    };
+    while (t < ntiles) {   // the bound is the same for every lane of a wave
+        load(wB, rsB, bbB, t + nw);
+        work(wA, rsA, bbA, t);
+        t += nw;
+        if (t >= ntiles) break;
+        load(wA, rsA, bbA, t + nw);
+        work(wB, rsB, bbB, t);
+        t += nw;
+    }
+}
+
 // The fused prep on its own: token row m = blockIdx.x -> int8 codes xq[m, 0 .. ldq) (zeros past K) and xs[m].
 // E columns per thread, the threads covering ldq; LB as in prep_finish.
 template <int E, int LB>
@@ -1039,12 +1162,50 @@ int launch_gemv_m(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
     return launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, 1, st);
 }
 
+int g_gemv_stream = 0;   // streaming GEMV: waves per CU (0 = the default, -1 = off)
+constexpr int kStreamWavesPerCU = 8;
+
+template <int FMT, int UD, bool ACC, int NS, int TT>
+int launch_stream_t(const QArgs &a, int rows_pad, hipStream_t st)
+{
+    const int ldl = NS * Geo<FMT, UD>::SC + 16, ntiles = rows_pad / 16;
+    const int wpc = g_gemv_stream > 0 ? g_gemv_stream : kStreamWavesPerCU;
+    const int waves = std::min(ntiles, device_cus() * wpc);
+    const int grid = eif_ceil_div(waves, kStreamThreads / 64);
+    qstream_kernel<FMT, UD, ACC, NS, TT><<<grid, kStreamThreads, (size_t)a.M * ldl, st>>>(a, ntiles);
+    EIF_HIP_LAUNCHED();
+    return EIF_HIP_OK;
+}
+
+// The streaming GEMV takes row-scaled INT4 / INT8 matrices of kBigTiles 16-row tiles or more (vocabulary heads)
+// with prepped activations, 4 to 32 token rows (1 to 3 as well when its launch size is set) and 8 or 16 steps
+// along K. Returns 1 for other shapes.
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
+{
+    if constexpr (FMT == kTern || GROUPED) {
+        return 1;
+    } else {
+        if (g_gemv_stream < 0 || p.x || p.sh_ml || a.amax_v || a.M > 32 || rows_pad / 16 < kBigTiles) return 1;
+        if (a.M < 4 && g_gemv_stream == 0) return 1;   // up to 3 token rows: the tiled GEMV measured as fast or faster
+        if (a.M <= 16) {
+            if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 1>(a, rows_pad, st);
+            if (a.nsteps == 16) return launch_stream_t<FMT, UD, ACC, 16, 1>(a, rows_pad, st);
+        } else {
+            if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 2>(a, rows_pad, st);
+        }
+        return 1;
+    }
+}
+
 // The batch in one workgroup when the fused prep or the shares are in (at most kFusedMaxM rows) or it is at
 // most kFusedMaxM rows; else workgroups of mw token rows (token tiles, then chunks), mw from kGemvDefaultWgM
 // (or the knob) halved until the staged rows and sums fit.
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemv(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
 {
+    const int rs = launch_stream<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
+    if (rs != 1) return rs;
     if (p.x || p.sh_ml || a.M <= kFusedMaxM) {
         if (a.M > (p.x ? kFusedMaxM : kGemvTileM)) return 1;
         QArgs a1 = a;
@@ -1448,6 +1609,13 @@ int eif_hip_set_gemv_row_tiles(int rt)
 {
     int old = g_gemv_rt;
     if (rt == 0 || rt == 1 || rt == 4) g_gemv_rt = rt;
+    return old;
+}
+
+int eif_hip_set_gemv_stream(int wpc)
+{
+    const int old = g_gemv_stream;
+    if (wpc >= -1 && wpc <= 32) g_gemv_stream = wpc;
     return old;
 }
 

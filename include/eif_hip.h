@@ -199,6 +199,12 @@ int eif_hip_set_gemv_row_tiles(int rt);
  * each weight tile through L2. Returns the previous setting. A tuning knob: results do not depend on it.   */
 int eif_hip_set_gemv_token_chunk(int m);
 
+/* The streaming GEMV of vocabulary-sized row-scaled INT4 / INT8 matrices (65,536 rows or more, prepped
+ * activations, 4 to 32 token rows, 8 or 16 steps of K): waves per CU of its launch (1..32, which also takes 1
+ * to 3 token rows; 0 = the default, 8; -1 = off, such matrices then take the GEMV above). Returns the previous
+ * setting. A tuning knob: results do not depend on it.                                                  */
+int eif_hip_set_gemv_stream(int wpc);
+
 /* Row tiles (of 4 rows) a wave takes at a time in the FP32-activation GEMVs of the host-pointer ABI (1 or 2;
  * 0 = chosen from the shape, the default); returns the previous setting. A tuning knob: results do not
  * depend on it.                                                                                          */

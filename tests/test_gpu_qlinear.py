@@ -446,3 +446,42 @@ def test_gguf_ternary_weight(gpu, oracle, kind):
     want = xq[:, :K].astype(np.int64) @ synth.unpack_ternary(oc, K).astype(np.int64).T
     assert np.array_equal(acc, want)
     qw.close()
+
+
+@pytest.mark.parametrize("fmt,N,K", [("int4", 151936, 1024), ("int4", 65600, 2048), ("int8", 70001, 512),
+                                     ("int8", 65536, 1024)])
+def test_stream_gemv(gpu, oracle, fmt, N, K):
+    """The streaming GEMV of vocabulary-sized row-scaled matrices (65,536 rows or more, 8 or 16 steps along K)
+    at M = 1, 5, 16, 17 and 32, with and without a bias: y and the integer sums bit for bit against the oracle,
+    and the same bits with the stream off (the tiled GEMV) and at other launch sizes."""
+    lib = gpu.load()
+    if fmt == "int8":
+        w, s = synth.int8_weight((67, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+        fn = oracle.orc_int8_gemv_i8act
+    else:
+        w, s = synth.int4_weight((68, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+        fn = oracle.orc_int4_gemv_i8act
+    old = lib.eif_hip_set_gemv_stream(0)
+    try:
+        for M in (1, 5, 16, 17, 32):
+            x = synth.activations((69, M, K), M, K)
+            xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+            bias = synth.rng(70, M).standard_normal(N).astype(np.float32) if M % 2 else None
+            oy = np.zeros((M, N), np.float32)
+            fn(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+            for wpc in (0, 3, -1):
+                lib.eif_hip_set_gemv_stream(wpc)
+                y = run_linear(gpu, qw, xq_d, xs_d, M, GEMV, bias)
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (M, wpc)
+            lib.eif_hip_set_gemv_stream(0)
+            if M in (1, 17):
+                acc = run_acc(gpu, qw, xq_d, M, (M, N), GEMV)
+                oacc = np.zeros((M, N), np.int32)
+                (oracle.orc_int8_acc_i32 if fmt == "int8" else oracle.orc_int4_acc_i32)(P(w), P(xq), qw.kpad, M, N,
+                                                                                       K, P(oacc))
+                assert np.array_equal(acc, oacc), M
+    finally:
+        lib.eif_hip_set_gemv_stream(old)
+    qw.close()
