@@ -87,8 +87,9 @@ struct QView {
     int fmt, rows, cols, group, ud, kpad, rows_pad, nsteps, wld, G;
 };
 int qweight_view(const eif_hip_qweight *w, QView *v);
-// The device's fixed scratch of eif_hip_qlinear_ex_noalloc (qlinear.hip), set up once per device.
-int scratch_init(int device, float **out);
+// The device's fixed scratch of eif_hip_qlinear_ex_noalloc (qlinear.hip) and its split GEMM counters, set up once
+// per device.
+int scratch_init(int device, float **out, int **cnt = nullptr);
 // The fused-prep linear of one token row (M = 1) whose input row is combined from attention shares in the prep:
 // column c = h hd + d is sum_s e^(M_s - M) O_s[d] / sum_s e^(M_s - M) L_s over the shares s of head h, M = max_s M_s,
 // with sh_o [K / hd][kAttnShares][hd] the outputs O_s and sh_ml [K / hd][2 kAttnShares] the maxima M_s, then the

@@ -145,6 +145,10 @@ EIF_DEV float ld_coh(const float *p) { return __hip_atomic_load(const_cast<float
 EIF_DEV void st_coh(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 EIF_DEV int ld_coh_i(const int *p) { return __hip_atomic_load(const_cast<int *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 EIF_DEV void st_coh_i(int *p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+EIF_DEV uint64_t ld_coh_u64(const uint64_t *p)
+{
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 struct PrepArgs {
     const float *x;       // [M, ldx] FP32 rows to prep in the kernel, or NULL (xq/xs of QArgs are staged)

@@ -53,7 +53,8 @@ struct QArgs {
     int ldy;
     int32_t *acc;          // parity output or NULL
     int M, N, nsteps;
-    float *part;           // GEMM split along K: partial sums [split][M][N]
+    float *part;           // GEMM split along K: partial sums [split][tile][thread][4 TT]
+    int *cnt;              // GEMM split along K: one arrival counter per output tile, zero between launches
     float *amax_v;         // row-scaled GEMV, M = 1: per 16-row tile, the largest output and its row
     int *amax_i;           //   (first of equal maxima; NaN never wins), or NULL
     int mw;                // GEMV: token rows per workgroup (0: all M in one workgroup)
@@ -210,17 +211,66 @@ void qgemm_kernel(QArgs a)
     if constexpr (GROUPED && ACC) return;
 
     if (gridDim.z > 1) {
-        // Split along K: the partial sums of this split (FP32 group combines, or the exact int32 sums) go to
-        // part[split][token][row]; qgemm_reduce_kernel adds them in split order and applies the epilogue.
+        // Split along K. Each split stores its partial sums (the FP32 group combines, or the exact int32 sums) for
+        // this thread's outputs, value-major (part[split][tile][4 TT values][256 threads]: every store and load
+        // instruction covers 256 contiguous bytes), with device-coherent stores (sc1: past the XCDs' non-coherent
+        // L2s), waits for them, and counts the workgroup's arrival on the tile's counter. The last split to arrive
+        // reads every split's partials back with device-coherent loads, adds them in split order, writes the
+        // epilogue and resets the counter for the next launch.
+        const int ntile = gridDim.x * gridDim.y, tile = blockIdx.y * gridDim.x + blockIdx.x, nz = gridDim.z;
+        auto pz = [&](int z) { return a.part + ((size_t)z * ntile + tile) * (4 * TT * kGemmThreads) + threadIdx.x; };
+        float *own = pz(blockIdx.z);
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                st_coh(own + (4 * tt + v) * kGemmThreads, GROUPED ? F[tt][v] : __int_as_float(C[tt][v] >> GE::SHIFT));
+        __builtin_amdgcn_s_waitcnt(0);
+        __shared__ int last_l;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last_l = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nz - 1;
+        __syncthreads();
+        if (!last_l) return;
+        if (threadIdx.x == 0) st_coh_i(a.cnt + tile, 0);
+        // split order, the loads of four splits in flight at once (indices past the last split read it again)
+        float fs[TT][4];
+        int is[TT][4];
+        for (int z0 = 0; z0 < nz; z0 += 4) {
+            float q[4][4 * TT];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float *p = pz(min(z0 + j, nz - 1));
+#pragma unroll
+                for (int i = 0; i < 4 * TT; ++i) q[j][i] = ld_coh(p + i * kGemmThreads);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (z0 + j >= nz) break;
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float f = q[j][4 * tt + v];
+                        if constexpr (GROUPED)
+                            fs[tt][v] = z0 + j == 0 ? f : fs[tt][v] + f;
+                        else
+                            is[tt][v] = (z0 + j == 0 ? 0 : is[tt][v]) + __float_as_int(f);
+                    }
+            }
+        }
         if (!row_ok) return;
-        float *pz = a.part + (size_t)blockIdx.z * a.M * a.N;
+        const float rs = (!GROUPED && a.scales) ? a.scales[row] : 1.0f;
+        const float bb = a.bias ? a.bias[row] : 0.0f;
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int tok = m0 + 16 * tt + 4 * s + v;
-                if (tok < a.M)
-                    pz[(size_t)tok * a.N + row] = GROUPED ? F[tt][v] : __int_as_float(C[tt][v] >> GE::SHIFT);
+                if (tok >= a.M) continue;
+                float out = GROUPED ? fs[tt][v] * a.xs[tok] : ((float)is[tt][v] * a.xs[tok]) * rs;
+                if (a.bias) out = out + bb;
+                a.y[(size_t)tok * a.ldy + row] = out;
             }
         return;
     }
@@ -248,27 +298,6 @@ void qgemm_kernel(QArgs a)
             if (a.bias) out = out + bb;
             a.y[(size_t)tok * a.ldy + row] = out;
         }
-}
-
-// Sum of the splits of a split GEMM, in split order, and the epilogue: one thread per (token, row).
-template <bool GROUPED>
-__global__ __launch_bounds__(256) void qgemm_reduce_kernel(QArgs a, int ks)
-{
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, mn = (size_t)a.M * a.N;
-    if (i >= mn) return;
-    const int tok = (int)(i / a.N), row = (int)(i % a.N);
-    float out;
-    if constexpr (GROUPED) {
-        float t = a.part[i];
-        for (int z = 1; z < ks; ++z) t += a.part[z * mn + i];
-        out = t * a.xs[tok];
-    } else {
-        int isum = __float_as_int(a.part[i]);
-        for (int z = 1; z < ks; ++z) isum += __float_as_int(a.part[z * mn + i]);
-        out = ((float)isum * a.xs[tok]) * (a.scales ? a.scales[row] : 1.0f);
-    }
-    if (a.bias) out = out + a.bias[row];
-    a.y[(size_t)tok * a.ldy + row] = out;
 }
 
 // ---- small-batch GEMV (M <= kGemvMaxM): RT 16-row tiles per workgroup, ks waves per tile ----
@@ -847,16 +876,18 @@ struct WsKeyHash {
 std::mutex g_ws_mu;
 std::unordered_map<WsKey, std::pair<float *, size_t>, WsKeyHash> g_ws[2];
 
-float *split_ws(hipStream_t st, size_t bytes, int slot = 0)
+float *split_ws(hipStream_t st, size_t bytes, int slot = 0, bool *fresh = nullptr)
 {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto &w = g_ws[slot][WsKey{st, std::this_thread::get_id()}];
+    if (fresh) *fresh = false;
     if (w.second < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
         float *p = nullptr;
         if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
         w = {p, bytes};   // the old buffer stays allocated
+        if (fresh) *fresh = true;
     }
     return w.first;
 }
@@ -904,9 +935,15 @@ int choose_split(int nsteps, int tiles)
 // uses its address per device from hipGetSymbolAddress (g_scratch_dev), never the array's name.
 constexpr size_t kScratchFloats = (size_t)8 << 20;   // 32 MiB
 static __device__ __align__(256) float scratch[kScratchFloats];
+// The split GEMM's arrival counters: one per output tile, zero between launches (each tile's last arrival resets
+// its own). The fixed scratch has its own (zero when the code object is loaded); a per-stream workspace starts
+// with them, zeroed when it is allocated.
+constexpr int kMaxSplitTiles = 65536;
+static __device__ __align__(256) int scratch_cnt[kMaxSplitTiles] = {};
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float *g_scratch_dev[kMaxDevices];
+int *g_scratch_cnt_dev[kMaxDevices];
 
 // Token tile of the GEMM (16 x TT tokens, see launch_gemm) and its row tiles x token tiles for M tokens.
 int gemm_tt(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
@@ -917,23 +954,33 @@ int gemm_tiles(int rows_pad, int M) { return rows_pad / 64 * eif_ceil_div(M, 16 
 struct FixedWs {
     float *ptr = nullptr;
     size_t bytes = 0;
+    int *cnt = nullptr;
 };
 thread_local FixedWs tl_fixed_ws;
 
-template <bool ACC>
+// Splits along K for `tiles` output tiles of 64 rows x 16 TT tokens, with the partials' space (ks x tiles x
+// 256 threads x 4 TT floats) and the tiles' counters; 1 when the launch is not split.
+template <bool ACC, int TT>
 int pick_split(QArgs &a, int tiles, hipStream_t st)
 {
     if (ACC) return 1;
     const int ks = choose_split(a.nsteps, tiles);
-    if (ks <= 1) return 1;
-    const size_t bytes = (size_t)ks * a.M * a.N * sizeof(float);
+    if (ks <= 1 || tiles > kMaxSplitTiles) return 1;
+    const size_t bytes = (size_t)ks * tiles * kGemmThreads * 4 * TT * sizeof(float);
     if (tl_fixed_ws.ptr) {   // a fixed workspace too small for this split: -1, nothing is launched
         if (bytes > tl_fixed_ws.bytes) return -1;
         a.part = tl_fixed_ws.ptr;
+        a.cnt = tl_fixed_ws.cnt;
         return ks;
     }
-    a.part = split_ws(st, bytes);
-    return a.part ? ks : 1;
+    constexpr size_t cnt_bytes = (size_t)kMaxSplitTiles * sizeof(int);
+    bool fresh = false;
+    float *ws = split_ws(st, cnt_bytes + bytes, 0, &fresh);
+    if (!ws) return 1;
+    a.cnt = reinterpret_cast<int *>(ws);
+    a.part = ws + kMaxSplitTiles;
+    if (fresh && hipMemsetAsync(a.cnt, 0, cnt_bytes, st) != hipSuccess) return -2;
+    return ks;
 }
 
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
@@ -943,16 +990,12 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     if ((size_t)a.M * a.ldq >= ((size_t)1 << 32) || (size_t)rows_pad * a.wld >= ((size_t)1 << 32)) return EIF_HIP_E_LIMIT;
     const int tm = eif_ceil_div(a.M, 16 * TT), tiles = rows_pad / 64 * tm;
     static_assert(TT == 1 || TT == 2 || TT == 4, "token tiles of gemm_tt");
-    const int ks = pick_split<ACC>(a, tiles, st);
+    const int ks = pick_split<ACC, TT>(a, tiles, st);
+    if (ks == -2) return EIF_HIP_E_DEVICE;
     if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
     qgemm_kernel<FMT, UD, GROUPED, ACC, TT><<<grid, kGemmThreads, 0, st>>>(a);
     EIF_HIP_LAUNCHED();
-    if (ks > 1) {
-        const size_t mn = (size_t)a.M * a.N;
-        qgemm_reduce_kernel<GROUPED><<<(unsigned)((mn + 255) / 256), 256, 0, st>>>(a, ks);
-        EIF_HIP_LAUNCHED();
-    }
     return EIF_HIP_OK;
 }
 
@@ -1387,20 +1430,23 @@ int qweight_row_tiles(const eif_hip_qweight *w) { return w ? w->rows_pad / 16 : 
 
 // The address of this device's scratch (device current), made once per device at eif_hip_init or at the first
 // eif_hip_qlinear_ex_noalloc call on the device.
-int scratch_init(int device, float **out)
+int scratch_init(int device, float **out, int **cnt)
 {
     if (device < 0 || device >= kMaxDevices) return EIF_HIP_E_DEVICE;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     if (!g_scratch_dev[device]) {
-        void *ptr = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        if (e != hipSuccess || !ptr) {
+        void *ptr = nullptr, *cptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e == hipSuccess) e = hipGetSymbolAddress(&cptr, HIP_SYMBOL(scratch_cnt));
+        if (e != hipSuccess || !ptr || !cptr) {
             fprintf(stderr, "libbitllm_hip: hipGetSymbolAddress(scratch) failed: %s\n", hipGetErrorString(e));
             return EIF_HIP_E_DEVICE;
         }
         g_scratch_dev[device] = static_cast<float *>(ptr);
+        g_scratch_cnt_dev[device] = static_cast<int *>(cptr);
     }
     if (out) *out = g_scratch_dev[device];
+    if (cnt) *cnt = g_scratch_cnt_dev[device];
     return EIF_HIP_OK;
 }
 
@@ -1749,9 +1795,10 @@ int eif_hip_qlinear_ex_noalloc(const eif_hip_qweight *w, const int8_t *xq, int l
     int dev = 0;
     float *ws = nullptr;
     if (hipGetDevice(&dev) != hipSuccess) return EIF_HIP_E_DEVICE;
-    const int rc = eif::scratch_init(dev, &ws);
+    int *cnt = nullptr;
+    const int rc = eif::scratch_init(dev, &ws, &cnt);
     if (rc) return rc;
-    tl_fixed_ws = FixedWs{ws, kScratchFloats * sizeof(float)};
+    tl_fixed_ws = FixedWs{ws, kScratchFloats * sizeof(float), cnt};
     const int r = eif::qlinear_scaled(w, w->scales, xq, ldq, xs, bias, y, ldy, M, path, (hipStream_t)stream);
     tl_fixed_ws = FixedWs{};
     return r;

@@ -222,8 +222,9 @@ int eif_hip_set_gemv_prep_cols(int e);
 
 /* Splits along K of the GEMM (1..16; 0 = chosen from the shape, the default); returns the previous setting.
  * A split GEMM adds the per-split FP32 partials of grouped ternary in split order (deterministic, within
- * 1e-5 of the oracle; unsplit launches match it bit for bit); integer sums do not depend on it. Splits use a
- * per-stream workspace allocated on first use outside graph capture.                                    */
+ * 1e-5 of the oracle; unsplit launches match it bit for bit); integer sums do not depend on it. Each tile's last
+ * split adds them in the same launch. Splits use a per-stream workspace allocated on first use outside graph
+ * capture.                                                                                              */
 int eif_hip_set_gemm_split(int k);
 
 #ifdef __cplusplus
