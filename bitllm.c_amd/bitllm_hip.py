@@ -128,6 +128,10 @@ _SIGS = {
     "eif_quantize_activation_i8": (None, [_vp, _vp, _vp, _i]),
     "eif_matmul_bitnet_i8xternary_f32": (None, [_vp, _vp, _vp, _f, _vp, _vp, _i, _i]),
     "eif_matmul_bitnet_act_quant_f32": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "eif_hip_set_host_weight_cache_limit": (_sz, [_sz]),
+    "eif_hip_host_weight_cache_bytes": (_sz, []),
+    "eif_hip_set_host_error_mode": (_i, [_i]),
+    "eif_hip_host_last_error": (_i, [_vp, _sz]),
     "eif_gpu_matmul_bitnet_f32": (C.c_bool, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     "eif_matmul_bitnet_block_f32": (None, [_vp, _vp, _i, _vp, _vp, _vp, _i, _i]),
     "eif_interleave_weights_4rows": (_sz, [_vp, _vp, _i, _i]),

@@ -11,11 +11,13 @@
 // buffer in place calls eif_hip_forget_host_weights(). GEMM operands are never cached (qwen35
 // dequantizes into reused temporaries, src/eif_qwen35.c:1038-1049).
 //
-// There is no CPU fallback: without a gfx950 device every compute entry point prints why and aborts.
+// There is no CPU fallback: without a gfx950 device every compute entry point prints why and aborts, or, in the
+// record error mode (eif_hip_set_host_error_mode), returns and records the error for the calling thread.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -63,8 +65,21 @@ DevState &dev_state()
     return st;
 }
 
+// Error policy (eif_hip_set_host_error_mode): abort, or record the error for the calling thread and end the call.
+// In record mode die() throws HostError, which each entry point catches (a function-try-block) and returns from;
+// the lock guards on the way release their mutexes.
+std::atomic<int> g_host_err_mode{EIF_HIP_HOST_ABORT};
+thread_local int t_err_code = EIF_HIP_OK;
+thread_local char t_err_msg[256];
+struct HostError {};
+
 [[noreturn]] void die(const char *fn, const char *what)
 {
+    if (g_host_err_mode.load(std::memory_order_relaxed) == EIF_HIP_HOST_RECORD) {
+        t_err_code = EIF_HIP_E_DEVICE;
+        snprintf(t_err_msg, sizeof t_err_msg, "%s: %s", fn, what);
+        throw HostError{};
+    }
     fprintf(stderr, "libbitllm_hip: %s: %s (no CPU fallback exists)\n", fn, what);
     fflush(stderr);
     abort();
@@ -153,10 +168,74 @@ struct WKeyHash {
 struct WEntry {
     void *raw = nullptr;
     eif_hip_qweight *q = nullptr;
+    size_t bytes = 0;     // device bytes held
+    int pins = 0;         // calls using it now
+    uint64_t used = 0;    // last use (g_tick)
 };
 
+// The resident copies are bounded: an insertion beyond the limit evicts the least recently used copies that no
+// call is using (every call synchronizes with its stream before it unpins, so an unpinned copy has no work in
+// flight). A call pins what it looks up until it returns (PinScope).
 std::mutex g_wmu;
 std::unordered_map<WKey, WEntry, WKeyHash> g_wcache;
+size_t g_cache_bytes = 0, g_cache_limit = 0;   // limit 0: three quarters of the device's memory
+uint64_t g_tick = 0;
+thread_local std::vector<WKey> t_pins;
+
+void free_entry(const WEntry &e)
+{
+    if (e.raw) (void)hipFree(e.raw);
+    if (e.q) eif_hip_qweight_destroy(e.q);
+}
+
+size_t cache_limit()   // g_wmu held
+{
+    if (g_cache_limit) return g_cache_limit;
+    size_t free_b = 0, total = 0;
+    if (hipMemGetInfo(&free_b, &total) != hipSuccess || total == 0) return SIZE_MAX;
+    return total / 4 * 3;
+}
+
+void make_room(size_t need)   // g_wmu held
+{
+    const size_t lim = cache_limit();
+    while (g_cache_bytes + need > lim) {
+        auto victim = g_wcache.end();
+        for (auto it = g_wcache.begin(); it != g_wcache.end(); ++it)
+            if (it->second.pins == 0 && (victim == g_wcache.end() || it->second.used < victim->second.used)) victim = it;
+        if (victim == g_wcache.end()) return;   // everything is in use: exceed the limit rather than fail
+        g_cache_bytes -= victim->second.bytes;
+        free_entry(victim->second);
+        g_wcache.erase(victim);
+    }
+}
+
+WEntry &pin(const WKey &k, WEntry &e)   // g_wmu held
+{
+    ++e.pins;
+    e.used = ++g_tick;
+    t_pins.push_back(k);
+    return e;
+}
+
+WEntry &insert(const WKey &k, const WEntry &e)   // g_wmu held
+{
+    g_cache_bytes += e.bytes;
+    return pin(k, g_wcache.emplace(k, e).first->second);
+}
+
+struct PinScope {
+    ~PinScope()
+    {
+        if (t_pins.empty()) return;
+        std::lock_guard<std::mutex> lock(g_wmu);
+        for (const WKey &k : t_pins) {
+            auto it = g_wcache.find(k);
+            if (it != g_wcache.end() && it->second.pins > 0) --it->second.pins;
+        }
+        t_pins.clear();
+    }
+};
 
 const void *resident_raw(const void *host, size_t n, const char *fn)
 {
@@ -164,13 +243,14 @@ const void *resident_raw(const void *host, size_t n, const char *fn)
     WKey k{host, n, kRaw, 0, 0};
     std::lock_guard<std::mutex> lock(g_wmu);
     auto it = g_wcache.find(k);
-    if (it != g_wcache.end()) return it->second.raw;
+    if (it != g_wcache.end()) return pin(k, it->second).raw;
     WEntry e;
-    DIE_ON(hipMalloc(&e.raw, n ? n : 16), fn);
+    e.bytes = n ? n : 16;
+    make_room(e.bytes);
+    DIE_ON(hipMalloc(&e.raw, e.bytes), fn);
     DIE_ON(hipMemcpyAsync(e.raw, host, n, hipMemcpyHostToDevice, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
-    g_wcache.emplace(k, e);
-    return e.raw;
+    return insert(k, e).raw;
 }
 
 // The row-tile copy (f32linear.hip) of a weight buffer in reference layout src_fmt (n bytes): the bytes go up once,
@@ -181,18 +261,19 @@ const void *resident_tiles(const void *host, size_t n, int src_fmt, int rows, in
     WKey k{host, n, kTiles + src_fmt, rows, cols};
     std::lock_guard<std::mutex> lock(g_wmu);
     auto it = g_wcache.find(k);
-    if (it != g_wcache.end()) return it->second.raw;
+    if (it != g_wcache.end()) return pin(k, it->second).raw;
     const int fmt = src_fmt == eif::kSrcInt4 ? eif::kF32Int4 : (src_fmt == eif::kSrcInt8 ? eif::kF32Int8 : eif::kF32Tern);
     WEntry e;
+    e.bytes = eif::f32_tiles_bytes(fmt, rows, cols);
+    make_room(e.bytes + n);
     void *tmp = nullptr;
     DIE_ON(hipMalloc(&tmp, n ? n : 16), fn);
-    DIE_ON(hipMalloc(&e.raw, eif::f32_tiles_bytes(fmt, rows, cols)), fn);
+    DIE_ON(hipMalloc(&e.raw, e.bytes), fn);
     DIE_ON(hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, c.st), fn);
     DIE_RC(eif::launch_f32_repack(src_fmt, (const uint8_t *)tmp, e.raw, rows, cols, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
     DIE_ON(hipFree(tmp), fn);
-    g_wcache.emplace(k, e);
-    return e.raw;
+    return insert(k, e).raw;
 }
 
 // The [tile][block][4 rows] copy of block scales [rows, ceil(cols / block)] (f32linear.hip), kept like weights.
@@ -203,17 +284,18 @@ const void *resident_block_scales(const float *host, int rows, int cols, int blo
     WKey k{host, n, kBlockScales, rows, block};
     std::lock_guard<std::mutex> lock(g_wmu);
     auto it = g_wcache.find(k);
-    if (it != g_wcache.end()) return it->second.raw;
+    if (it != g_wcache.end()) return pin(k, it->second).raw;
     WEntry e;
+    e.bytes = eif::f32_scales_bytes(rows, cols, block);
+    make_room(e.bytes + n);
     void *tmp = nullptr;
     DIE_ON(hipMalloc(&tmp, n), fn);
-    DIE_ON(hipMalloc(&e.raw, eif::f32_scales_bytes(rows, cols, block)), fn);
+    DIE_ON(hipMalloc(&e.raw, e.bytes), fn);
     DIE_ON(hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, c.st), fn);
     DIE_RC(eif::launch_f32_scales((const float *)tmp, e.raw, rows, cols, block, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
     DIE_ON(hipFree(tmp), fn);
-    g_wcache.emplace(k, e);
-    return e.raw;
+    return insert(k, e).raw;
 }
 
 const eif_hip_qweight *resident_tern_row(const uint8_t *host, int rows, int cols, const char *fn)
@@ -223,11 +305,14 @@ const eif_hip_qweight *resident_tern_row(const uint8_t *host, int rows, int cols
     WKey k{host, n, kQTernRow, rows, cols};
     std::lock_guard<std::mutex> lock(g_wmu);
     auto it = g_wcache.find(k);
-    if (it != g_wcache.end()) return it->second.q;
+    if (it != g_wcache.end()) return pin(k, it->second).q;
     WEntry e;
+    make_room(n + n / 8);   // the GPU layout is about the reference's size
     DIE_RC(eif_hip_qweight_create(&e.q, EIF_HIP_W_TERNARY, rows, cols, 0, host, nullptr, 0, c.st), fn);
-    g_wcache.emplace(k, e);
-    return e.q;
+    size_t qb = 0;
+    eif_hip_qweight_info(e.q, nullptr, nullptr, nullptr, nullptr, &qb);
+    e.bytes = qb;
+    return insert(k, e).q;
 }
 
 float norm_fastmath(int block)
@@ -282,13 +367,41 @@ float eif_hip_wht_norm(int block) { return block > 0 ? norm_fastmath(block) : 1.
 
 float eif_hip_wht_norm_exact(int block) { return block > 0 ? (float)(1.0 / sqrt((double)block)) : 1.0f; }
 
+size_t eif_hip_set_host_weight_cache_limit(size_t bytes)
+{
+    std::lock_guard<std::mutex> lock(g_wmu);
+    const size_t old = g_cache_limit;
+    g_cache_limit = bytes;
+    return old;
+}
+
+size_t eif_hip_host_weight_cache_bytes(void)
+{
+    std::lock_guard<std::mutex> lock(g_wmu);
+    return g_cache_bytes;
+}
+
+int eif_hip_set_host_error_mode(int mode)
+{
+    if (mode != EIF_HIP_HOST_ABORT && mode != EIF_HIP_HOST_RECORD) return -1;
+    return g_host_err_mode.exchange(mode);
+}
+
+int eif_hip_host_last_error(char *msg, size_t len)
+{
+    const int code = t_err_code;
+    if (msg && len) snprintf(msg, len, "%s", code == EIF_HIP_OK ? "" : t_err_msg);
+    t_err_code = EIF_HIP_OK;
+    return code;
+}
+
 void eif_hip_forget_host_weights(const void *host_ptr)
 {
     std::lock_guard<std::mutex> lock(g_wmu);
     for (auto it = g_wcache.begin(); it != g_wcache.end();) {
         if (host_ptr == nullptr || it->first.p == host_ptr) {
-            if (it->second.raw) (void)hipFree(it->second.raw);
-            if (it->second.q) eif_hip_qweight_destroy(it->second.q);
+            g_cache_bytes -= it->second.bytes;
+            free_entry(it->second);
             it = g_wcache.erase(it);
         } else {
             ++it;
@@ -363,7 +476,7 @@ int eif_bitnet_group_size(int n, int max_group)
 
 // ---- activation prep ----
 
-void eif_hadamard_rotate_f32(float *x, const float *signs, int n, int block)
+void eif_hadamard_rotate_f32(float *x, const float *signs, int n, int block) try
 {
     static const char *fn = "eif_hadamard_rotate_f32";
     if (!x || block <= 0 || n % block != 0 || !pow2(block)) return;
@@ -372,9 +485,9 @@ void eif_hadamard_rotate_f32(float *x, const float *signs, int n, int block)
     const float *ds = (const float *)upload(c, 1, signs, sizeof(float) * n, fn);
     DIE_RC(eif::launch_rotate_rows(dx, n, ds, 1, n, block, eif_hip_wht_norm(block), c.st), fn);
     download_sync(c, x, dx, sizeof(float) * n, fn);
-}
+} catch (const HostError &) {}
 
-void eif_quantize_activation_i8(const float *x_f32, int8_t *x_i8, float *out_scale, int n)
+void eif_quantize_activation_i8(const float *x_f32, int8_t *x_i8, float *out_scale, int n) try
 {
     static const char *fn = "eif_quantize_activation_i8";
     if (n <= 0) {
@@ -390,13 +503,14 @@ void eif_quantize_activation_i8(const float *x_f32, int8_t *x_i8, float *out_sca
     DIE_ON(hipMemcpyAsync(&s, ds, sizeof(float), hipMemcpyDeviceToHost, c.st), fn);
     download_sync(c, x_i8, dq, (size_t)n, fn);
     if (out_scale) *out_scale = s;
-}
+} catch (const HostError &) {}
 
 // ---- INT8-activation ternary (MFMA kernel, resident repacked codes) ----
 
 static void i8xternary(const char *fn, const uint8_t *w, const float *scales, const int8_t *xq_host,
                        const float *x_host, float scale_in, const float *bias, float *out, int rows, int cols)
 {
+    PinScope pins;
     ThreadCtx &c = ctx(fn);
     const eif_hip_qweight *q = resident_tern_row(w, rows, cols, fn);
     int kpad = 0;
@@ -420,25 +534,26 @@ static void i8xternary(const char *fn, const uint8_t *w, const float *scales, co
 }
 
 void eif_matmul_bitnet_i8xternary_f32(const uint8_t *weights, const float *scales, const int8_t *input_i8,
-                                      float scale_in, const float *bias, float *output, int rows, int cols)
+                                      float scale_in, const float *bias, float *output, int rows, int cols) try
 {
     if (!weights || !input_i8 || !output || rows <= 0 || cols <= 0) return;
     i8xternary("eif_matmul_bitnet_i8xternary_f32", weights, scales, input_i8, nullptr, scale_in, bias, output,
                rows, cols);
-}
+} catch (const HostError &) {}
 
 void eif_matmul_bitnet_act_quant_f32(const uint8_t *weights, const float *scales, const float *input_f32,
-                                     const float *bias, float *output, int rows, int cols)
+                                     const float *bias, float *output, int rows, int cols) try
 {
     if (!weights || !input_f32 || !output || rows <= 0 || cols <= 0) return;
     i8xternary("eif_matmul_bitnet_act_quant_f32", weights, scales, nullptr, input_f32, 1.0f, bias, output, rows,
                cols);
-}
+} catch (const HostError &) {}
 
 void eif_matmul_bitnet_int8(const uint8_t *weights, float scale_w, const int8_t *input, float scale_in,
-                            const int32_t *bias, int8_t *output, float scale_out, int rows, int cols)
+                            const int32_t *bias, int8_t *output, float scale_out, int rows, int cols) try
 {
     static const char *fn = "eif_matmul_bitnet_int8";
+    PinScope pins;
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
     ThreadCtx &c = ctx(fn);
     const float eff = (scale_w * scale_in) / (scale_out > 1e-12f ? scale_out : 1.0f);
@@ -448,13 +563,14 @@ void eif_matmul_bitnet_int8(const uint8_t *weights, float scale_w, const int8_t 
     int8_t *dy = (int8_t *)slot(c, 2, (size_t)rows, fn);
     DIE_RC(eif::launch_tern_int8_out(dw, dx, db, dy, eff, rows, cols, c.st), fn);
     download_sync(c, output, dy, (size_t)rows, fn);
-}
+} catch (const HostError &) {}
 
 // ---- FP32-activation ternary (the reference engines' x86 path) ----
 
 static void tern_f32(const char *fn, const uint8_t *w, size_t wbytes, const float *scales, size_t nsc, int mode,
                      int block, const float *x, const float *bias, float *out, int rows, int cols, int il)
 {
+    PinScope pins;
     ThreadCtx &c = ctx(fn);
     const bool tiles = eif::f32_tiles_fit(cols, mode ? block : 0);
     const void *dw = tiles ? resident_tiles(w, wbytes, il ? eif::kSrcTernIl : eif::kSrcTernRow, rows, cols, fn)
@@ -472,36 +588,38 @@ static void tern_f32(const char *fn, const uint8_t *w, size_t wbytes, const floa
 }
 
 void eif_matmul_bitnet_f32(const uint8_t *weights, const float *scales, const float *input, const float *bias,
-                           float *output, int rows, int cols)
+                           float *output, int rows, int cols) try
 {
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
     tern_f32("eif_matmul_bitnet_f32", weights, (size_t)rows * ((cols + 3) / 4), scales, (size_t)rows, 0, 0, input,
              bias, output, rows, cols, 0);
-}
+} catch (const HostError &) {}
 
 bool eif_gpu_matmul_bitnet_f32(eif_gpu_context_t *ctx, const uint8_t *weights, const float *scales,
-                               const float *input, const float *bias, float *output, int rows, int cols)
+                               const float *input, const float *bias, float *output, int rows, int cols) try
 {
     (void)ctx;
     if (!weights || !input || !output || rows <= 0 || cols <= 0 || !dev_state().ok) return false;
     tern_f32("eif_gpu_matmul_bitnet_f32", weights, (size_t)rows * ((cols + 3) / 4), scales, (size_t)rows, 0, 0,
              input, bias, output, rows, cols, 0);
     return true;
+} catch (const HostError &) {
+    return false;
 }
 
 void eif_matmul_bitnet_block_f32(const uint8_t *weights, const float *block_scales, int block_size,
-                                 const float *input, const float *bias, float *output, int rows, int cols)
+                                 const float *input, const float *bias, float *output, int rows, int cols) try
 {
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
     if (block_size <= 0) block_size = 64;
     const size_t nb = (size_t)((cols + block_size - 1) / block_size);
     tern_f32("eif_matmul_bitnet_block_f32", weights, (size_t)rows * ((cols + 3) / 4), block_scales, rows * nb, 1,
              block_size, input, bias, output, rows, cols, 0);
-}
+} catch (const HostError &) {}
 
 void eif_matmul_bitnet_f32_w1w3(float *out_w1, float *out_w3, const uint8_t *w1, const uint8_t *w3,
                                 const float *scale_w1, const float *scale_w3, const float *input, int hidden_dim,
-                                int dim)
+                                int dim) try
 {
     if (!out_w1 || !out_w3 || !w1 || !w3 || !input || hidden_dim <= 0 || dim <= 0) return;
     const size_t wb = (size_t)hidden_dim * ((dim + 3) / 4);
@@ -509,21 +627,22 @@ void eif_matmul_bitnet_f32_w1w3(float *out_w1, float *out_w3, const uint8_t *w1,
              hidden_dim, dim, 0);
     tern_f32("eif_matmul_bitnet_f32_w1w3", w3, wb, scale_w3, (size_t)hidden_dim, 0, 0, input, nullptr, out_w3,
              hidden_dim, dim, 0);
-}
+} catch (const HostError &) {}
 
 void eif_matmul_bitnet_tmac_interleaved_f32(const uint8_t *interleaved_weights, const float *scales,
                                            const float *input, const float *bias, float *output, int rows,
-                                           int cols)
+                                           int cols) try
 {
     if (!interleaved_weights || !input || !output || rows <= 0 || cols <= 0) return;
     tern_f32("eif_matmul_bitnet_tmac_interleaved_f32", interleaved_weights, (size_t)rows * ((cols + 3) / 4), scales,
              (size_t)rows, 0, 0, input, bias, output, rows, cols, 1);
-}
+} catch (const HostError &) {}
 
 void eif_matmul_bitnet_dense_f32(const uint8_t *weights, const float *scales, const float *input,
-                                 const float *bias, float *output, int rows, int cols)
+                                 const float *bias, float *output, int rows, int cols) try
 {
     static const char *fn = "eif_matmul_bitnet_dense_f32";
+    PinScope pins;
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
     ThreadCtx &c = ctx(fn);
     const size_t wb = (size_t)rows * ((cols + 4) / 5);
@@ -538,13 +657,14 @@ void eif_matmul_bitnet_dense_f32(const uint8_t *weights, const float *scales, co
     else
         DIE_RC(eif::launch_dense_f32((const uint8_t *)dw, dsc, dx, db, dy, rows, cols, c.st), fn);
     download_sync(c, output, dy, sizeof(float) * rows, fn);
-}
+} catch (const HostError &) {}
 
 // ---- INT8 / INT4 row-scaled, FP32 activations ----
 
 static void int_f32(const char *fn, bool int4, const void *w, const float *sc, const float *x, float *out, int rows,
                     int cols)
 {
+    PinScope pins;
     ThreadCtx &c = ctx(fn);
     const size_t wb = int4 ? (size_t)rows * ((cols + 1) / 2) : (size_t)rows * cols;
     const bool tiles = eif::f32_tiles_fit(cols, 0);
@@ -564,28 +684,28 @@ static void int_f32(const char *fn, bool int4, const void *w, const float *sc, c
 }
 
 void tinyllm_matmul_int8_rowscale(float *y, const int8_t *w, const float *x, int in_dim, int out_dim,
-                                  const float *scales)
+                                  const float *scales) try
 {
     if (!y || !w || !x || in_dim <= 0 || out_dim <= 0) return;
     int_f32("tinyllm_matmul_int8_rowscale", false, w, scales, x, y, out_dim, in_dim);
-}
+} catch (const HostError &) {}
 
-void eif_int8_gemv_f32(float *out, const int8_t *W, const float *sc, const float *x, int rows, int cols)
+void eif_int8_gemv_f32(float *out, const int8_t *W, const float *sc, const float *x, int rows, int cols) try
 {
     if (!out || !W || !x || rows <= 0 || cols <= 0) return;
     int_f32("eif_int8_gemv_f32", false, W, sc, x, out, rows, cols);
-}
+} catch (const HostError &) {}
 
-void eif_int4_gemv_f32(float *out, const uint8_t *W, const float *sc, const float *x, int rows, int cols)
+void eif_int4_gemv_f32(float *out, const uint8_t *W, const float *sc, const float *x, int rows, int cols) try
 {
     if (!out || !W || !x || rows <= 0 || cols <= 0) return;
     int_f32("eif_int4_gemv_f32", true, W, sc, x, out, rows, cols);
-}
+} catch (const HostError &) {}
 
 // ---- FP32 GEMM and softmax ----
 
 void eif_gemm_f32_nt_ld(const float *A, int lda, const float *W, int ldw, const float *bias, float *C, int ldc,
-                        int M, int N, int K, int act, int accumulate)
+                        int M, int N, int K, int act, int accumulate) try
 {
     static const char *fn = "eif_gemm_f32_nt_ld";
     if (M <= 0 || N <= 0 || !C) return;
@@ -609,7 +729,7 @@ void eif_gemm_f32_nt_ld(const float *A, int lda, const float *W, int ldw, const 
     DIE_ON(hipMemcpy2DAsync(C, sizeof(float) * ldc, dC, sizeof(float) * N, sizeof(float) * N, M,
                             hipMemcpyDeviceToHost, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
-}
+} catch (const HostError &) {}
 
 void eif_gemm_f32_nt(const float *A, const float *W, const float *bias, float *C, int M, int N, int K, int act,
                      int accumulate)
@@ -617,7 +737,7 @@ void eif_gemm_f32_nt(const float *A, const float *W, const float *bias, float *C
     eif_gemm_f32_nt_ld(A, K, W, K, bias, C, N, M, N, K, act, accumulate);
 }
 
-void eif_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale)
+void eif_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale) try
 {
     static const char *fn = "eif_softmax_rows_f32";
     if (!S || rows <= 0 || cols <= 0 || ld < cols) return;
@@ -629,6 +749,6 @@ void eif_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale)
     DIE_ON(hipMemcpy2DAsync(S, sizeof(float) * ld, dS, sizeof(float) * cols, sizeof(float) * cols, rows,
                             hipMemcpyDeviceToHost, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
-}
+} catch (const HostError &) {}
 
 }  // extern "C"

@@ -178,6 +178,27 @@ int eif_hip_qweight_from_gguf_ternary(eif_hip_qweight **out, int gguf_type, cons
  * of them). Call it after rewriting such a buffer in place or before freeing it.                          */
 void eif_hip_forget_host_weights(const void *host_ptr);
 
+/* Bound on the device bytes of those copies (0: three quarters of the device's memory, the default); returns the
+ * previous setting. A copy that would exceed it first evicts the least recently used copies that no call is
+ * using; a later call needing an evicted buffer uploads it again.                                       */
+size_t eif_hip_set_host_weight_cache_limit(size_t bytes);
+/* Device bytes those copies hold now.                                                                   */
+size_t eif_hip_host_weight_cache_bytes(void);
+
+/* What the host-pointer ABI (eif_quantize_bitnet.h, eif_gemm.h, eif_quant_linear.h) does when a call fails
+ * (no usable gfx950 device, a HIP error). Its functions return void, as the reference's do.
+ *   EIF_HIP_HOST_ABORT (the default): print the call and the error, then abort().
+ *   EIF_HIP_HOST_RECORD: return from the failing call with its outputs not (or not fully) written, and record the
+ *   error for the calling thread (eif_hip_host_last_error).
+ * The mode applies to all threads. Returns the previous mode, or -1 for an unknown one.                 */
+#define EIF_HIP_HOST_ABORT 0
+#define EIF_HIP_HOST_RECORD 1
+int eif_hip_set_host_error_mode(int mode);
+
+/* The calling thread's last error recorded by the host-pointer ABI (EIF_HIP_OK if none), cleared by this call;
+ * msg (may be NULL) receives its description, at most len bytes with the terminating NUL.              */
+int eif_hip_host_last_error(char *msg, size_t len);
+
 /* Token count from which the auto path uses the MFMA GEMM (default 64); returns the previous value. Below it
  * the auto path takes the streaming GEMV for up to 8 tokens, and for more where one workgroup stages 16
  * token rows of the weight's columns and the batch is at most 32 tokens or the weights at most 4 MiB

@@ -357,3 +357,28 @@ def test_gpu_seat(lib, oracle):
     assert not lib.eif_gpu_matmul_bitnet_f32(None, P(w), P(s), P(x), None, P(z), 0, cols)
     assert np.all(z == 7.0)
     lib.eif_hip_forget_host_weights(P(w))
+
+
+def test_weight_cache_bound(lib, oracle):
+    """With a bound on the resident copies, least recently used copies are evicted and uploaded again when needed:
+    the cache stays within the bound and every output matches the oracle."""
+    lib.eif_hip_forget_host_weights(None)
+    assert lib.eif_hip_host_weight_cache_bytes() == 0
+    rows, cols, g = 2048, 2560, 128
+    ws = [synth.ternary_weight((96, i), rows, cols, g) for i in range(4)]   # 1.3 MB codes + 160 KB scales each
+    x = synth.activations((97,), 1, cols)[0]
+    old = lib.eif_hip_set_host_weight_cache_limit(4 << 20)
+    try:
+        for rep in range(2):
+            for i, (w, s) in enumerate(ws):
+                y, o = np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+                lib.eif_matmul_bitnet_block_f32(P(w), P(s), g, P(x), None, P(y), rows, cols)
+                oracle.orc_matmul_bitnet_block_f32(P(w), P(s), g, P(x), None, P(o), rows, cols)
+                codes = synth.unpack_ternary(w, cols).astype(np.float64)
+                mag = (np.abs(codes) * np.repeat(s, g, axis=1)) @ np.abs(x.astype(np.float64))
+                assert within(y, o, mag), (rep, i)
+                assert lib.eif_hip_host_weight_cache_bytes() <= 4 << 20, (rep, i)
+    finally:
+        lib.eif_hip_set_host_weight_cache_limit(old)
+        lib.eif_hip_forget_host_weights(None)
+    assert lib.eif_hip_host_weight_cache_bytes() == 0
