@@ -107,20 +107,17 @@ EIF_DEV v4i mfma64(long a0, long a1, long b0, long b1, v4i c)
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// c += sum_i a[i] * b[OFF + i] over the N operands of a: an even count in pairs on the 64-deep form, an odd
-// count on the 32-deep form throughout (an accumulation chain never mixes the two forms: a 64-deep result fed
-// straight into a dependent 32-deep MFMA gave wrong sums on gfx950). Array references with a compile-time
-// offset keep both operand arrays in registers.
+// c += sum_i a[i] * b[OFF + i] over the N operands of a, in pairs on the 64-deep form; an odd last operand is
+// paired with zero operands on the same form (a g96 group's three operands take two MFMAs, not three 32-deep
+// ones at the same issue cost each). An accumulation chain never mixes the two forms: a 64-deep result fed
+// straight into a dependent 32-deep MFMA gave wrong sums on gfx950. Array references with a compile-time offset
+// keep both operand arrays in registers.
 template <int OFF, int N, int NB>
 EIF_DEV v4i mfma_ops(const long (&a)[N], const long (&b)[NB], v4i c)
 {
-    if constexpr (N % 2 == 0) {
 #pragma unroll
-        for (int i = 0; i < N; i += 2) c = mfma64(a[i], a[i + 1], b[OFF + i], b[OFF + i + 1], c);
-    } else {
-#pragma unroll
-        for (int i = 0; i < N; ++i) c = mfma(a[i], b[OFF + i], c);
-    }
+    for (int i = 0; i + 1 < N; i += 2) c = mfma64(a[i], a[i + 1], b[OFF + i], b[OFF + i + 1], c);
+    if constexpr (N % 2 == 1) c = mfma64(a[N - 1], 0, b[OFF + N - 1], 0, c);
     return c;
 }
 

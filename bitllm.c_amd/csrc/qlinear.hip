@@ -87,11 +87,11 @@ void qgemm_kernel(QArgs a)
     constexpr int PPT = (TM * PR + kGemmThreads - 1) / kGemmThreads;
     constexpr int LDA = GE::SC + 16;               // LDS row stride of the staged block
     __shared__ __align__(16) int8_t xa[2][TM * LDA];
+    __shared__ float scl[2][GROUPED ? 256 : 1];    // grouped: the step's two group scales of the 64 rows, [grp][row]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, s = lane >> 4;
     const int row = blockIdx.x * 64 + wave * 16 + r16;   // < rows_pad
     const bool row_ok = row < a.N;
-    const int row_c = row_ok ? row : a.N - 1;
     const int m0 = blockIdx.y * TM;
     // split along K (gridDim.z > 1): this workgroup's steps [s0, s0 + ns)
     const int s0 = (int)(blockIdx.z * a.nsteps / gridDim.z);
@@ -99,7 +99,7 @@ void qgemm_kernel(QArgs a)
 
     v4i ra[2][PPT];   // a clang vector type: an array of HIP's int4 structs would live in scratch
     uint32_t wb[2][NW];
-    float sc[2][2];
+    float sc[2];      // grouped: the scale this thread stages, of row (tid & 63) and group (tid >> 6) of the step
     // 32-bit byte offsets from the uniform bases (the launcher keeps the batch's int8 rows and the weights below
     // 4 GiB): the loads take the scalar-base form and a step adds st * SC (st * 4 * SB) to them.
     const uint32_t wo = (uint32_t)row * (uint32_t)a.wld + (uint32_t)(s * GE::SB);
@@ -111,26 +111,27 @@ void qgemm_kernel(QArgs a)
         const int tok = m0 + (t < TM ? t : TM - 1);
         xo[i] = (uint32_t)(tok < a.M ? tok : a.M - 1) * (uint32_t)a.ldq + (uint32_t)(16 * q);
     }
-    const uint32_t so = GROUPED ? (uint32_t)row_c * (uint32_t)a.G : 0u;
-    auto load_step = [&](int st, v4i (&r)[PPT], uint32_t (&w)[NW], float (&c)[2]) __attribute__((always_inline)) {
+    // Grouped: threads 0..127 stage the step's scales (threads 128..255 the same ones again, into an unread half),
+    // so they travel with the activation block through LDS. A loaded value that the loop carried in registers to
+    // the next step was copied at the loop's end, and the copy waited for every load in flight.
+    const int sc_row = blockIdx.x * 64 + (threadIdx.x & 63), sc_grp = (threadIdx.x >> 6) & 1;
+    const uint32_t so = GROUPED ? (uint32_t)(sc_row < a.N ? sc_row : a.N - 1) * (uint32_t)a.G : 0u;
+    auto load_step = [&](int st, v4i (&r)[PPT], uint32_t (&w)[NW], float &c) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) r[i] = *reinterpret_cast<const v4i *>(a.xq + (xo[i] + (uint32_t)(st * GE::SC)));
         load_words<NW>(a.W + (wo + (uint32_t)(st * 4 * GE::SB)), w);
         if constexpr (GROUPED) {
-            // the loaded scales are only moved here, so the step's loads stay in flight until the step that uses
-            // them (a select on a loaded value would wait for it, and loads complete in order: for all of them)
-#pragma unroll
-            for (int grp = 0; grp < 2; ++grp) {
-                const int gi = 2 * st + grp;
-                c[grp] = a.scales[so + (uint32_t)(gi < a.G ? gi : a.G - 1)];
-            }
+            const int gi = 2 * st + sc_grp;
+            c = a.scales[so + (uint32_t)(gi < a.G ? gi : a.G - 1)];
         }
     };
     // The MFMA sums carry the weight codes' 2^SHIFT; the combine takes them unshifted against the group scale
     // times 2^-SHIFT: fmaf((float)sum, s * 2^-SHIFT, F) == fmaf((float)(sum >> SHIFT), s, F) bit for bit, since both
-    // products are exact (|sum| < 2^24 and a power-of-two factor is exact for a normal scale).
+    // products are exact (|sum| < 2^24 and a power-of-two factor is exact for a normal scale). The staged scale is
+    // s * 2^-SHIFT, and 0 for a group past the row's last one (a ragged final step), which then adds nothing:
+    // F + 0 * x == F.
     constexpr float kUnshift = 1.0f / (float)(1 << GE::SHIFT);
-    auto store_step = [&](int b, const v4i (&r)[PPT]) __attribute__((always_inline)) {
+    auto store_step = [&](int b, int st, const v4i (&r)[PPT], float c) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
             const int pc = threadIdx.x + i * kGemmThreads;
@@ -139,6 +140,7 @@ void qgemm_kernel(QArgs a)
                 *reinterpret_cast<v4i *>(&xa[b][t * LDA + 16 * q]) = r[i];
             }
         }
+        if constexpr (GROUPED) scl[b][threadIdx.x] = 2 * st + sc_grp < a.G ? c * kUnshift : 0.0f;
     };
 
     float F[TT][4];
@@ -150,7 +152,7 @@ void qgemm_kernel(QArgs a)
         for (int v = 0; v < 4; ++v) F[tt][v] = 0.0f;
     }
 
-    auto compute = [&](int b, int st, const uint32_t (&w)[NW], const float (&c)[2]) __attribute__((always_inline)) {
+    auto compute = [&](int b, int st, const uint32_t (&w)[NW]) __attribute__((always_inline)) {
         long bop[GE::NMF];
         decode<FMT, UD>(w, bop);
 #pragma unroll
@@ -174,8 +176,7 @@ void qgemm_kernel(QArgs a)
                                 }
                             }
                         } else {
-                            // a group past the row's last one (a ragged final step) adds nothing: F + 0 * x == F
-                            const float cu = gi < a.G ? c[grp] * kUnshift : 0.0f;
+                            const float cu = scl[b][64 * grp + 16 * wave + r16];
 #pragma unroll
                             for (int v = 0; v < 4; ++v) F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
                         }
@@ -193,21 +194,30 @@ void qgemm_kernel(QArgs a)
         }
     };
 
+    // The loop runs whole pairs of steps (buffer 0, then buffer 1) and has one exit, at its head; an odd last step
+    // follows it from buffer 0. Every prefetch is issued, past the split's last step as a reload of that step, and
+    // every staging store is made (past the last step into a buffer no later step reads). A load or store skipped
+    // on some path, or an exit in the middle of the loop, gives the loop head an entry with other loads in flight,
+    // and the compiler then waits there for nearly all of them.
+    const int s_last = s0 + ns - 1;
+    auto clamp_step = [&](int st) { return st < s_last ? st : s_last; };
     load_step(s0, ra[0], wb[0], sc[0]);
-    if (ns > 1) load_step(s0 + 1, ra[1], wb[1], sc[1]);
-    store_step(0, ra[0]);
+    load_step(clamp_step(s0 + 1), ra[1], wb[1], sc[1]);
+    store_step(0, s0, ra[0], sc[0]);
     __syncthreads();
-    for (int j = 0; j < ns; j += 2) {
-        compute(0, s0 + j, wb[0], sc[0]);
-        if (j + 2 < ns) load_step(s0 + j + 2, ra[0], wb[0], sc[0]);
-        if (j + 1 < ns) store_step(1, ra[1]);
+    const int npairs = ns >> 1;
+    for (int p = 0; p < npairs; ++p) {
+        const int st = s0 + 2 * p;
+        compute(0, st, wb[0]);
+        load_step(clamp_step(st + 2), ra[0], wb[0], sc[0]);
+        store_step(1, clamp_step(st + 1), ra[1], sc[1]);
         __syncthreads();
-        if (j + 1 >= ns) break;
-        compute(1, s0 + j + 1, wb[1], sc[1]);
-        if (j + 3 < ns) load_step(s0 + j + 3, ra[1], wb[1], sc[1]);
-        if (j + 2 < ns) store_step(0, ra[0]);
+        compute(1, st + 1, wb[1]);
+        load_step(clamp_step(st + 3), ra[1], wb[1], sc[1]);
+        store_step(0, clamp_step(st + 2), ra[0], sc[0]);
         __syncthreads();
     }
+    if (ns & 1) compute(0, s_last, wb[0]);
     if constexpr (GROUPED && ACC) return;
 
     if (gridDim.z > 1) {
@@ -945,9 +955,8 @@ std::mutex g_scratch_mu;
 float *g_scratch_dev[kMaxDevices];
 int *g_scratch_cnt_dev[kMaxDevices];
 
-// Token tile of the GEMM (16 x TT tokens, see launch_gemm) and its row tiles x token tiles for M tokens.
+// Token tiles of the GEMM (16 x TT tokens per workgroup, see launch_gemm) for M tokens.
 int gemm_tt(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
-int gemm_tiles(int rows_pad, int M) { return rows_pad / 64 * eif_ceil_div(M, 16 * gemm_tt(M)); }
 
 // A caller-provided split workspace (eif_hip_qlinear_ex_noalloc): while set on this thread, the GEMM takes its
 // split partials from it instead of the per-stream workspace.
@@ -958,15 +967,15 @@ struct FixedWs {
 };
 thread_local FixedWs tl_fixed_ws;
 
-// Splits along K for `tiles` output tiles of 64 rows x 16 TT tokens, with the partials' space (ks x tiles x
-// 256 threads x 4 TT floats) and the tiles' counters; 1 when the launch is not split.
-template <bool ACC, int TT>
-int pick_split(QArgs &a, int tiles, hipStream_t st)
+// Splits along K for `tiles` output tiles of nv values per thread, with the partials' space (ks x tiles x 256
+// threads x nv floats) and the tiles' counters; 1 when the launch is not split.
+template <bool ACC>
+int pick_split(QArgs &a, int tiles, int nv, hipStream_t st)
 {
     if (ACC) return 1;
     const int ks = choose_split(a.nsteps, tiles);
     if (ks <= 1 || tiles > kMaxSplitTiles) return 1;
-    const size_t bytes = (size_t)ks * tiles * kGemmThreads * 4 * TT * sizeof(float);
+    const size_t bytes = (size_t)ks * tiles * kGemmThreads * nv * sizeof(float);
     if (tl_fixed_ws.ptr) {   // a fixed workspace too small for this split: -1, nothing is launched
         if (bytes > tl_fixed_ws.bytes) return -1;
         a.part = tl_fixed_ws.ptr;
@@ -990,7 +999,7 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     if ((size_t)a.M * a.ldq >= ((size_t)1 << 32) || (size_t)rows_pad * a.wld >= ((size_t)1 << 32)) return EIF_HIP_E_LIMIT;
     const int tm = eif_ceil_div(a.M, 16 * TT), tiles = rows_pad / 64 * tm;
     static_assert(TT == 1 || TT == 2 || TT == 4, "token tiles of gemm_tt");
-    const int ks = pick_split<ACC, TT>(a, tiles, st);
+    const int ks = pick_split<ACC>(a, tiles, 4 * TT, st);
     if (ks == -2) return EIF_HIP_E_DEVICE;
     if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
