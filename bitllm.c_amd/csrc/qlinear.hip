@@ -72,9 +72,10 @@ struct QArgs {
 constexpr int kGemmThreads = 256;
 
 // Waves per SIMD the register budget is cut for: four for the g128 ternary and INT formats (their MFMA sums
-// would otherwise sit in accumulation registers, at three waves), the compiler's choice for the rest.
+// would otherwise sit in accumulation registers, at three waves), the compiler's choice for the other group sizes
+// (g32 at four waves spilled).
 template <int FMT, int UD>
-constexpr int gemm_waves() { return FMT == kTern && UD == 3 ? 1 : 4; }
+constexpr int gemm_waves() { return FMT == kTern && UD != 4 ? 1 : 4; }
 
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<FMT, UD>())))

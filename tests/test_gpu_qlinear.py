@@ -61,6 +61,9 @@ TERN_GROUPED = [
     (2560, 6912, 96, 64, GEMM),
     (300, 2560, 128, 200, GEMM),
     (17, 96, 96, 1, GEMM),
+    (130, 200, 32, 70, GEMM),       # g32, g64, g256 with 64-token tiles (the compiler's register budget)
+    (70, 640, 64, 100, GEMM),
+    (64, 512, 256, 40, GEMM),
 ]
 
 
