@@ -427,6 +427,7 @@ def cpu_child(args):
 
 
 def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in, norm):
+    import numpy as np
     ex = {}
     reps = max(50, args.steps // 2)
     ncopy = len(copies)
@@ -485,31 +486,37 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
     for h in heads:
         h.close()
 
-    # INT8 Qwen2.5-0.5B-like layer, M = 1 and 128
+    # INT8 Qwen2.5-0.5B-like layer, M = 1 and 128: q|k|v and gate|up share their input and are stacked into one
+    # weight each (1152x896, 9728x896), as the BitNet layer above stacks them, so a layer is four launches
     l8 = synth.QWEN25_05B_LAYER
     base8 = {name: synth.int8_weight((105, i), N, K) for i, (name, N, K) in enumerate(l8)}
-    wb8 = sum(synth.int_linear_bytes(N, K, 8, 0) for _, N, K in l8)
-    c8 = [{name: bh.QWeight(bh.W_INT8, N, K, 0, *base8[name]) for name, N, K in l8} for _ in range(copies_for(wb8))]
+    stack = {"qkv": ("q", "k", "v"), "o": ("o",), "gateup": ("gate", "up"), "down": ("down",)}
+    s8 = [(name, sum(base8[p][0].shape[0] for p in parts), base8[parts[0]][0].shape[1]) for name, parts in stack.items()]
+    sbase = {name: (np.concatenate([base8[p][0] for p in parts]), np.concatenate([base8[p][1] for p in parts]))
+             for name, parts in stack.items()}
+    wb8 = sum(synth.int_linear_bytes(N, K, 8, 0) for _, N, K in s8)
+    c8 = [{name: bh.QWeight(bh.W_INT8, N, K, 0, *sbase[name]) for name, N, K in s8} for _ in range(copies_for(wb8))]
     for M in (1, 128):
         xk = {K: torch.from_numpy(synth.activations((106, K, M), M, K)).to(dev) for K in (896, 4864)}
         qk = {K: torch.zeros((M, (K + 63) // 64 * 64), dtype=torch.int8, device=dev) for K in (896, 4864)}
         sk = {K: torch.zeros(M, dtype=torch.float32, device=dev) for K in (896, 4864)}
         for K in (896, 4864):
             bh.prep_rows(xk[K], qk[K], sk[K], 0, 1.0)
-        yk = {name: torch.zeros((M, N), dtype=torch.float32, device=dev) for name, N, K in l8}
+        yk = {name: torch.zeros((M, N), dtype=torch.float32, device=dev) for name, N, K in s8}
 
         def lin8(i):
             for name, q in c8[i % len(c8)].items():
                 q.linear(qk[q.cols], sk[q.cols], yk[name])
         t = timer(lin8, max(20, reps // 4))
-        b = sum(synth.int_linear_bytes(N, K, 8, M) for _, N, K in l8)
-        ex[f"int8_qwen05b_layer_m{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1)}
+        b = sum(synth.int_linear_bytes(N, K, 8, M) for _, N, K in s8)
+        ex[f"int8_qwen05b_layer_m{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                                          "launches": "qkv 1152x896, o 896x896, gate|up 9728x896, down 896x4864",
+                                          "path": "gemm" if M >= bh.load().eif_hip_gemm_min_tokens() else "gemv"}
     for cs in c8:
         for q in cs.values():
             q.close()
 
     # the drop-in host API (host x in, host y out over PCIe; weights resident after the first call), M = 1
-    import numpy as np
     lib = bh.load()
     N, K, g = 6912, 2560, 128
     hw, hsc = synth.ternary_weight((107,), N, K, g)

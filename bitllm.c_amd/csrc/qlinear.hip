@@ -917,26 +917,22 @@ int device_cus()
 
 int g_gemm_split = 0;   // splits along K of the GEMM, 0 = chosen from the shape
 
-// Splits along K (at most 16, at least three steps per split). Fewer tiles than CUs: the split with the fewest
-// rounds of workgroups per unit of work, ceil(tiles s / CUs) / s, the smallest of equal ones. One round or
-// more: 2 when a long K (24 steps or more) leaves the last round under 70% full (e.g. 320 tiles on 256 CUs).
-// 1 for the parity outputs and when no workspace can be had (first use of a stream inside a graph capture).
+// Splits along K (at most 16, at least three steps per split). Fewer tiles than CUs: none for a short K loop
+// (under 24 steps, where a split's coherent round trip costs more than the steps it takes off), else about two
+// workgroups per CU, floor(2 CUs / tiles), keeping six steps or more per split. One round or more: 2 when a long
+// K (24 steps or more) leaves the last round under 70% full (e.g. 320 tiles on 256 CUs). 1 for the parity
+// outputs and when no workspace can be had (first use of a stream inside a graph capture). Measured per shape
+// (INT8 896x4864 at 128 tokens: 15.4 us unsplit, 10.2 at 4 splits, 12.9 at 16; ternary 2560x2560 at 64 tokens:
+// 6.0 unsplit, 6.4 at 3).
 int choose_split(int nsteps, int tiles)
 {
     int ks = g_gemm_split;
     if (ks == 0) {
-        const int C = device_cus(), smax = std::min(16, std::max(1, nsteps / 3));
-        if (tiles < C) {
-            ks = 1;
-            double best = 1.0;
-            for (int s2 = 2; s2 <= smax; ++s2) {
-                const double r = (double)eif_ceil_div(tiles * s2, C) / s2;
-                if (r < best - 1e-9) best = r, ks = s2;
-            }
-        } else {
-            const int rounds = eif_ceil_div(tiles, C);
-            ks = nsteps >= 24 && (double)tiles < 0.7 * rounds * C ? 2 : 1;
-        }
+        const int C = device_cus();
+        if (tiles < C)
+            ks = nsteps < 24 ? 1 : std::max(1, std::min(2 * C / std::max(1, tiles), nsteps / 6));
+        else
+            ks = nsteps >= 24 && (double)tiles < 0.7 * eif_ceil_div(tiles, C) * C ? 2 : 1;
     }
     return std::min(ks, std::min(16, std::max(1, nsteps / 3)));
 }
@@ -956,8 +952,24 @@ std::mutex g_scratch_mu;
 float *g_scratch_dev[kMaxDevices];
 int *g_scratch_cnt_dev[kMaxDevices];
 
-// Token tiles of the GEMM (16 x TT tokens per workgroup, see launch_gemm) for M tokens.
-int gemm_tt(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+int g_gemm_tt = 0;   // token tiles of a GEMM workgroup (1, 2, 4), 0 = chosen from the batch
+
+// Token tiles of the GEMM (16 x TT tokens per workgroup) for M tokens on rt64 tiles of 64 rows and nsteps steps
+// of K. The largest tile that holds the batch (64 tokens above 32), made smaller while the workgroups do not
+// fill the CUs once (a 64-token tile: twice, when the K loop is short), since a workgroup's time is a chain of
+// dependent steps and more, shorter chains finish sooner; each extra token tile re-reads the weight tile, mostly
+// from L2. Measured: INT8 896x896 at 128 tokens 7.7 us with 64-token tiles, 5.4 with 16; ternary 13824x2560 at 64
+// tokens 13.7 / 10.5 (32-token tiles) / 13.9 (16); ternary 2560x2560 at 512 tokens 16.0 / 12.2 (32).
+int gemm_tt(int M, int rt64, int nsteps)
+{
+    if (g_gemm_tt > 0) return g_gemm_tt;
+    int tt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    const int C = device_cus();
+    auto wgs = [&](int t) { return rt64 * eif_ceil_div(M, 16 * t); };
+    if (tt == 4 && nsteps < 24 && wgs(4) < 2 * C) tt = 2;
+    while (tt > 1 && wgs(tt) < C) tt /= 2;
+    return tt;
+}
 
 // A caller-provided split workspace (eif_hip_qlinear_ex_noalloc): while set on this thread, the GEMM takes its
 // split partials from it instead of the per-stream workspace.
@@ -1009,11 +1021,11 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     return EIF_HIP_OK;
 }
 
-// Token tile of the GEMM: 16, 32 or 64 tokens, the smallest that holds the batch (larger batches: 64).
+// Token tile of the GEMM: 16, 32 or 64 tokens (gemm_tt).
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemm(const QArgs &a, int rows_pad, hipStream_t st)
 {
-    switch (gemm_tt(a.M)) {
+    switch (gemm_tt(a.M, rows_pad / 64, a.nsteps)) {
     case 1: return launch_gemm_t<FMT, UD, GROUPED, ACC, 1>(a, rows_pad, st);
     case 2: return launch_gemm_t<FMT, UD, GROUPED, ACC, 2>(a, rows_pad, st);
     default: return launch_gemm_t<FMT, UD, GROUPED, ACC, 4>(a, rows_pad, st);
@@ -1651,6 +1663,13 @@ int eif_hip_set_gemm_split(int k)
 {
     int old = g_gemm_split;
     if (k >= 0 && k <= 16) g_gemm_split = k;
+    return old;
+}
+
+int eif_hip_set_gemm_token_tiles(int tt)
+{
+    const int old = g_gemm_tt;
+    if (tt == 0 || tt == 1 || tt == 2 || tt == 4) g_gemm_tt = tt;
     return old;
 }
 

@@ -248,6 +248,10 @@ int eif_hip_set_gemv_prep_cols(int e);
  * capture.                                                                                              */
 int eif_hip_set_gemm_split(int k);
 
+/* Token tiles of 16 tokens per GEMM workgroup (1, 2 or 4; 0 = chosen from the batch, the default: 1 up to 16
+ * tokens, 2 up to 32, else 4). Returns the previous setting. A tuning knob: results do not depend on it.     */
+int eif_hip_set_gemm_token_tiles(int tt);
+
 #ifdef __cplusplus
 }
 #endif
