@@ -112,6 +112,7 @@ _SIGS = {
     "eif_hip_set_gemv_row_tiles": (_i, [_i]),
     "eif_hip_set_gemv_token_chunk": (_i, [_i]),
     "eif_hip_set_gemv_stream": (_i, [_i]),
+    "eif_hip_set_gemv_rowpair": (_i, [_i]),
     "eif_hip_set_f32_tiles_per_wave": (_i, [_i]),
     "eif_hip_set_f32_ksplit": (_i, [_i]),
     "eif_hip_set_gemv_prep_cols": (_i, [_i]),

@@ -772,6 +772,128 @@ __global__ __launch_bounds__(kStreamThreads) void qstream_kernel(QArgs a, int nt
     }
 }
 
+// ---- row-pair GEMV for vocabulary-sized row-scaled matrices at one token row (INT4, INT8) ----
+//
+// The MFMA GEMV's load instructions each cover 64 bytes of 16 rows 512 bytes or more apart. Here each half-wave
+// reads 512 contiguous bytes of one row, so a load instruction is two 512-byte runs of whole cache lines, and
+// the products are taken with v_dot4_i32_i8 on the resident layouts as they are:
+//   INT8: a row is in column order, so the 16-byte chunk k holds columns 16k .. 16k + 15;
+//   INT4: the 16-byte chunk k of a row (step k / 4, slot k % 4) holds columns 32k .. 32k + 31: dword t's high
+//         nibbles columns 32k + 8t + b, its low nibbles 32k + 8t + 4 + b (b = byte), each 16 v after masking.
+// Lane h of a half reads chunks h, h + 32, .. (pass p = 0 .. P-1) of its row, so the activation bytes it needs
+// are the same for every row: they are loaded once into registers. A wave takes one 16-row tile, 8 row pairs
+// (half 0 the even row) x P passes, all its loads issued first. Each lane's sums of its 8 row pairs are summed
+// over the half-wave by a transposed reduction (xor 16, 8, 4 exchanging half the values each time, then xor
+// 2, 1), which leaves the sum of row pair (h >> 2) on the four lanes of each quad. The int32 sums are exact, so
+// y has the MFMA GEMV's bits: ((float)isum * xs) * s[r] (+ bias); the per-tile maxima too.
+constexpr int kRowPairThreads = 256;
+// Passes of 512 bytes per row it is compiled for (32 registers of codes per pass, plus 8 (INT4) or 4 (INT8) of
+// activations): INT4 K up to 4096, INT8 K up to 2560.
+template <int FMT>
+constexpr int rowpair_max_p() { return FMT == kI4 ? 4 : 5; }
+
+template <int FMT, int P, bool ACC>
+__global__ __launch_bounds__(kRowPairThreads) void qrowpair_kernel(QArgs a, int ntiles)
+{
+    static_assert(FMT == kI4 || FMT == kI8, "row-scaled INT4 / INT8 layouts");
+    constexpr int SHIFT = Geo<FMT, 0>::SHIFT;
+    constexpr int CB = FMT == kI4 ? 32 : 16;   // activation bytes (columns) of a 16-byte chunk
+    const int lane = threadIdx.x & 63, h = lane & 31, half = lane >> 5;
+    const int tile = blockIdx.x * (kRowPairThreads / 64) + (int)(threadIdx.x >> 6);
+    if (tile >= ntiles) return;   // the last workgroup's spare waves (no barrier in this kernel)
+
+    // 1. weight loads (rows are padded to whole tiles), then the activation chunks, the row's scale and bias
+    uint4 wv[8][P];
+    const uint8_t *wp = a.W + (size_t)(tile * 16 + half) * a.wld + 16 * h;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int q = 0; q < P; ++q) wv[c][q] = *reinterpret_cast<const uint4 *>(wp + (size_t)(2 * c) * a.wld + 512 * q);
+    uint4 xv[P][CB / 16];
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+#pragma unroll
+        for (int i = 0; i < CB / 16; ++i)
+            xv[q][i] = *reinterpret_cast<const uint4 *>(a.xq + CB * (32 * q + h) + 16 * i);
+    const int orow = tile * 16 + 2 * (h >> 2) + half;   // the row whose sum this lane's quad ends with
+    const bool row_ok = orow < a.N;
+    const int rc = row_ok ? orow : a.N - 1;
+    const float *w0 = reinterpret_cast<const float *>(a.W);
+    const float rs_raw = *(a.scales ? a.scales + rc : w0);
+    const float bb_raw = *(a.bias ? a.bias + rc : w0);
+    const float xs = a.xs[0];
+    const bool b4 = h & 16, b3 = h & 8, b2 = h & 4;
+    // 2. dot products, row pair by row pair in load order
+    int acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        int sum = 0;
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+            const uint32_t d[4] = {wv[c][q].x, wv[c][q].y, wv[c][q].z, wv[c][q].w};
+            if constexpr (FMT == kI4) {
+                const uint32_t x8[8] = {xv[q][0].x, xv[q][0].y, xv[q][0].z, xv[q][0].w,
+                                        xv[q][1].x, xv[q][1].y, xv[q][1].z, xv[q][1].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    sum = __builtin_amdgcn_sdot4((int)(d[t] & 0xF0F0F0F0u), (int)x8[2 * t], sum, false);
+                    sum = __builtin_amdgcn_sdot4((int)((d[t] << 4) & 0xF0F0F0F0u), (int)x8[2 * t + 1], sum, false);
+                }
+            } else {
+                const uint32_t x4[4] = {xv[q][0].x, xv[q][0].y, xv[q][0].z, xv[q][0].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) sum = __builtin_amdgcn_sdot4((int)d[t], (int)x4[t], sum, false);
+            }
+        }
+        acc[c] = sum;
+    }
+
+    // 3. transposed reduction over the 32 lanes of the half
+    int w4[4], w2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int keep = b4 ? acc[4 + i] : acc[i], give = b4 ? acc[i] : acc[4 + i];
+        w4[i] = keep + __shfl_xor(give, 16, 64);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int keep = b3 ? w4[2 + i] : w4[i], give = b3 ? w4[i] : w4[2 + i];
+        w2[i] = keep + __shfl_xor(give, 8, 64);
+    }
+    int z = (b2 ? w2[1] : w2[0]) + __shfl_xor(b2 ? w2[0] : w2[1], 4, 64);
+    z += __shfl_xor(z, 2, 64);
+    z += __shfl_xor(z, 1, 64);
+
+    // 4. epilogue: one lane per quad writes; the tile's largest output and its first row over all 16 rows
+    const int isum = z >> SHIFT;
+    float out = -INFINITY;
+    if (row_ok) {
+        if constexpr (ACC) {
+            if ((h & 3) == 0) a.acc[orow] = isum;
+        } else {
+            out = ((float)isum * xs) * (a.scales ? rs_raw : 1.0f);
+            if (a.bias) out = out + bb_raw;
+            if ((h & 3) == 0) a.y[orow] = out;
+        }
+    }
+    if constexpr (!ACC) {
+        if (a.amax_v) {
+            float bv = out == out ? out : -INFINITY;
+            int bi = row_ok ? orow : 0x7fffffff;
+#pragma unroll
+            for (int off = 4; off < 64; off <<= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+            }
+            if (lane == 0) {
+                a.amax_v[tile] = bv;
+                a.amax_i[tile] = bi;
+            }
+        }
+    }
+}
+
 // The fused prep on its own: token row m = blockIdx.x -> int8 codes xq[m, 0 .. ldq) (zeros past K) and xs[m].
 // E columns per thread, the threads covering ldq; LB as in prep_finish.
 template <int E, int LB>
@@ -1263,12 +1385,49 @@ int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t s
     }
 }
 
+// The row-pair GEMV: row-scaled INT4 / INT8 matrices at one prepped token row whose rows are whole 512-byte runs
+// (at most rowpair_max_p of them); by default only vocabulary-sized ones (kBigTiles tiles or more), where
+// bandwidth decides. Returns 1 for other shapes.
+int g_gemv_rowpair = 0;   // 0 = vocabulary-sized matrices, 1 = every shape it takes, -1 = off
+
+template <int FMT, int UD, bool GROUPED, bool ACC>
+int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
+{
+    if constexpr (FMT == kTern || GROUPED) {
+        return 1;
+    } else {
+        if (g_gemv_rowpair < 0 || p.x || p.sh_ml || a.M != 1 || a.wld % 512 != 0) return 1;
+        const int ntiles = rows_pad / 16;
+        if (g_gemv_rowpair == 0 && ntiles < kBigTiles) return 1;
+        const int grid = eif_ceil_div(ntiles, kRowPairThreads / 64);
+        constexpr int PM = rowpair_max_p<FMT>();
+        static_assert(PM <= 5, "one case per pass count");
+        switch (a.wld / 512) {
+        case 1: qrowpair_kernel<FMT, 1, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
+        case 2: qrowpair_kernel<FMT, 2, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
+        case 3: qrowpair_kernel<FMT, 3, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
+        case 4: qrowpair_kernel<FMT, 4, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
+        case 5:
+            if constexpr (PM >= 5) {
+                qrowpair_kernel<FMT, PM >= 5 ? 5 : 1, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles);
+                break;
+            }
+            return 1;
+        default: return 1;
+        }
+        EIF_HIP_LAUNCHED();
+        return EIF_HIP_OK;
+    }
+}
+
 // The batch in one workgroup when the fused prep or the shares are in (at most kFusedMaxM rows) or it is at
 // most kFusedMaxM rows; else workgroups of mw token rows (token tiles, then chunks), mw from kGemvDefaultWgM
 // (or the knob) halved until the staged rows and sums fit.
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemv(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
 {
+    const int rp = launch_rowpair<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
+    if (rp != 1) return rp;
     const int rs = launch_stream<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
     if (rs != 1) return rs;
     if (p.x || p.sh_ml || a.M <= kFusedMaxM) {
@@ -1663,6 +1822,13 @@ int eif_hip_set_gemm_split(int k)
 {
     int old = g_gemm_split;
     if (k >= 0 && k <= 16) g_gemm_split = k;
+    return old;
+}
+
+int eif_hip_set_gemv_rowpair(int mode)
+{
+    const int old = g_gemv_rowpair;
+    if (mode >= -1 && mode <= 1) g_gemv_rowpair = mode;
     return old;
 }
 

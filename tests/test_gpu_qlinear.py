@@ -488,3 +488,42 @@ def test_stream_gemv(gpu, oracle, fmt, N, K):
     finally:
         lib.eif_hip_set_gemv_stream(old)
     qw.close()
+
+
+@pytest.mark.parametrize("fmt,N,K,mode", [("int4", 151936, 1024, 0), ("int8", 128256, 2560, 0),
+                                          ("int8", 65600, 512, 0), ("int4", 1000, 2048, 1), ("int4", 77, 4096, 1),
+                                          ("int8", 130, 1536, 1), ("int8", 64, 2048, 1)])
+def test_rowpair_gemv(gpu, oracle, fmt, N, K, mode):
+    """The row-pair GEMV (one token row; rows of whole 512-byte runs read half a wave at a time, v_dot4 products
+    on the resident layout) on vocabulary-sized matrices (its default) and, forced on, on small and ragged ones:
+    y with and without a bias and the int32 sums bit for bit against the oracle, and the same bits with it off
+    (the tiled GEMV)."""
+    lib = gpu.load()
+    if fmt == "int8":
+        w, s = synth.int8_weight((71, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+        fn, afn = oracle.orc_int8_gemv_i8act, oracle.orc_int8_acc_i32
+    else:
+        w, s = synth.int4_weight((72, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+        fn, afn = oracle.orc_int4_gemv_i8act, oracle.orc_int4_acc_i32
+    old = lib.eif_hip_set_gemv_rowpair(mode)
+    try:
+        x = synth.activations((73, N, K), 1, K)
+        xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+        oacc = np.zeros((1, N), np.int32)
+        afn(P(w), P(xq), qw.kpad, 1, N, K, P(oacc))
+        for bias in (None, synth.rng(74, N).standard_normal(N).astype(np.float32)):
+            oy = np.zeros((1, N), np.float32)
+            fn(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, 1, N, K)
+            for m in (mode, -1):
+                lib.eif_hip_set_gemv_rowpair(m)
+                y = run_linear(gpu, qw, xq_d, xs_d, 1, GEMV, bias)
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (m, bias is None)
+        for m in (mode, -1):
+            lib.eif_hip_set_gemv_rowpair(m)
+            acc = run_acc(gpu, qw, xq_d, 1, (1, N), GEMV)
+            assert np.array_equal(acc, oacc), m
+    finally:
+        lib.eif_hip_set_gemv_rowpair(old)
+    qw.close()
