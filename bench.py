@@ -486,6 +486,34 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
     for h in heads:
         h.close()
 
+    # INT4 Qwen3.5-style FFN linears (hidden 1024, FFN 3584), M = 1 and 32: gate|up stacked (7168x1024), down
+    # 1024x3584
+    l4 = synth.QWEN35_INT4_LAYER
+    base4 = {name: synth.int4_weight((109, i), N, K) for i, (name, N, K) in enumerate(l4)}
+    f4 = {"gateup": (np.concatenate([base4["gate"][0], base4["up"][0]]),
+                     np.concatenate([base4["gate"][1], base4["up"][1]])), "down": base4["down"]}
+    s4 = [("gateup", 7168, 1024), ("down", 1024, 3584)]
+    wb4 = sum(synth.int_linear_bytes(N, K, 4, 0) for _, N, K in s4)
+    c4w = [{name: bh.QWeight(bh.W_INT4, N, K, 0, *f4[name]) for name, N, K in s4} for _ in range(copies_for(wb4))]
+    for M in (1, 32):
+        xk = {K: torch.from_numpy(synth.activations((110, K, M), M, K)).to(dev) for K in (1024, 3584)}
+        qk = {K: torch.zeros((M, c4w[0][name].kpad), dtype=torch.int8, device=dev) for name, _, K in s4}
+        sk = {K: torch.zeros(M, dtype=torch.float32, device=dev) for K in (1024, 3584)}
+        for K in (1024, 3584):
+            bh.prep_rows(xk[K], qk[K], sk[K], 0, 1.0)
+        yk = {name: torch.zeros((M, N), dtype=torch.float32, device=dev) for name, N, K in s4}
+
+        def lin4(i):
+            for name, q in c4w[i % len(c4w)].items():
+                q.linear(qk[q.cols], sk[q.cols], yk[name])
+        t = timer(lin4, max(20, reps // 4))
+        b = sum(synth.int_linear_bytes(N, K, 4, M) for _, N, K in s4)
+        ex[f"int4_qwen35_ffn_m{M}"] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                                       "launches": "gate|up 7168x1024, down 1024x3584"}
+    for cs in c4w:
+        for q in cs.values():
+            q.close()
+
     # INT8 Qwen2.5-0.5B-like layer, M = 1 and 128: q|k|v and gate|up share their input and are stacked into one
     # weight each (1152x896, 9728x896), as the BitNet layer above stacks them, so a layer is four launches
     l8 = synth.QWEN25_05B_LAYER

@@ -1574,18 +1574,19 @@ bool gemv_fits_tile(const eif_hip_qweight *w)
 }
 
 // Auto path: the GEMV up to kFusedMaxM tokens; below eif_hip_gemm_min_tokens() also where a token tile fits one
-// workgroup and the batch is at most two tiles or the weights at most kGemvSmallBytes (the GEMV streams the
-// weights once per workgroup chunk, the GEMM once per 64 tokens); else the GEMM.
-constexpr size_t kGemvSmallBytes = (size_t)4 << 20;
+// workgroup and the batch is at most two tiles, or the matrix has under 32 tiles of 64 rows (few GEMM
+// workgroups, each with a long chain along K); else the GEMM. Measured at 48 and 63 tokens: ternary 3840x2560
+// GEMV 8.5 / 8.5 us, GEMM 6.5 / 6.5; 2560x2560 6.5 / 8.3 against 6.1 / 6.1; INT4 3584x1024 5.6 / 5.7 against
+// 4.7 / 4.7; INT4 1024x3584 5.5 / 5.5 against 6.3 / 6.6.
+constexpr int kGemvFewRows = 32 * 64;
 
 int resolve_path(const eif_hip_qweight *w, int path, int M)
 {
     if (path != EIF_HIP_PATH_AUTO) return path;
     if (M >= g_gemm_min_tokens) return EIF_HIP_PATH_GEMM;
     if (M <= kFusedMaxM) return EIF_HIP_PATH_GEMV;
-    const size_t bytes = (size_t)w->rows_pad * w->wld + (size_t)w->rows * (w->ngroups > 0 ? w->ngroups : 1) * 4;
-    return gemv_fits_tile(w) && (M <= 2 * kGemvTileM || bytes <= kGemvSmallBytes) ? EIF_HIP_PATH_GEMV
-                                                                                   : EIF_HIP_PATH_GEMM;
+    return gemv_fits_tile(w) && (M <= 2 * kGemvTileM || w->rows_pad < kGemvFewRows) ? EIF_HIP_PATH_GEMV
+                                                                                     : EIF_HIP_PATH_GEMM;
 }
 
 QArgs make_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
