@@ -1155,8 +1155,9 @@ int launch_gemm(const QArgs &a, int rows_pad, hipStream_t st)
 }
 
 // Waves per tile of the small-batch GEMV (measured on MI355X with graph-chained launches): two steps per wave
-// for the 1-9 MB matrices of a layer, four for long rows (>= 24 steps), eight when the tiles alone fill the
-// chip (vocabulary heads), at most 16 waves.
+// for the 1-9 MB matrices of a layer, four for long rows (>= 24 steps), eight for very long ones (>= 64 steps:
+// INT8 896x4864 at one token 6.4 us with 10 waves, 7.6 with 16) and when the tiles alone fill the chip
+// (vocabulary heads), at most 16 waves.
 // Row tiles from which a row-scaled GEMV of prepped activations is shaped for streaming (one tile per
 // workgroup, about 10 KiB of weights per wave) and from which eif_hip_qlinear_prep runs its prep separately once
 // instead of in every workgroup (the vocabulary heads).
@@ -1164,7 +1165,7 @@ constexpr int kBigTiles = 4096;
 
 int pick_ks_gemv(int row_tiles, int nsteps)
 {
-    const int spw = row_tiles >= 4096 ? 8 : (nsteps >= 24 ? 4 : 2);
+    const int spw = row_tiles >= 4096 || nsteps >= 64 ? 8 : (nsteps >= 24 ? 4 : 2);
     int ks = eif_ceil_div(nsteps, spw);
     return ks > 16 ? 16 : (ks < 1 ? 1 : ks);
 }
