@@ -238,6 +238,11 @@ def test_ternary_rowscale_bit_exact(gpu, oracle, N, K, M, path, with_bias):
     ("int4", 3584, 1024, 1, GEMV), ("int4", 1024, 3584, 1, GEMV), ("int4", 3584, 1024, 32, GEMM),
     ("int4", 3584, 1024, 32, GEMV), ("int4", 1024, 3584, 16, GEMV),
     ("int4", 50, 333, 4, GEMV), ("int4", 50, 333, 40, GEMM), ("int4", 50, 333, 40, GEMV),
+    # the GEMM's token tiles and splits chosen from the workgroup count: 16-token tiles with 4 splits along K
+    # (896x4864 at 128), unsplit 16-token tiles (the stacked q|k|v), 32-token tiles (the stacked gate|up), INT4
+    # FFN shapes at 64 and 32 tokens
+    ("int8", 896, 4864, 128, GEMM), ("int8", 1152, 896, 128, GEMM), ("int8", 9728, 896, 128, GEMM),
+    ("int4", 1024, 3584, 64, GEMM), ("int4", 7168, 1024, 32, GEMM),
 ])
 def test_int_rowscale_bit_exact(gpu, oracle, fmt, N, K, M, path):
     if fmt == "int8":
