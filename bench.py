@@ -526,7 +526,7 @@ def extra_workloads(args, torch, bh, synth, timer, dev, copies, xq, xs, y, x_in,
     c8 = [{name: bh.QWeight(bh.W_INT8, N, K, 0, *sbase[name]) for name, N, K in s8} for _ in range(copies_for(wb8))]
     for M in (1, 128):
         xk = {K: torch.from_numpy(synth.activations((106, K, M), M, K)).to(dev) for K in (896, 4864)}
-        qk = {K: torch.zeros((M, (K + 63) // 64 * 64), dtype=torch.int8, device=dev) for K in (896, 4864)}
+        qk = {K: torch.zeros((M, c8[0][name].kpad), dtype=torch.int8, device=dev) for name, _, K in s8}
         sk = {K: torch.zeros(M, dtype=torch.float32, device=dev) for K in (896, 4864)}
         for K in (896, 4864):
             bh.prep_rows(xk[K], qk[K], sk[K], 0, 1.0)

@@ -33,7 +33,7 @@ struct Geo<kI4, UD> {
 };
 template <int UD>
 struct Geo<kI8, UD> {
-    static constexpr int SB = 16, SC = 64, NMF = 2, SHIFT = 0;
+    static constexpr int SB = 32, SC = 128, NMF = 4, SHIFT = 0;
 };
 
 template <int N>
@@ -90,8 +90,8 @@ EIF_DEV void decode(const uint32_t (&w)[Geo<FMT, UD>::SB / 4], long (&b)[Geo<FMT
 #pragma unroll
         for (int t = 0; t < 4; ++t) b[t] = pack2(w[t] & 0xF0F0F0F0u, (w[t] << 4) & 0xF0F0F0F0u);
     } else {
-        b[0] = pack2(w[0], w[1]);
-        b[1] = pack2(w[2], w[3]);
+#pragma unroll
+        for (int i = 0; i < Geo<FMT, UD>::NMF; ++i) b[i] = pack2(w[2 * i], w[2 * i + 1]);
     }
 }
 

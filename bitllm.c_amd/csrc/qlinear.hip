@@ -18,7 +18,8 @@
 //   int4: steps of 128 columns, 4 slots x 4 dwords; dword t of slot s, byte b: high nibble = column
 //     128*step + 32*s + 8*t + b, low nibble = that column + 4; nibbles hold v & 15 (two's complement), decoded
 //     as (dword & 0xF0F0F0F0) and ((dword << 4) & 0xF0F0F0F0) = 16*v.
-//   int8: the reference row-major layout, rows padded; steps of 64 columns, slot s owns bytes 16s..16s+15.
+//   int8: the reference row-major layout, rows padded; steps of 128 columns, slot s owns bytes 32s..32s+31 (two
+//     64-deep MFMA operands per lane and step, so a K step of the GEMM carries as many MFMAs as INT4's).
 //   Every layout pads rows to a multiple of 64 and columns to a whole number of steps with zero weights.
 //
 // Accumulation contract (reference: src/eif_quantize_bitnet.c:1143-1203 for the row-scaled epilogue,
@@ -1894,7 +1895,7 @@ int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, i
         sc_count = group > 0 ? rows * q.ngroups : rows;
     } else if (fmt == kI4 || fmt == kI8) {
         if (group != 0) return EIF_HIP_E_ARG;
-        q.kpad = eif_round_up(cols, fmt == kI4 ? 128 : 64);
+        q.kpad = eif_round_up(cols, 128);
         q.wld = fmt == kI4 ? q.kpad / 2 : q.kpad;
         src_bytes = fmt == kI4 ? (size_t)rows * ((cols + 1) / 2) : (size_t)rows * cols;
         sc_count = rows;
@@ -1902,7 +1903,7 @@ int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, i
         return EIF_HIP_E_ARG;
     }
     if (fmt == kTern && group > 0 && !scales) return EIF_HIP_E_ARG;
-    q.nsteps = q.kpad / (fmt == kTern ? 64 * q.ud : (fmt == kI4 ? 128 : 64));
+    q.nsteps = q.kpad / (fmt == kTern ? 64 * q.ud : 128);
     const size_t wbytes = (size_t)q.rows_pad * q.wld;
 
     void *src_dev = nullptr;
