@@ -17,7 +17,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -103,6 +105,11 @@ struct ThreadCtx {
     hipStream_t st = nullptr;
     void *buf[8] = {};
     size_t cap[8] = {};
+    // pinned host bounce buffers of the uploads (per slot) and of the download: a copy from or to pageable memory
+    // would otherwise be staged by the runtime on every call
+    void *pin[9] = {};
+    size_t pcap[9] = {};
+    bool pending = false;   // an upload from a pinned buffer may still be in flight (no download has synced since)
 };
 thread_local ThreadCtx t_ctx;
 
@@ -132,18 +139,68 @@ void *slot(ThreadCtx &c, int i, size_t bytes, const char *fn)
     return c.buf[i];
 }
 
+// Pinned bounce buffer i (0..7 uploads, 8 the download) of at least `bytes`, or nullptr above kPinMax (the copy then
+// goes from the caller's memory directly). Grown buffers are freed after the stream has drained.
+constexpr size_t kPinMax = (size_t)4 << 20;
+
+void *pinned(ThreadCtx &c, int i, size_t bytes, const char *fn)
+{
+    if (bytes > kPinMax) return nullptr;
+    if (c.pcap[i] < bytes) {
+        if (c.pin[i]) {
+            DIE_ON(hipStreamSynchronize(c.st), fn);
+            c.pending = false;
+            DIE_ON(hipHostFree(c.pin[i]), fn);
+            c.pin[i] = nullptr;
+            c.pcap[i] = 0;
+        }
+        const size_t cap = std::max<size_t>(bytes + bytes / 4, 4096);
+        DIE_ON(hipHostMalloc(&c.pin[i], cap, hipHostMallocDefault), fn);
+        c.pcap[i] = cap;
+    }
+    return c.pin[i];
+}
+
 void *upload(ThreadCtx &c, int i, const void *host, size_t bytes, const char *fn)
 {
     if (!host) return nullptr;
     void *d = slot(c, i, bytes, fn);
-    DIE_ON(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, c.st), fn);
+    if (c.pending) {   // a call that returned before its download: its copies may still read the pinned buffers
+        DIE_ON(hipStreamSynchronize(c.st), fn);
+        c.pending = false;
+    }
+    void *p = pinned(c, i, bytes, fn);
+    if (p) {
+        std::memcpy(p, host, bytes);
+        DIE_ON(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, c.st), fn);
+        c.pending = true;
+    } else {
+        DIE_ON(hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, c.st), fn);
+    }
     return d;
+}
+
+// A kernel's output buffer: the pinned download buffer itself (the device writes it over PCIe, so no copy follows
+// the kernel), or device slot i above kPinMax.
+void *out_slot(ThreadCtx &c, int i, size_t bytes, const char *fn)
+{
+    void *p = pinned(c, 8, bytes, fn);
+    return p ? p : slot(c, i, bytes, fn);
 }
 
 void download_sync(ThreadCtx &c, void *host, const void *dev, size_t bytes, const char *fn)
 {
-    DIE_ON(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, c.st), fn);
+    if (dev == c.pin[8]) {   // written in place by the kernel
+        DIE_ON(hipStreamSynchronize(c.st), fn);
+        c.pending = false;
+        std::memcpy(host, dev, bytes);
+        return;
+    }
+    void *p = pinned(c, 8, bytes, fn);
+    DIE_ON(hipMemcpyAsync(p ? p : host, dev, bytes, hipMemcpyDeviceToHost, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
+    c.pending = false;
+    if (p) std::memcpy(host, p, bytes);
 }
 
 // ---- resident weights ----
@@ -527,7 +584,7 @@ static void i8xternary(const char *fn, const uint8_t *w, const float *scales, co
     }
     const float *dsc = (const float *)upload(c, 3, scales, sizeof(float) * rows, fn);
     const float *db = (const float *)upload(c, 4, bias, sizeof(float) * rows, fn);
-    float *dy = (float *)slot(c, 5, sizeof(float) * rows, fn);
+    float *dy = (float *)out_slot(c, 5, sizeof(float) * rows, fn);
     DIE_RC(eif::qlinear_scaled(q, dsc, dq, kpad, dxs, db, dy, rows, 1, EIF_HIP_PATH_GEMV, c.st), fn);
     download_sync(c, out, dy, sizeof(float) * rows, fn);
     if (xq_host) DIE_ON(hipStreamSynchronize(c.st), fn);
@@ -560,7 +617,7 @@ void eif_matmul_bitnet_int8(const uint8_t *weights, float scale_w, const int8_t 
     const uint8_t *dw = (const uint8_t *)resident_raw(weights, (size_t)rows * ((cols + 3) / 4), fn);
     const int8_t *dx = (const int8_t *)upload(c, 0, input, (size_t)cols, fn);
     const int32_t *db = (const int32_t *)upload(c, 1, bias, sizeof(int32_t) * rows, fn);
-    int8_t *dy = (int8_t *)slot(c, 2, (size_t)rows, fn);
+    int8_t *dy = (int8_t *)out_slot(c, 2, (size_t)rows, fn);
     DIE_RC(eif::launch_tern_int8_out(dw, dx, db, dy, eff, rows, cols, c.st), fn);
     download_sync(c, output, dy, (size_t)rows, fn);
 } catch (const HostError &) {}
@@ -579,7 +636,7 @@ static void tern_f32(const char *fn, const uint8_t *w, size_t wbytes, const floa
     const float *dsc = tiles && mode && scales ? (const float *)resident_block_scales(scales, rows, cols, block, fn)
                                                : (const float *)upload(c, 1, scales, sizeof(float) * nsc, fn);
     const float *db = (const float *)upload(c, 2, bias, sizeof(float) * rows, fn);
-    float *dy = (float *)slot(c, 3, sizeof(float) * rows, fn);
+    float *dy = (float *)out_slot(c, 3, sizeof(float) * rows, fn);
     if (tiles)
         DIE_RC(eif::launch_f32_tiles(eif::kF32Tern, dw, dsc, mode ? block : 0, dx, db, dy, rows, cols, c.st), fn);
     else
@@ -651,7 +708,7 @@ void eif_matmul_bitnet_dense_f32(const uint8_t *weights, const float *scales, co
     const float *dx = (const float *)upload(c, 0, input, sizeof(float) * cols, fn);
     const float *dsc = (const float *)upload(c, 1, scales, sizeof(float) * rows, fn);
     const float *db = (const float *)upload(c, 2, bias, sizeof(float) * rows, fn);
-    float *dy = (float *)slot(c, 3, sizeof(float) * rows, fn);
+    float *dy = (float *)out_slot(c, 3, sizeof(float) * rows, fn);
     if (tiles)
         DIE_RC(eif::launch_f32_tiles(eif::kF32Tern, dw, dsc, 0, dx, db, dy, rows, cols, c.st), fn);
     else
@@ -672,7 +729,7 @@ static void int_f32(const char *fn, bool int4, const void *w, const float *sc, c
                            : resident_raw(w, wb, fn);
     const float *dx = (const float *)upload(c, 0, x, sizeof(float) * cols, fn);
     const float *dsc = (const float *)upload(c, 1, sc, sizeof(float) * rows, fn);
-    float *dy = (float *)slot(c, 2, sizeof(float) * rows, fn);
+    float *dy = (float *)out_slot(c, 2, sizeof(float) * rows, fn);
     if (tiles)
         DIE_RC(eif::launch_f32_tiles(int4 ? eif::kF32Int4 : eif::kF32Int8, dw, dsc, 0, dx, nullptr, dy, rows, cols, c.st),
                fn);
