@@ -127,7 +127,7 @@ def traffic_from_dbs(fetch_db, write_db):
                      "write_kib": round(w["kib"], 1), "kernel": f["kernel"], "dispatches": f["dispatches"]}
     rec = {"workload": "bitnet2b_layer_linears_m1", "kernel": "qgemv_kernel (prep fused, ternary int8-MFMA GEMV)",
            "source_sha256": source_hash(),
-           "commands": [f"rocprofv3 --pmc {c} -d gpurun_out/prof_{c.lower()} -o run -- python3 bench.py --no-cpu "
+           "commands": [f"rocprofv3 --pmc {c} -d prof_{c.lower()} -o run -- python3 bench.py --no-cpu "
                         f"--no-extra --no-decode --steps 20 --warmup 2 --calib-copy-mib 256" for c in
                         ("FETCH_SIZE", "WRITE_SIZE")] +
                        [f"python3 bench.py --traffic-from {fetch_db} {write_db}"],
