@@ -382,3 +382,26 @@ def test_weight_cache_bound(lib, oracle):
         lib.eif_hip_set_host_weight_cache_limit(old)
         lib.eif_hip_forget_host_weights(None)
     assert lib.eif_hip_host_weight_cache_bytes() == 0
+
+
+def test_host_api_beyond_pinned_buffers(lib, oracle):
+    """Inputs and outputs above the 4 MiB of a thread's pinned bounce buffers are copied from and to the caller's
+    memory directly; calls before and after them go through the pinned buffers. Every result against the oracle:
+    an INT8 row-scaled GEMV with a 4.4 MB activation row (3 x 1,100,000) and one with a 4.4 MB output
+    (1,100,000 x 16), between two small ones."""
+    def run(rows, cols, key):
+        w = synth.rng(90, key).integers(-127, 128, size=(rows, cols), dtype=np.int8)
+        s = (np.abs(synth.rng(91, key).standard_normal(rows)) * 0.01).astype(np.float32)
+        x = synth.rng(92, key).standard_normal(cols).astype(np.float32)
+        y = np.full(rows, np.nan, np.float32)
+        lib.tinyllm_matmul_int8_rowscale(P(y), P(w), P(x), cols, rows, P(s))
+        o = np.zeros(rows, np.float32)
+        oracle.orc_int8_rowscale_f32(P(o), P(w), P(x), cols, rows, P(s))
+        mag = (np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))) * s
+        assert np.all(np.isfinite(y)) and within(y, o, mag), (rows, cols)
+        lib.eif_hip_forget_host_weights(P(w))
+    run(64, 896, 1)
+    run(3, 1_100_000, 2)     # x: 4.4 MB
+    run(64, 896, 3)
+    run(1_100_000, 16, 4)    # y: 4.4 MB
+    run(64, 896, 5)
