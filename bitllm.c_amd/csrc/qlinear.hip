@@ -786,7 +786,9 @@ __global__ __launch_bounds__(kStreamThreads) void qstream_kernel(QArgs a, int nt
 // (half 0 the even row) x P passes, all its loads issued first. Each lane's sums of its 8 row pairs are summed
 // over the half-wave by a transposed reduction (xor 16, 8, 4 exchanging half the values each time, then xor
 // 2, 1), which leaves the sum of row pair (h >> 2) on the four lanes of each quad. The int32 sums are exact, so
-// y has the MFMA GEMV's bits: ((float)isum * xs) * s[r] (+ bias); the per-tile maxima too.
+// y has the MFMA GEMV's bits: ((float)isum * xs) * s[r] (+ bias); the per-tile maxima too. The codes are read
+// once each, in whole-line runs, with non-temporal loads: the INT4 151936x1024 head 15.3 -> 13.4 us, the INT8
+// 128256x2560 head 54.8 -> 48.0 us against plain loads (the streaming GEMV's 16-row pattern lost with them).
 constexpr int kRowPairThreads = 256;
 // Passes of 512 bytes per row it is compiled for (32 registers of codes per pass, plus 8 (INT4) or 4 (INT8) of
 // activations): INT4 K up to 4096, INT8 K up to 2560.
@@ -809,7 +811,10 @@ __global__ __launch_bounds__(kRowPairThreads) void qrowpair_kernel(QArgs a, int 
 #pragma unroll
     for (int c = 0; c < 8; ++c)
 #pragma unroll
-        for (int q = 0; q < P; ++q) wv[c][q] = *reinterpret_cast<const uint4 *>(wp + (size_t)(2 * c) * a.wld + 512 * q);
+        for (int q = 0; q < P; ++q) {
+            const v4i t = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wp + (size_t)(2 * c) * a.wld + 512 * q));
+            wv[c][q] = make_uint4((uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z, (uint32_t)t.w);
+        }
     uint4 xv[P][CB / 16];
 #pragma unroll
     for (int q = 0; q < P; ++q)
@@ -1351,6 +1356,7 @@ int launch_gemv_m(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
     return launch_gemv_tiles<FMT, UD, GROUPED, ACC>(a, p, rows_pad, 1, st);
 }
 
+int g_gemv_rowpair = 0;   // 0 = vocabulary-sized matrices, 1 = every shape it takes, -1 = off
 int g_gemv_stream = 0;   // streaming GEMV: waves per CU (0 = the default, -1 = off)
 constexpr int kStreamWavesPerCU = 8;
 
@@ -1390,7 +1396,6 @@ int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t s
 // The row-pair GEMV: row-scaled INT4 / INT8 matrices at one prepped token row whose rows are whole 512-byte runs
 // (at most rowpair_max_p of them); by default only vocabulary-sized ones (kBigTiles tiles or more), where
 // bandwidth decides. Returns 1 for other shapes.
-int g_gemv_rowpair = 0;   // 0 = vocabulary-sized matrices, 1 = every shape it takes, -1 = off
 
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
@@ -1404,19 +1409,21 @@ int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t 
         const int grid = eif_ceil_div(ntiles, kRowPairThreads / 64);
         constexpr int PM = rowpair_max_p<FMT>();
         static_assert(PM <= 5, "one case per pass count");
+#define EIF_RP(PP) qrowpair_kernel<FMT, PP, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles)
         switch (a.wld / 512) {
-        case 1: qrowpair_kernel<FMT, 1, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
-        case 2: qrowpair_kernel<FMT, 2, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
-        case 3: qrowpair_kernel<FMT, 3, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
-        case 4: qrowpair_kernel<FMT, 4, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles); break;
+        case 1: EIF_RP(1); break;
+        case 2: EIF_RP(2); break;
+        case 3: EIF_RP(3); break;
+        case 4: EIF_RP(4); break;
         case 5:
             if constexpr (PM >= 5) {
-                qrowpair_kernel<FMT, PM >= 5 ? 5 : 1, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles);
+                EIF_RP(PM >= 5 ? 5 : 1);
                 break;
             }
             return 1;
         default: return 1;
         }
+#undef EIF_RP
         EIF_HIP_LAUNCHED();
         return EIF_HIP_OK;
     }
