@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <memory>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -73,11 +74,18 @@ DevState &dev_state()
 std::atomic<int> g_host_err_mode{EIF_HIP_HOST_ABORT};
 thread_local int t_err_code = EIF_HIP_OK;
 thread_local char t_err_msg[256];
+thread_local int t_force_record = 0;   // > 0: record whatever the global mode (the GPU seat's bool contract)
 struct HostError {};
+
+// Record mode for the calling thread while it lives, whatever eif_hip_set_host_error_mode says.
+struct ForceRecord {
+    ForceRecord() { ++t_force_record; }
+    ~ForceRecord() { --t_force_record; }
+};
 
 [[noreturn]] void die(const char *fn, const char *what)
 {
-    if (g_host_err_mode.load(std::memory_order_relaxed) == EIF_HIP_HOST_RECORD) {
+    if (t_force_record > 0 || g_host_err_mode.load(std::memory_order_relaxed) == EIF_HIP_HOST_RECORD) {
         t_err_code = EIF_HIP_E_DEVICE;
         snprintf(t_err_msg, sizeof t_err_msg, "%s: %s", fn, what);
         throw HostError{};
@@ -124,6 +132,37 @@ ThreadCtx &ctx(const char *fn)
     return t_ctx;
 }
 
+// The calling thread's context at the start of a host-ABI call. A previous call that ended before its download
+// (an error in record mode) may still have copies in flight from the pinned buffers, so the stream is drained
+// once here. The uploads of one call use distinct pinned buffers, so they never wait for each other.
+ThreadCtx &call_ctx(const char *fn)
+{
+    ThreadCtx &c = ctx(fn);
+    if (c.pending) {
+        DIE_ON(hipStreamSynchronize(c.st), fn);
+        c.pending = false;
+    }
+    return c;
+}
+
+// Device memory owned until released: frees itself on the error paths of record mode (die() throws).
+struct DevBuf {
+    void *p = nullptr;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    ~DevBuf()
+    {
+        if (p) (void)hipFree(p);
+    }
+    void *release()
+    {
+        void *q = p;
+        p = nullptr;
+        return q;
+    }
+};
+
 void *slot(ThreadCtx &c, int i, size_t bytes, const char *fn)
 {
     if (bytes == 0) bytes = 16;
@@ -165,10 +204,6 @@ void *upload(ThreadCtx &c, int i, const void *host, size_t bytes, const char *fn
 {
     if (!host) return nullptr;
     void *d = slot(c, i, bytes, fn);
-    if (c.pending) {   // a call that returned before its download: its copies may still read the pinned buffers
-        DIE_ON(hipStreamSynchronize(c.st), fn);
-        c.pending = false;
-    }
     void *p = pinned(c, i, bytes, fn);
     if (p) {
         std::memcpy(p, host, bytes);
@@ -304,9 +339,11 @@ const void *resident_raw(const void *host, size_t n, const char *fn)
     WEntry e;
     e.bytes = n ? n : 16;
     make_room(e.bytes);
-    DIE_ON(hipMalloc(&e.raw, e.bytes), fn);
-    DIE_ON(hipMemcpyAsync(e.raw, host, n, hipMemcpyHostToDevice, c.st), fn);
+    DevBuf raw;
+    DIE_ON(hipMalloc(&raw.p, e.bytes), fn);
+    DIE_ON(hipMemcpyAsync(raw.p, host, n, hipMemcpyHostToDevice, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
+    e.raw = raw.release();
     return insert(k, e).raw;
 }
 
@@ -323,13 +360,14 @@ const void *resident_tiles(const void *host, size_t n, int src_fmt, int rows, in
     WEntry e;
     e.bytes = eif::f32_tiles_bytes(fmt, rows, cols);
     make_room(e.bytes + n);
-    void *tmp = nullptr;
-    DIE_ON(hipMalloc(&tmp, n ? n : 16), fn);
-    DIE_ON(hipMalloc(&e.raw, e.bytes), fn);
-    DIE_ON(hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, c.st), fn);
-    DIE_RC(eif::launch_f32_repack(src_fmt, (const uint8_t *)tmp, e.raw, rows, cols, c.st), fn);
+    DevBuf tmp, raw;
+    DIE_ON(hipMalloc(&tmp.p, n ? n : 16), fn);
+    DIE_ON(hipMalloc(&raw.p, e.bytes), fn);
+    DIE_ON(hipMemcpyAsync(tmp.p, host, n, hipMemcpyHostToDevice, c.st), fn);
+    DIE_RC(eif::launch_f32_repack(src_fmt, (const uint8_t *)tmp.p, raw.p, rows, cols, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
-    DIE_ON(hipFree(tmp), fn);
+    DIE_ON(hipFree(tmp.release()), fn);
+    e.raw = raw.release();
     return insert(k, e).raw;
 }
 
@@ -345,13 +383,14 @@ const void *resident_block_scales(const float *host, int rows, int cols, int blo
     WEntry e;
     e.bytes = eif::f32_scales_bytes(rows, cols, block);
     make_room(e.bytes + n);
-    void *tmp = nullptr;
-    DIE_ON(hipMalloc(&tmp, n), fn);
-    DIE_ON(hipMalloc(&e.raw, e.bytes), fn);
-    DIE_ON(hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, c.st), fn);
-    DIE_RC(eif::launch_f32_scales((const float *)tmp, e.raw, rows, cols, block, c.st), fn);
+    DevBuf tmp, raw;
+    DIE_ON(hipMalloc(&tmp.p, n), fn);
+    DIE_ON(hipMalloc(&raw.p, e.bytes), fn);
+    DIE_ON(hipMemcpyAsync(tmp.p, host, n, hipMemcpyHostToDevice, c.st), fn);
+    DIE_RC(eif::launch_f32_scales((const float *)tmp.p, raw.p, rows, cols, block, c.st), fn);
     DIE_ON(hipStreamSynchronize(c.st), fn);
-    DIE_ON(hipFree(tmp), fn);
+    DIE_ON(hipFree(tmp.release()), fn);
+    e.raw = raw.release();
     return insert(k, e).raw;
 }
 
@@ -365,11 +404,16 @@ const eif_hip_qweight *resident_tern_row(const uint8_t *host, int rows, int cols
     if (it != g_wcache.end()) return pin(k, it->second).q;
     WEntry e;
     make_room(n + n / 8);   // the GPU layout is about the reference's size
-    DIE_RC(eif_hip_qweight_create(&e.q, EIF_HIP_W_TERNARY, rows, cols, 0, host, nullptr, 0, c.st), fn);
+    eif_hip_qweight *q = nullptr;
+    DIE_RC(eif_hip_qweight_create(&q, EIF_HIP_W_TERNARY, rows, cols, 0, host, nullptr, 0, c.st), fn);
+    std::unique_ptr<eif_hip_qweight, void (*)(eif_hip_qweight *)> own(q, eif_hip_qweight_destroy);
     size_t qb = 0;
-    eif_hip_qweight_info(e.q, nullptr, nullptr, nullptr, nullptr, &qb);
+    eif_hip_qweight_info(q, nullptr, nullptr, nullptr, nullptr, &qb);
     e.bytes = qb;
-    return insert(k, e).q;
+    e.q = q;
+    WEntry &ins = insert(k, e);
+    own.release();
+    return ins.q;
 }
 
 float norm_fastmath(int block)
@@ -537,7 +581,7 @@ void eif_hadamard_rotate_f32(float *x, const float *signs, int n, int block) try
 {
     static const char *fn = "eif_hadamard_rotate_f32";
     if (!x || block <= 0 || n % block != 0 || !pow2(block)) return;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     float *dx = (float *)upload(c, 0, x, sizeof(float) * n, fn);
     const float *ds = (const float *)upload(c, 1, signs, sizeof(float) * n, fn);
     DIE_RC(eif::launch_rotate_rows(dx, n, ds, 1, n, block, eif_hip_wht_norm(block), c.st), fn);
@@ -551,7 +595,7 @@ void eif_quantize_activation_i8(const float *x_f32, int8_t *x_i8, float *out_sca
         if (out_scale) *out_scale = 1.0f;
         return;
     }
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     const float *dx = (const float *)upload(c, 0, x_f32, sizeof(float) * n, fn);
     int8_t *dq = (int8_t *)slot(c, 1, (size_t)n, fn);
     float *ds = (float *)slot(c, 2, sizeof(float), fn);
@@ -568,7 +612,7 @@ static void i8xternary(const char *fn, const uint8_t *w, const float *scales, co
                        const float *x_host, float scale_in, const float *bias, float *out, int rows, int cols)
 {
     PinScope pins;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     const eif_hip_qweight *q = resident_tern_row(w, rows, cols, fn);
     int kpad = 0;
     eif_hip_qweight_info(q, nullptr, nullptr, &kpad, nullptr, nullptr);
@@ -612,7 +656,7 @@ void eif_matmul_bitnet_int8(const uint8_t *weights, float scale_w, const int8_t 
     static const char *fn = "eif_matmul_bitnet_int8";
     PinScope pins;
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     const float eff = (scale_w * scale_in) / (scale_out > 1e-12f ? scale_out : 1.0f);
     const uint8_t *dw = (const uint8_t *)resident_raw(weights, (size_t)rows * ((cols + 3) / 4), fn);
     const int8_t *dx = (const int8_t *)upload(c, 0, input, (size_t)cols, fn);
@@ -628,7 +672,7 @@ static void tern_f32(const char *fn, const uint8_t *w, size_t wbytes, const floa
                      int block, const float *x, const float *bias, float *out, int rows, int cols, int il)
 {
     PinScope pins;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     const bool tiles = eif::f32_tiles_fit(cols, mode ? block : 0);
     const void *dw = tiles ? resident_tiles(w, wbytes, il ? eif::kSrcTernIl : eif::kSrcTernRow, rows, cols, fn)
                            : resident_raw(w, wbytes, fn);
@@ -657,6 +701,7 @@ bool eif_gpu_matmul_bitnet_f32(eif_gpu_context_t *ctx, const uint8_t *weights, c
 {
     (void)ctx;
     if (!weights || !input || !output || rows <= 0 || cols <= 0 || !dev_state().ok) return false;
+    ForceRecord rec;   // a failure returns false (the caller runs its CPU kernel), never aborts
     tern_f32("eif_gpu_matmul_bitnet_f32", weights, (size_t)rows * ((cols + 3) / 4), scales, (size_t)rows, 0, 0,
              input, bias, output, rows, cols, 0);
     return true;
@@ -701,7 +746,7 @@ void eif_matmul_bitnet_dense_f32(const uint8_t *weights, const float *scales, co
     static const char *fn = "eif_matmul_bitnet_dense_f32";
     PinScope pins;
     if (!weights || !input || !output || rows <= 0 || cols <= 0) return;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     const size_t wb = (size_t)rows * ((cols + 4) / 5);
     const bool tiles = eif::f32_tiles_fit(cols, 0);
     const void *dw = tiles ? resident_tiles(weights, wb, eif::kSrcDense, rows, cols, fn) : resident_raw(weights, wb, fn);
@@ -722,7 +767,7 @@ static void int_f32(const char *fn, bool int4, const void *w, const float *sc, c
                     int cols)
 {
     PinScope pins;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     const size_t wb = int4 ? (size_t)rows * ((cols + 1) / 2) : (size_t)rows * cols;
     const bool tiles = eif::f32_tiles_fit(cols, 0);
     const void *dw = tiles ? resident_tiles(w, wb, int4 ? eif::kSrcInt4 : eif::kSrcInt8, rows, cols, fn)
@@ -767,7 +812,7 @@ void eif_gemm_f32_nt_ld(const float *A, int lda, const float *W, int ldw, const 
     static const char *fn = "eif_gemm_f32_nt_ld";
     if (M <= 0 || N <= 0 || !C) return;
     if (K > 0 && (!A || !W)) return;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     float *dA = nullptr, *dW = nullptr;
     if (K > 0) {
         dA = (float *)slot(c, 0, sizeof(float) * (size_t)M * K, fn);
@@ -798,7 +843,7 @@ void eif_softmax_rows_f32(float *S, int rows, int cols, int ld, float scale) try
 {
     static const char *fn = "eif_softmax_rows_f32";
     if (!S || rows <= 0 || cols <= 0 || ld < cols) return;
-    ThreadCtx &c = ctx(fn);
+    ThreadCtx &c = call_ctx(fn);
     float *dS = (float *)slot(c, 0, sizeof(float) * (size_t)rows * cols, fn);
     DIE_ON(hipMemcpy2DAsync(dS, sizeof(float) * cols, S, sizeof(float) * ld, sizeof(float) * cols, rows,
                             hipMemcpyHostToDevice, c.st), fn);

@@ -601,6 +601,17 @@ int persist_create(PersistPlan **out, const PersistModel &pm)
         persist_destroy(p);
         return EIF_HIP_E_DEVICE;
     }
+    // the grid barriers need every workgroup resident at once: one 1024-thread workgroup with this LDS must fit
+    // on a CU (what other streams hold at run time is caught by the barriers' bounded spin instead)
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kPT, (size_t)lds) != hipSuccess) {
+        persist_destroy(p);
+        return EIF_HIP_E_DEVICE;
+    }
+    if (per_cu < 1) {
+        persist_destroy(p);
+        return EIF_HIP_E_LIMIT;
+    }
     a.layers = p->layers;
     a.n_layers = pm.n_layers, a.dim = pm.dim, a.hidden = pm.hidden, a.q_dim = pm.q_dim, a.kv_dim = pm.kv_dim;
     a.n_heads = pm.n_heads, a.n_kv = pm.n_kv, a.seq_len = pm.seq_len;

@@ -30,7 +30,9 @@ typedef struct {
 /* output[r] = scales[r] * sum_c W[r][c] input[c] + bias[r] (scales NULL = 1, bias NULL = 0), W in the 2-bit
  * row-major format of eif_matmul_bitnet_f32, all pointers host memory. ctx is not read (it may be NULL).
  * Returns true when the GPU computed the output, and false when the caller must run its CPU kernel: no usable
- * gfx950 device, or invalid sizes. The weights stay resident, as for eif_matmul_bitnet_f32.
+ * gfx950 device, invalid sizes, or a HIP error during the call. The call never aborts, whatever
+ * eif_hip_set_host_error_mode says: a failure is recorded for the calling thread (eif_hip_host_last_error) and
+ * false returned. The weights stay resident, as for eif_matmul_bitnet_f32.
  *                                                                        ref: include/eif_gpu.h:55-70 */
 bool eif_gpu_matmul_bitnet_f32(eif_gpu_context_t *ctx, const uint8_t *weights, const float *scales,
                                const float *input, const float *bias, float *output, int rows, int cols);

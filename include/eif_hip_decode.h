@@ -85,9 +85,11 @@ int eif_hip_bitnet_reset(eif_hip_bitnet *m, const int *prompt, int n_prompt, voi
  * kernel, whose weights are already in LDS, waits for it and for a grid barrier of about 1.8 us per stage.
  * Shapes outside the persistent kernel (head_dim other than 128, row-scaled ternary matrices, ...) always take
  * the separate launches. on = -1 only queries. Returns 1 when steps run persistent, 0 when not, or a negative
- * error (all layers and the globals must be set). A persistent step that gives up waiting at a grid barrier (all
- * workgroups could not run at once) makes the next eif_hip_bitnet_tokens / _logits / _position return
- * EIF_HIP_E_DEVICE.                                                                                     */
+ * error (all layers and the globals must be set); EIF_HIP_E_LIMIT when one workgroup of the kernel cannot be
+ * resident on a CU. A persistent step that gives up waiting at a grid barrier (all workgroups could not run at
+ * once, e.g. other work held CUs) makes the next eif_hip_bitnet_tokens / _logits / _position return
+ * EIF_HIP_E_DEVICE; its position, KV cache and tokens are then undefined, and eif_hip_bitnet_reset must be
+ * called before the model is used again.                                                                */
 int eif_hip_bitnet_set_persistent(eif_hip_bitnet *m, int on);
 
 /* Runs n token steps from the current position. The step at position p consumes the current token and

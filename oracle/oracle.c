@@ -20,6 +20,9 @@
  *   orc_*_acc_i32                       int64 numpy brute force (exact), KAT 4x8 of test_all_features.c:104-186
  *   orc_matmul_bitnet_i8xternary_f32    bit-exact vs compiled reference
  *   orc_matmul_bitnet_int8              bit-exact vs compiled reference
+ *   orc_int8/int4_gemv_i8act            int32 sums vs int64 brute force; FP32 outputs within 1e-6 of the float64
+ *                                       closed form acc*xs[m]*s[r] + bias[r] (normalised by |acc|*xs*s + |bias|),
+ *                                       a planted xs / scale-index / bias-order mistake failing it
  *   FP32-activation GEMVs, GEMM, softmax  float64 references with the reference tests' bounds
  *                                       (test_int8_gemv.c:10-44, test_q35_int4.c:24-33, test_gemm.c:9-34)
  *   orc_quant_rows                      numpy float32 restatement, nibble order of test_q35_int4.c:20,
@@ -355,13 +358,31 @@ void orc_int4_acc_i32(const uint8_t *w, const int8_t *xq, int ldq, int M, int ro
         }
 }
 
+/* Row-scaled FP32 epilogue of the INT8 / INT4 linears on INT8 activations:
+ * y = ((float)isum * xs[m]) * s[r] + bias[r]: the int32 sum times the activation scale, then the row scale, the
+ * order of the reference's INT8-activation INT4 GEMV (src/eif_qwen35.c:221-224, aarch64), then the bias. The
+ * x86 reference has no INT8-activation INT8/INT4 kernel, so these bits are this library's contract; the float64
+ * closed form pins them (tests/test_oracle_pins.py).
+ * ORC_PLANT_ROWSCALE (tests only, default 0) plants one mistake so the closed-form pin can be shown to catch it:
+ * 1 = xs[0] for every token, 2 = the row scale indexed by token, 3 = the bias added before the xs multiply. */
+#ifndef ORC_PLANT_ROWSCALE
+#define ORC_PLANT_ROWSCALE 0
+#endif
 static void rowscale_epilogue(const int32_t *acc, const float *scales, const float *xs, const float *bias,
                               float *y, int ldy, int M, int rows)
 {
     for (int m = 0; m < M; m++)
         for (int r = 0; r < rows; r++) {
-            float v = ((float)acc[(size_t)m * rows + r] * xs[m]) * (scales ? scales[r] : 1.0f);
-            if (bias) v = v + bias[r];
+            const float xsm = ORC_PLANT_ROWSCALE == 1 ? xs[0] : xs[m];
+            const int si = ORC_PLANT_ROWSCALE == 2 ? m : r;
+            const float b = bias ? bias[r] : 0.0f;
+            float v;
+            if (ORC_PLANT_ROWSCALE == 3) {
+                v = (((float)acc[(size_t)m * rows + r] + b) * xsm) * (scales ? scales[si] : 1.0f);
+            } else {
+                v = ((float)acc[(size_t)m * rows + r] * xsm) * (scales ? scales[si] : 1.0f);
+                if (bias) v = v + b;
+            }
             y[(size_t)m * ldy + r] = v;
         }
 }

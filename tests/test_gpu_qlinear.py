@@ -1,12 +1,13 @@
 """INT8-activation linears (MFMA GEMV and GEMM paths) against the oracle.
 
 Integer accumulators are compared bit for bit; row-scaled outputs bit for bit (same epilogue order as the
-reference build); group-scaled FP32 outputs to 1e-5 relative to sum_g |s*acc_g|*xs + |bias| and, since the
+reference build) and, for INT8 / INT4, within 1e-6 of the float64 closed form acc * xs[m] * s[r] + bias[r]; group-scaled FP32 outputs to 1e-5 relative to sum_g |s*acc_g|*xs + |bias| and, since the
 kernels combine a row's groups in group order as the oracle does, bit for bit.
 """
 import numpy as np
 import pytest
 
+import closed_form as cf
 from conftest import P
 import synth
 
@@ -257,17 +258,22 @@ def test_int_rowscale_bit_exact(gpu, oracle, fmt, N, K, M, path):
     xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
     acc = run_acc(gpu, qw, xq_d, M, (M, N), path)
     assert np.array_equal(acc, xq[:, :K].astype(np.int64) @ vals.astype(np.int64).T)
-    y = run_linear(gpu, qw, xq_d, xs_d, M, path)
-    oy = np.zeros((M, N), np.float32)
     fn = oracle.orc_int8_gemv_i8act if fmt == "int8" else oracle.orc_int4_gemv_i8act
-    fn(P(w), P(s), P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
-    assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
+    bias = synth.rng(45, N).standard_normal(N).astype(np.float32)
+    exact = acc.astype(np.float64)
+    for b in (None, bias):
+        y = run_linear(gpu, qw, xq_d, xs_d, M, path, bias=b)
+        oy = np.zeros((M, N), np.float32)
+        fn(P(w), P(s), P(xq), qw.kpad, P(xs), P(b), P(oy), N, M, N, K)
+        assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
+        # the FP32 epilogue against the float64 closed form acc * xs[m] * s[r] + bias[r]
+        assert cf.rowscale_error(y, exact, xs, s, b) <= cf.ROWSCALE_TOL
     qw.close()
 
 
 def test_int4_tied_head_full_size(gpu, oracle):
     # the 151936 x 1024 INT4 head at M = 1 and 32 (GEMV) and M = 32 (GEMM): int32 sums against an exact integer
-    # product
+    # product; y (with a bias at 32 rows) bit for bit against the oracle and within 1e-6 of the float64 closed form
     N, K = synth.QWEN35_INT4_HEAD[1:]
     w, s = synth.int4_weight((49,), N, K)
     qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
@@ -278,11 +284,13 @@ def test_int4_tied_head_full_size(gpu, oracle):
         acc = run_acc(gpu, qw, xq_d, M, (M, N), path)
         exact = xq[:, :K].astype(np.float64) @ vals.T          # integer-valued, |sums| < 2^53
         assert np.array_equal(acc.astype(np.float64), exact)
-        if M > 1 and path == GEMV:
-            y = run_linear(gpu, qw, xq_d, xs_d, M, path)
-            oy = np.zeros((M, N), np.float32)
-            oracle.orc_int4_gemv_i8act(P(w), P(s), P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
-            assert np.array_equal(y.view(np.uint32), oy.view(np.uint32))
+        bias = synth.rng(51, N).standard_normal(N).astype(np.float32) if M > 1 else None
+        y = run_linear(gpu, qw, xq_d, xs_d, M, path, bias=bias)
+        oy = np.zeros((M, N), np.float32)
+        oracle.orc_int4_gemv_i8act(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+        assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (M, path)
+        # the FP32 epilogue against the float64 closed form acc * xs[m] * s[r] + bias[r]
+        assert cf.rowscale_error(y, exact, xs, s, bias) <= cf.ROWSCALE_TOL, (M, path)
     qw.close()
 
 

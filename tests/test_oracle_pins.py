@@ -4,6 +4,8 @@ Each check is chosen so that a plausible mistake fails it: the reference's known
 (tests/test_all_features.c, tests/test_bitnet_hadamard.c), closed forms (Sylvester matrix, involution, integer
 brute force in int64) and bit-for-bit agreement with the reference compiled from its own sources (oracle/_ref).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -348,6 +350,95 @@ def test_int8_int4_fp32_bounds_vs_ref(oracle, ref):
             y = np.zeros(rows, np.float32)
             fn(P(y), P(w), P(sc), P(x), rows, cols)
             assert np.max(np.abs(want - y / sc) / (1e-6 * mag * 4 + 1e-30)) <= 1.0
+
+
+# ---- a14/a15 on INT8 activations: the row-scaled FP32 epilogue ----
+
+def _int_linear(fmt, key, N, K):
+    if fmt == "int8":
+        w, s = synth.int8_weight(key, N, K)
+        return w, s, w
+    w, s = synth.int4_weight(key, N, K)
+    return w, s, synth.unpack_int4(w, K)
+
+
+def _prep(oracle, key, M, K):
+    kpad = -(-K // 128) * 128
+    x = synth.activations(key, M, K)
+    xq = np.zeros((M, kpad), np.int8)
+    xs = np.zeros(M, np.float32)
+    assert oracle.orc_prep_rows(P(x), K, None, M, K, 0, 1.0, P(xq), kpad, P(xs), None, 0) == 0
+    return xq, xs, kpad
+
+
+INT_I8ACT_SHAPES = [
+    # Qwen2.5-0.5B-like INT8 layer: gate/up, down, stacked q|k|v, at one and 128 token rows
+    ("int8", 4864, 896, 1), ("int8", 4864, 896, 128), ("int8", 896, 4864, 1), ("int8", 896, 4864, 128),
+    ("int8", 1152, 896, 1), ("int8", 1152, 896, 128),
+    # INT4 FFN linears and the 151936 x 1024 tied head, at one and 32 token rows
+    ("int4", 3584, 1024, 1), ("int4", 3584, 1024, 32), ("int4", 1024, 3584, 1), ("int4", 1024, 3584, 32),
+    ("int4", 151936, 1024, 1), ("int4", 151936, 1024, 32),
+]
+
+
+@pytest.mark.parametrize("fmt,N,K,M", INT_I8ACT_SHAPES)
+def test_int_i8act_vs_double(oracle, fmt, N, K, M):
+    # orc_int8_gemv_i8act / orc_int4_gemv_i8act (the GPU linears' FP32 contract) against the float64 closed form
+    # acc * xs[m] * s[r] + bias[r] with acc the exact integer product, per-token xs from the prep, with and
+    # without a bias, to 1e-6 of |acc| * xs * s + |bias|.
+    import closed_form as cf
+    w, s, vals = _int_linear(fmt, (70, N, K), N, K)
+    xq, xs, kpad = _prep(oracle, (71, M, K), M, K)
+    assert M == 1 or len(set(xs.tolist())) == M       # per-token scales differ, so an xs[0] mistake shows
+    bias = synth.rng(72, N).standard_normal(N).astype(np.float32)
+    acc = cf.exact_acc(xq, vals)
+    fn = oracle.orc_int8_gemv_i8act if fmt == "int8" else oracle.orc_int4_gemv_i8act
+    for b in (None, bias):
+        y = np.full((M, N), np.nan, np.float32)
+        fn(P(w), P(s), P(xq), kpad, P(xs), P(b), P(y), N, M, N, K)
+        assert cf.rowscale_error(y, acc, xs, s, b) <= cf.ROWSCALE_TOL, (fmt, N, K, M, b is not None)
+
+
+@pytest.fixture(scope="module")
+def planted_oracles(tmp_path_factory):
+    """The oracle built three more times, each with one planted mistake in its row-scaled epilogue
+    (ORC_PLANT_ROWSCALE in oracle.c: 1 = xs[0] for every token, 2 = the scale indexed by token, 3 = the bias added
+    before the xs multiply)."""
+    import shutil
+    import subprocess
+    import oracle_api
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        pytest.skip("no C compiler to build the planted oracles")
+    src = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle")
+    d = tmp_path_factory.mktemp("planted")
+    libs = {}
+    for k in (1, 2, 3):
+        so = str(d / f"liboracle_plant{k}.so")
+        subprocess.run([cc, "-std=c99", "-D_GNU_SOURCE", "-O1", "-fno-fast-math", "-ffp-contract=off", "-fPIC",
+                        "-shared", f"-DORC_PLANT_ROWSCALE={k}", "-o", so, os.path.join(src, "oracle.c"),
+                        os.path.join(src, "decode_oracle.c"), "-lm"], check=True)
+        libs[k] = oracle_api.load(so)
+    return libs
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_int_i8act_planted_mistakes_fail(oracle, planted_oracles, fmt):
+    # the closed form above rejects each planted epilogue mistake, at several token rows, with a bias
+    import closed_form as cf
+    N, K, M = 96, 640, 4
+    w, s, vals = _int_linear(fmt, (73, N, K), N, K)
+    xq, xs, kpad = _prep(oracle, (74, M, K), M, K)
+    bias = synth.rng(75, N).standard_normal(N).astype(np.float32)
+    acc = cf.exact_acc(xq, vals)
+    name = "orc_int8_gemv_i8act" if fmt == "int8" else "orc_int4_gemv_i8act"
+    y = np.zeros((M, N), np.float32)
+    getattr(oracle, name)(P(w), P(s), P(xq), kpad, P(xs), P(bias), P(y), N, M, N, K)
+    assert cf.rowscale_error(y, acc, xs, s, bias) <= cf.ROWSCALE_TOL
+    for k, lib in planted_oracles.items():
+        yb = np.zeros((M, N), np.float32)
+        getattr(lib, name)(P(w), P(s), P(xq), kpad, P(xs), P(bias), P(yb), N, M, N, K)
+        assert cf.rowscale_error(yb, acc, xs, s, bias) > 100 * cf.ROWSCALE_TOL, f"planted mistake {k} not caught"
 
 
 def test_gemm_softmax_vs_double(oracle):
