@@ -244,19 +244,27 @@ EIF_DEV void load4(const float *base, int idx, float (&v)[E])
 // pre-op, the sign flip and the zeroing past K happen in prep_finish.
 //   v: x; sg: signs; v2: x2 (SwiGLU); nw: the RMSNorm weight (operands that are absent hold x).
 template <int E, bool COH = false>
+EIF_DEV void prep_load_rows(const float *xr, const float *sgr, const float *x2r, const float *nwr, int K,
+                            float (&v)[E], float (&sg)[E], float (&v2)[E], float (&nw)[E], int tid = threadIdx.x)
+{
+    const int i0 = E * tid;
+    const int ic = i0 < K ? i0 : 0;
+    load4<E, COH>(xr, ic, v);
+    load4<E>(sgr, ic, sg);
+    load4<E, COH>(x2r, ic, v2);
+    load4<E>(nwr, ic, nw);
+}
+
+// Every load is issued, from x where an operand is absent (scalar pointer selects, no branches): a load count
+// that is the same on every path lets the compiler wait for these loads alone, behind which the weight and scale
+// loads stay in flight. prep_load_rows takes the four rows as given (a kernel's preloaded arguments).
+template <int E, bool COH = false>
 EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E], float (&v2)[E], float (&nw)[E],
                        int tid = threadIdx.x)
 {
-    // Every load is issued, from x where an operand is absent (scalar pointer selects, no branches): a load
-    // count that is the same on every path lets the compiler wait for these loads alone, behind which the
-    // weight and scale loads stay in flight.
-    const int i0 = E * tid;
-    const int ic = i0 < p.K ? i0 : 0;
     const float *xr = p.x + (size_t)m * p.ldx;
-    load4<E, COH>(xr, ic, v);
-    load4<E>(p.signs ? p.signs : xr, ic, sg);
-    load4<E, COH>(p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 + (size_t)m * p.ldx : xr, ic, v2);
-    load4<E>(p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : xr, ic, nw);
+    prep_load_rows<E, COH>(xr, p.signs ? p.signs : xr, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 + (size_t)m * p.ldx : xr,
+                           p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : xr, p.K, v, sg, v2, nw, tid);
 }
 
 // The attention shares of thread t's columns [E t, E t + E) (head h = E t / sh_hd, dims from E t % sh_hd): every
@@ -269,17 +277,25 @@ struct Shares {
 };
 
 template <int E, bool COH = false>
-EIF_DEV void prep_load_sh(const PrepArgs &p, Shares<E> &sh, float (&sg)[E], float (&nw)[E], int tid = threadIdx.x)
+EIF_DEV void prep_load_sh_rows(const float *sh_o, const float *sh_ml, const float *sgr, const float *nwr, int K,
+                               int sh_hd, Shares<E> &sh, float (&sg)[E], float (&nw)[E], int tid = threadIdx.x)
 {
     const int i0 = E * tid;
-    const int ic = i0 < p.K ? i0 : 0;
-    const int h = ic / p.sh_hd, d = ic - h * p.sh_hd;
-    load4<2 * kAttnShares, COH>(p.sh_ml, h * 2 * kAttnShares, sh.ml);
-    const int o = h * kAttnShares * p.sh_hd + d;
+    const int ic = i0 < K ? i0 : 0;
+    const int h = ic / sh_hd, d = ic - h * sh_hd;
+    load4<2 * kAttnShares, COH>(sh_ml, h * 2 * kAttnShares, sh.ml);
+    const int o = h * kAttnShares * sh_hd + d;
 #pragma unroll
-    for (int s = 0; s < kAttnShares; ++s) load4<E, COH>(p.sh_o, o + s * p.sh_hd, sh.o[s]);
-    load4<E>(p.signs ? p.signs : p.sh_o, ic, sg);
-    load4<E>(p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : p.sh_o, ic, nw);
+    for (int s = 0; s < kAttnShares; ++s) load4<E, COH>(sh_o, o + s * sh_hd, sh.o[s]);
+    load4<E>(sgr, ic, sg);
+    load4<E>(nwr, ic, nw);
+}
+
+template <int E, bool COH = false>
+EIF_DEV void prep_load_sh(const PrepArgs &p, Shares<E> &sh, float (&sg)[E], float (&nw)[E], int tid = threadIdx.x)
+{
+    prep_load_sh_rows<E, COH>(p.sh_o, p.sh_ml, p.signs ? p.signs : p.sh_o,
+                              p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : p.sh_o, p.K, p.sh_hd, sh, sg, nw, tid);
 }
 
 // v = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s, M = max_s M_s (share 0 always holds rows, so M is finite).

@@ -345,14 +345,33 @@ constexpr int kFusedMaxM = 8;    // token rows of the fused-prep GEMV (each work
 constexpr int kMaxPieces = 4;
 constexpr int kMaxScLoads = 8;
 
+// Scale loads per thread of the GEMV's group scales (a fixed count, so the waits count loads exactly): two for the
+// BitNet layouts (g96, g128: up to 8 x the waves' groups per row), kMaxScLoads for the other group sizes.
+template <int FMT, int UD, bool GROUPED>
+constexpr int gemv_scl() { return FMT == kTern && GROUPED && (UD == 3 || UD == 4) ? 2 : kMaxScLoads; }
+
 // E = 0: activations come prepped (xq/xs); E = 4/8/16: prep fused, E columns per thread, LB as in prep_finish.
 // RT row tiles of 16 rows per workgroup; wave w works on tile w % RT and on steps w / RT, w / RT + ks, ... of
 // it (ks = waves / RT). SPW: steps per wave held in registers at once; the first SPW are loaded unconditionally
 // (a wave with fewer steps loads its last step again and skips the copies), later chunks only when a row has
 // more steps. TT: token tiles (E = 0 only). SH: one token row combined from attention shares (PrepArgs::sh_o)
 // in the prep.
+//
+// The leading arguments are what the first loads need, so they are preloaded into SGPRs at wave launch
+// (-amdgpu-kernarg-preload-count, qlinear.hip's build line; struct arguments are not preloaded) and the
+// activation and weight loads issue before any kernel-argument fetch returns (gemv_hot() builds them):
+//   E > 0:  r0 = x row 0, r1 = signs (x where absent), r2 = x2 (SwiGLU up rows; x where absent), r3 = the norm
+//           weight (x where absent), i0 = K, i1 = ldx;
+//   SH:     r0 = shares' outputs, r1 = shares' maxima and sums, r2 = signs, r3 = norm weight (absent: r0),
+//           i0 = K, i1 = the shares' head dim;
+//   E = 0:  r0 = xq, r1 = xs, r2 = r3 unused, i0 = M, i1 = ldq | (token rows per workgroup << 24).
+// Loads are issued in the order activations, weights, scales, each group with a count known at compile time,
+// so the prep waits for the activations alone.
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT = 1, bool SH = false>
-__global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
+__global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0, const void *__restrict__ r1,
+                                                     const void *__restrict__ r2, const void *__restrict__ r3,
+                                                     const uint8_t *__restrict__ W, int wld, int nsteps, int i0,
+                                                     int i1, QArgs a, PrepArgs p)
 {
     static_assert(TT == 1 || E == 0, "token tiles with staged activations only");
     using GE = Geo<FMT, UD>;
@@ -363,20 +382,27 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     extern __shared__ __align__(16) int8_t smem[];
     __shared__ float xs_l[kGemvTileM * TT];
     __shared__ float red_max[16], red_ss[16];
-    // token chunks: workgroup id -> (row block, chunk); ids 8 apart share the XCD (see above)
+    a.W = W, a.wld = wld, a.nsteps = nsteps;
+    if constexpr (E == 0) {
+        a.xq = static_cast<const int8_t *>(r0), a.xs = static_cast<const float *>(r1), a.M = i0;
+        a.ldq = i1 & 0xFFFFFF, a.mw = i1 >> 24;
+    }
+    // token chunks (E = 0 only): workgroup id -> (row block, chunk); ids 8 apart share the XCD (see above)
     int rb = blockIdx.x;
-    if (a.mw > 0 && a.mw < a.M) {   // uniform
-        const int nch = (a.M + a.mw - 1) / a.mw;
-        const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
-        const int ch = k % nch;
-        rb = (k / nch) * 8 + xcd;
-        if (rb >= a.nrb) return;   // the grid is rounded up to whole XCD rounds
-        const int m0 = ch * a.mw;
-        a.M = min(a.mw, a.M - m0);
-        a.xq += (size_t)m0 * a.ldq;
-        a.xs += m0;
-        a.y += (size_t)m0 * a.ldy;
-        if (a.acc) a.acc += (size_t)m0 * a.N * (GROUPED ? a.G : 1);
+    if constexpr (E == 0) {
+        if (a.mw > 0 && a.mw < a.M) {   // uniform
+            const int nch = (a.M + a.mw - 1) / a.mw;
+            const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+            const int ch = k % nch;
+            rb = (k / nch) * 8 + xcd;
+            if (rb >= a.nrb) return;   // the grid is rounded up to whole XCD rounds
+            const int m0 = ch * a.mw;
+            a.M = min(a.mw, a.M - m0);
+            a.xq += (size_t)m0 * a.ldq;
+            a.xs += m0;
+            a.y += (size_t)m0 * a.ldy;
+            if (a.acc) a.acc += (size_t)m0 * a.N * (GROUPED ? a.G : 1);
+        }
     }
     const int ks = (blockDim.x >> 6) / RT;
     // the wave index through readfirstlane: a scalar, so the per-wave step bounds below are scalar branches
@@ -385,18 +411,11 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     const int r16 = lane & 15, s = lane >> 4;
     const int row0 = rb * TR;
     const int row = row0 + 16 * rt + r16;
-    const bool row_ok = row < a.N;
-    const int kpad = a.nsteps * GE::SC;
-    const int nj = (a.nsteps - kw + ks - 1) / ks;
+    const int kpad = nsteps * GE::SC;
+    const int nj = (nsteps - kw + ks - 1) / ks;
     int8_t *lds_x = smem;
-    // after the staged activations: grouped -> int32 group sums [M][TR][gld] and scales [TR][G];
-    // row-scaled -> int32 K-split partials [ks-1][RT][4][64]
-    const int gld = (a.G + 3) & ~3;
-    int32_t *red = reinterpret_cast<int32_t *>(smem + a.M * p.ldl);
-    int32_t *acc_l = red;
-    float *sc_l = reinterpret_cast<float *>(acc_l + a.M * TR * gld);
 
-    // 1. activation loads
+    // 1. activation loads (preloaded pointers only)
     float v[EV], sg[EV], v2[EV], nwv[EV];
     int4 pc0, pc1, pc2, pc3;   // up to kMaxPieces 16-byte pieces of the int8 rows per thread
     const int pieces = kpad / 16;
@@ -416,9 +435,11 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     float xs_v = 0.0f;
     [[maybe_unused]] Shares<SH ? EV : 1> shv;
     if constexpr (SH) {
-        prep_load_sh<E>(p, shv, sg, nwv);
+        prep_load_sh_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
+                             static_cast<const float *>(r2), static_cast<const float *>(r3), i0, i1, shv, sg, nwv);
     } else if constexpr (E > 0) {
-        prep_load<E>(p, 0, v, sg, v2, nwv);
+        prep_load_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
+                          static_cast<const float *>(r2), static_cast<const float *>(r3), i0, v, sg, v2, nwv);
     } else {
         pc0 = *piece_at(0);
         pc1 = *piece_at(1);
@@ -433,42 +454,53 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
 
     // 2. weight loads: unconditional, with the step clamped into the row (steps past nj are loaded from the
     // last step and never used); no branch, no wait.
-    const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
+    const uint8_t *wp = W + (size_t)row * wld + s * GE::SB;
     uint32_t wq[MS][NW];
     auto load_chunk = [&](int j0) {
 #pragma unroll
         for (int j = 0; j < MS; ++j) {
             if (j0 > 0 && j0 + j >= nj) break;   // later chunks: wave-uniform bound
             const int stj = kw + (j0 + j) * ks;
-            const int st = stj < a.nsteps ? stj : a.nsteps - 1;
+            const int st = stj < nsteps ? stj : nsteps - 1;
             load_words<NW>(wp + (size_t)st * 4 * GE::SB, wq[j]);
         }
     };
     load_chunk(0);
 
-    // the workgroup's group scales, rows row0 .. row0 + TR - 1: one contiguous block of the [N, G] array,
-    // loaded flat (kMaxScLoads per thread at most, clamped to the array) and staged in LDS after the prep. They
-    // are issued after the weight loads: the prep waits for the activation loads only (the oldest), and the
-    // scales are not needed before the weights.
+    // 3. the workgroup's group scales, rows row0 .. row0 + TR - 1: one contiguous block of the [N, G] array,
+    // loaded flat (gemv_scl() per thread, a fixed count) and staged in LDS after the prep. Row-scaled: the
+    // row's scale and bias. A load with nothing to fetch reads an address the workgroup reads anyway (its first
+    // scale, or the lane's own weight word), never one address shared by every workgroup: thousands of waves on
+    // one cache line serialise on one L2 channel. The kernel arguments these need are read while the
+    // activation and weight loads are in flight.
     __builtin_amdgcn_sched_barrier(0);
-    float scv[kMaxScLoads];
-    const int nsc = TR * a.G, last_sc = a.N * a.G - 1;
+    const bool row_ok = row < a.N;
+    const int gld = (a.G + 3) & ~3;
+    int32_t *red = reinterpret_cast<int32_t *>(smem + a.M * p.ldl);
+    int32_t *acc_l = red;
+    float *sc_l = reinterpret_cast<float *>(acc_l + a.M * TR * gld);
+    constexpr int SCL = gemv_scl<FMT, UD, GROUPED>();
+    float scv[SCL];
+    const int nsc = TR * a.G, last_sc = a.N * a.G - 1, sc0 = min(row0 * a.G, last_sc);
     if constexpr (GROUPED && !ACC) {
 #pragma unroll
-        for (int i = 0; i < kMaxScLoads; ++i) {
-            if (i > 0 && i * (int)blockDim.x >= nsc) break;   // uniform bound
+        for (int i = 0; i < SCL; ++i) {
             const int idx = row0 * a.G + (int)threadIdx.x + i * (int)blockDim.x;
-            scv[i] = a.scales[idx < last_sc ? idx : last_sc];
+            scv[i] = a.scales[idx <= last_sc && idx < row0 * a.G + nsc ? idx : sc0];
         }
     }
-    // row-scaled: the row's scale and bias, loaded now (from the weights' first word where absent, selected
-    // at use) so the epilogue does not wait on them
     float rs_raw = 0.0f, bb_raw = 0.0f;
     if constexpr (!GROUPED && !ACC) {
         const int rc = row_ok ? row : a.N - 1;
-        const float *w0 = reinterpret_cast<const float *>(a.W);
-        rs_raw = *(a.scales ? a.scales + rc : w0);
-        bb_raw = *(a.bias ? a.bias + rc : w0);
+        const float *sp0 = a.scales ? a.scales + rc : reinterpret_cast<const float *>(wp);
+        rs_raw = *sp0;
+        bb_raw = *(a.bias ? a.bias + rc : sp0);
+    }
+    // grouped: the bias of the row this thread combines (row0 + threadIdx % TR for every token), loaded now
+    float gb_raw = 0.0f;
+    if constexpr (GROUPED && !ACC) {
+        const int br = min(row0 + (int)threadIdx.x % TR, a.N - 1);
+        gb_raw = *(a.bias ? a.bias + br : a.scales + sc0);
     }
 
     // 3. activations -> LDS
@@ -493,8 +525,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
     }
     if constexpr (GROUPED && !ACC) {
 #pragma unroll
-        for (int i = 0; i < kMaxScLoads; ++i) {
-            if (i > 0 && i * (int)blockDim.x >= nsc) break;
+        for (int i = 0; i < SCL; ++i) {
             const int idx = (int)threadIdx.x + i * (int)blockDim.x;
             if (idx < nsc) sc_l[idx] = scv[i];
         }
@@ -581,6 +612,32 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
             const float *sp = sc_l + r * a.G;
             float t = 0.0f;
             int g = 0;
+            if ((a.G & 3) == 0) {   // the row's scales 16-byte aligned: 16 groups' sums and scales per LDS round trip
+                for (; g + 16 <= a.G; g += 16) {
+                    int4 av[4];
+                    float4 sv[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        av[q] = *reinterpret_cast<const int4 *>(ap + g + 4 * q);
+                        sv[q] = *reinterpret_cast<const float4 *>(sp + g + 4 * q);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        t = fmaf((float)av[q].x, sv[q].x, t);
+                        t = fmaf((float)av[q].y, sv[q].y, t);
+                        t = fmaf((float)av[q].z, sv[q].z, t);
+                        t = fmaf((float)av[q].w, sv[q].w, t);
+                    }
+                }
+                for (; g + 4 <= a.G; g += 4) {
+                    const int4 a4 = *reinterpret_cast<const int4 *>(ap + g);
+                    const float4 s4 = *reinterpret_cast<const float4 *>(sp + g);
+                    t = fmaf((float)a4.x, s4.x, t);
+                    t = fmaf((float)a4.y, s4.y, t);
+                    t = fmaf((float)a4.z, s4.z, t);
+                    t = fmaf((float)a4.w, s4.w, t);
+                }
+            }
             for (; g + 4 <= a.G; g += 4) {
                 const int4 a4 = *reinterpret_cast<const int4 *>(ap + g);
                 t = fmaf((float)a4.x, sp[g], t);
@@ -590,7 +647,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(QArgs a, PrepArgs p)
             }
             for (; g < a.G; ++g) t = fmaf((float)ap[g], sp[g], t);
             float out = t * xs_l[tok];
-            if (a.bias) out = out + a.bias[orow];
+            if (a.bias) out = out + gb_raw;
             a.y[(size_t)tok * a.ldy + orow] = out;
         }
         return;
@@ -687,17 +744,18 @@ __global__ __launch_bounds__(kStreamThreads) void qstream_kernel(QArgs a, int nt
     const float xs_v = a.xs[(int)threadIdx.x < a.M ? threadIdx.x : 0];
     __builtin_amdgcn_sched_barrier(0);
 
-    // a tile's loads: unconditional, the tile clamped into the matrix (rows are padded to whole tiles); the row's
-    // scale and bias from the codes' first word where absent (selected at use)
-    const float *w0 = reinterpret_cast<const float *>(a.W);
+    // a tile's loads: unconditional, the tile clamped into the matrix (rows are padded to whole tiles); an absent
+    // scale or bias reads an address the lane reads anyway (its row's scale, else its first code word; selected at
+    // use), so absent operands do not send every wave to one cache line
     auto load = [&](uint32_t (&w)[NS][NW], float &rs, float &bb, int tile) {
         const int row = min(tile, ntiles - 1) * 16 + r16;
         const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
 #pragma unroll
         for (int st = 0; st < NS; ++st) load_words<NW>(wp + (size_t)st * 4 * GE::SB, w[st]);
         const int rc = min(row, a.N - 1);
-        rs = *(a.scales ? a.scales + rc : w0);
-        bb = *(a.bias ? a.bias + rc : w0);
+        const float *sp0 = a.scales ? a.scales + rc : reinterpret_cast<const float *>(wp);
+        rs = *sp0;
+        bb = *(a.bias ? a.bias + rc : sp0);
     };
     uint32_t wA[NS][NW], wB[NS][NW];
     float rsA, bbA, rsB, bbB;
@@ -824,9 +882,10 @@ __global__ __launch_bounds__(kRowPairThreads) void qrowpair_kernel(QArgs a, int 
     const int orow = tile * 16 + 2 * (h >> 2) + half;   // the row whose sum this lane's quad ends with
     const bool row_ok = orow < a.N;
     const int rc = row_ok ? orow : a.N - 1;
-    const float *w0 = reinterpret_cast<const float *>(a.W);
-    const float rs_raw = *(a.scales ? a.scales + rc : w0);
-    const float bb_raw = *(a.bias ? a.bias + rc : w0);
+    // an absent scale or bias reads an address the lane reads anyway (its row's scale, else its first code word)
+    const float *sp0 = a.scales ? a.scales + rc : reinterpret_cast<const float *>(wp);
+    const float rs_raw = *sp0;
+    const float bb_raw = *(a.bias ? a.bias + rc : sp0);
     const float xs = a.xs[0];
     const bool b4 = h & 16, b3 = h & 8, b2 = h & 4;
     // 2. dot products, row pair by row pair in load order
@@ -1222,13 +1281,36 @@ size_t gemv_max_lds()
 template <int FMT, int UD, bool GROUPED>
 constexpr bool gemv_tuned() { return FMT != kTern || (GROUPED && (UD == 3 || UD == 4)); }
 
+// The preloaded leading arguments of qgemv_kernel (its header comment gives their meaning per form).
+struct GemvHot {
+    const void *r0, *r1, *r2, *r3;
+    int i0, i1;
+};
+
+GemvHot gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares)
+{
+    if (shares) {
+        const float *o = p.sh_o;
+        return {o, p.sh_ml, p.signs ? p.signs : o, p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : o, p.K, p.sh_hd};
+    }
+    if (fused) {
+        const float *x = p.x;
+        return {x, p.signs ? p.signs : x, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 : x,
+                p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : x, p.K, p.ldx};
+    }
+    return {a.xq, a.xs, a.xq, a.xq, a.M, a.ldq | (a.mw << 24)};
+}
+
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT>
 int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
     const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
     QArgs ag = a;
     const int grid = gemv_grid(ag, rows_pad / (16 * RT));
-    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT, TT><<<grid, 64 * RT * ks, lds, st>>>(ag, p);
+    if (E == 0 && ((ag.ldq >> 24) || ag.mw < 0 || ag.mw > 127)) return EIF_HIP_E_LIMIT;   // packed into i1
+    const GemvHot h = gemv_hot(ag, p, E > 0, false);
+    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT, TT><<<grid, 64 * RT * ks, lds, st>>>(
+        h.r0, h.r1, h.r2, h.r3, ag.W, ag.wld, ag.nsteps, h.i0, h.i1, ag, p);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
@@ -1240,7 +1322,9 @@ int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipS
 {
     if constexpr (FMT == kTern && !ACC && (E == 4 || E == 8) && RT == 1) {
         const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
-        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true><<<rows_pad / 16, 64 * ks, lds, st>>>(a, p);
+        const GemvHot h = gemv_hot(a, p, true, true);
+        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true><<<rows_pad / 16, 64 * ks, lds, st>>>(
+            h.r0, h.r1, h.r2, h.r3, a.W, a.wld, a.nsteps, h.i0, h.i1, a, p);
         EIF_HIP_LAUNCHED();
         return EIF_HIP_OK;
     } else {
@@ -1287,7 +1371,7 @@ int launch_gemv_fused(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, i
 // Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses the GEMM).
 // Shape: four row tiles per workgroup for matrices of 768 tiles or more (fewer workgroups repeat the
 // activation prep and staging), ks waves per tile from pick_ks_gemv, raised until the threads cover the row
-// (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
+// (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (gemv_scl()).
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, hipStream_t st)
 {
@@ -1301,7 +1385,7 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
         ks = ks < 1 ? 1 : ks;
     }
     if (ks > maxks) ks = maxks;
-    auto scales_fit = [&](int k) { return !GROUPED || ACC || a.G <= kMaxScLoads * 4 * k; };
+    auto scales_fit = [&](int k) { return !GROUPED || ACC || a.G <= gemv_scl<FMT, UD, GROUPED>() * 4 * k; };
     auto lds_fit = [&](int k) { return gemv_lds_bytes(GROUPED, a, p.ldl, rt, k) <= gemv_max_lds(); };
     if (p.x) {
         // E columns per thread: the fewest that let at most 16 waves cover the padded row (short per-thread
@@ -1333,7 +1417,7 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
 // Returns 1 when the shape is outside what the small-batch kernel stages (the caller uses the GEMM).
 // Shape: four row tiles per workgroup for matrices of 768 tiles or more (fewer workgroups repeat the
 // activation prep and staging), else one; ks waves per tile from pick_ks_gemv, raised until the threads cover
-// the row (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (kMaxScLoads).
+// the row (fused prep), the int8 pieces fit (kMaxPieces per thread) and the scale block fits (gemv_scl()).
 // A shape that does not fit with four tiles is launched with one.
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemv_m(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
