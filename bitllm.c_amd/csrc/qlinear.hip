@@ -79,9 +79,13 @@ template <int FMT, int UD>
 constexpr int gemm_waves() { return FMT == kTern && UD != 4 ? 1 : 4; }
 
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
+// The leading arguments (preloaded into SGPRs at wave launch, as qgemv_kernel's) duplicate the QArgs fields the
+// first loads need.
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<FMT, UD>())))
-void qgemm_kernel(QArgs a)
+void qgemm_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W, const float *__restrict__ scales,
+                  int wld, int ldq, int M, int nsteps, int G, int N, QArgs a)
 {
+    a.xq = xq, a.W = W, a.scales = scales, a.wld = wld, a.ldq = ldq, a.M = M, a.nsteps = nsteps, a.G = G, a.N = N;
     using GE = Geo<FMT, UD>;
     constexpr int NW = GE::SB / 4;
     constexpr int TM = 16 * TT;                    // tokens per workgroup
@@ -717,8 +721,11 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
 constexpr int kStreamThreads = 256;
 
 template <int FMT, int UD, bool ACC, int NS, int TT>
-__global__ __launch_bounds__(kStreamThreads) void qstream_kernel(QArgs a, int ntiles)
+__global__ __launch_bounds__(kStreamThreads) void qstream_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W,
+                                                                  const float *__restrict__ scales, int wld, int ldq,
+                                                                  int M, int N, int ntiles, QArgs a)
 {
+    a.xq = xq, a.W = W, a.scales = scales, a.wld = wld, a.ldq = ldq, a.M = M, a.N = N;   // preloaded (see qgemm_kernel)
     static_assert(FMT != kTern, "row-scaled INT4 / INT8 layouts");
     using GE = Geo<FMT, UD>;
     constexpr int NW = GE::SB / 4, NMF = GE::NMF;
@@ -854,8 +861,11 @@ template <int FMT>
 constexpr int rowpair_max_p() { return FMT == kI4 ? 4 : 5; }
 
 template <int FMT, int P, bool ACC>
-__global__ __launch_bounds__(kRowPairThreads) void qrowpair_kernel(QArgs a, int ntiles)
+__global__ __launch_bounds__(kRowPairThreads) void qrowpair_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W,
+                                                                    const float *__restrict__ scales, int wld, int N,
+                                                                    int ntiles, QArgs a)
 {
+    a.xq = xq, a.W = W, a.scales = scales, a.wld = wld, a.N = N;   // preloaded (see qgemm_kernel)
     static_assert(FMT == kI4 || FMT == kI8, "row-scaled INT4 / INT8 layouts");
     constexpr int SHIFT = Geo<FMT, 0>::SHIFT;
     constexpr int CB = FMT == kI4 ? 32 : 16;   // activation bytes (columns) of a 16-byte chunk
@@ -1203,7 +1213,8 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     if (ks == -2) return EIF_HIP_E_DEVICE;
     if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
-    qgemm_kernel<FMT, UD, GROUPED, ACC, TT><<<grid, kGemmThreads, 0, st>>>(a);
+    qgemm_kernel<FMT, UD, GROUPED, ACC, TT><<<grid, kGemmThreads, 0, st>>>(a.xq, a.W, a.scales, a.wld, a.ldq, a.M,
+                                                                           a.nsteps, a.G, a.N, a);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
@@ -1451,7 +1462,8 @@ int launch_stream_t(const QArgs &a, int rows_pad, hipStream_t st)
     const int wpc = g_gemv_stream > 0 ? g_gemv_stream : kStreamWavesPerCU;
     const int waves = std::min(ntiles, device_cus() * wpc);
     const int grid = eif_ceil_div(waves, kStreamThreads / 64);
-    qstream_kernel<FMT, UD, ACC, NS, TT><<<grid, kStreamThreads, (size_t)a.M * ldl, st>>>(a, ntiles);
+    qstream_kernel<FMT, UD, ACC, NS, TT><<<grid, kStreamThreads, (size_t)a.M * ldl, st>>>(a.xq, a.W, a.scales, a.wld, a.ldq,
+                                                                                        a.M, a.N, ntiles, a);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
@@ -1493,7 +1505,7 @@ int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t 
         const int grid = eif_ceil_div(ntiles, kRowPairThreads / 64);
         constexpr int PM = rowpair_max_p<FMT>();
         static_assert(PM <= 5, "one case per pass count");
-#define EIF_RP(PP) qrowpair_kernel<FMT, PP, ACC><<<grid, kRowPairThreads, 0, st>>>(a, ntiles)
+#define EIF_RP(PP) qrowpair_kernel<FMT, PP, ACC><<<grid, kRowPairThreads, 0, st>>>(a.xq, a.W, a.scales, a.wld, a.N, ntiles, a)
         switch (a.wld / 512) {
         case 1: EIF_RP(1); break;
         case 2: EIF_RP(2); break;
