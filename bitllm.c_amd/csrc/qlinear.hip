@@ -365,10 +365,12 @@ constexpr int gemv_scl() { return FMT == kTern && GROUPED && (UD == 3 || UD == 4
 // (-amdgpu-kernarg-preload-count, qlinear.hip's build line; struct arguments are not preloaded) and the
 // activation and weight loads issue before any kernel-argument fetch returns (gemv_hot() builds them):
 //   E > 0:  r0 = x row 0, r1 = signs (x where absent), r2 = x2 (SwiGLU up rows; x where absent), r3 = the norm
-//           weight (x where absent), i0 = K, i1 = ldx;
+//           weight (x where absent), i0 = K;
 //   SH:     r0 = shares' outputs, r1 = shares' maxima and sums, r2 = signs, r3 = norm weight (absent: r0),
-//           i0 = K, i1 = the shares' head dim;
-//   E = 0:  r0 = xq, r1 = xs, r2 = r3 unused, i0 = M, i1 = ldq | (token rows per workgroup << 24).
+//           i0 = K, i1 bits 0..26 = the shares' head dim;
+//   E = 0:  r0 = xq, r1 = xs, r2 = r3 unused, i0 = M, i1 bits 0..19 = ldq, bits 20..26 = token rows per workgroup;
+//   every form: i1 bits 27..31 = ks, the waves per row tile (blockDim.x / 64 / RT: the workgroup size is itself
+//           a kernel-argument fetch, and the weight steps of a wave depend on it).
 // Loads are issued in the order activations, weights, scales, each group with a count known at compile time,
 // so the prep waits for the activations alone.
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT = 1, bool SH = false>
@@ -387,9 +389,10 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     __shared__ float xs_l[kGemvTileM * TT];
     __shared__ float red_max[16], red_ss[16];
     a.W = W, a.wld = wld, a.nsteps = nsteps;
+    const int ks = (int)((unsigned)i1 >> 27), nthr = 64 * RT * ks;   // nthr == blockDim.x
     if constexpr (E == 0) {
         a.xq = static_cast<const int8_t *>(r0), a.xs = static_cast<const float *>(r1), a.M = i0;
-        a.ldq = i1 & 0xFFFFFF, a.mw = i1 >> 24;
+        a.ldq = i1 & 0xFFFFF, a.mw = (i1 >> 20) & 0x7F;
     }
     // token chunks (E = 0 only): workgroup id -> (row block, chunk); ids 8 apart share the XCD (see above)
     int rb = blockIdx.x;
@@ -408,7 +411,6 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
             if (a.acc) a.acc += (size_t)m0 * a.N * (GROUPED ? a.G : 1);
         }
     }
-    const int ks = (blockDim.x >> 6) / RT;
     // the wave index through readfirstlane: a scalar, so the per-wave step bounds below are scalar branches
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rt = wv % RT, kw = wv / RT;
@@ -424,13 +426,13 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     int4 pc0, pc1, pc2, pc3;   // up to kMaxPieces 16-byte pieces of the int8 rows per thread
     const int pieces = kpad / 16;
     auto piece_at = [&](int i) -> const int4 * {
-        const int idx = threadIdx.x + i * blockDim.x;
+        const int idx = threadIdx.x + i * nthr;
         const int ic = idx < a.M * pieces ? idx : a.M * pieces - 1;
         const int m = ic / pieces, c = ic - m * pieces;
         return reinterpret_cast<const int4 *>(a.xq + (size_t)m * a.ldq + 16 * c);
     };
     auto piece_store = [&](int i, const int4 &val) {
-        const int idx = threadIdx.x + i * blockDim.x;
+        const int idx = threadIdx.x + i * nthr;
         if (idx < a.M * pieces) {
             const int m = idx / pieces, c = idx - m * pieces;
             *reinterpret_cast<int4 *>(lds_x + m * p.ldl + 16 * c) = val;
@@ -440,7 +442,8 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     [[maybe_unused]] Shares<SH ? EV : 1> shv;
     if constexpr (SH) {
         prep_load_sh_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
-                             static_cast<const float *>(r2), static_cast<const float *>(r3), i0, i1, shv, sg, nwv);
+                             static_cast<const float *>(r2), static_cast<const float *>(r3), i0, i1 & 0x7FFFFFF, shv,
+                             sg, nwv);
     } else if constexpr (E > 0) {
         prep_load_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
                           static_cast<const float *>(r2), static_cast<const float *>(r3), i0, v, sg, v2, nwv);
@@ -489,7 +492,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     if constexpr (GROUPED && !ACC) {
 #pragma unroll
         for (int i = 0; i < SCL; ++i) {
-            const int idx = row0 * a.G + (int)threadIdx.x + i * (int)blockDim.x;
+            const int idx = row0 * a.G + (int)threadIdx.x + i * nthr;
             scv[i] = a.scales[idx <= last_sc && idx < row0 * a.G + nsc ? idx : sc0];
         }
     }
@@ -530,7 +533,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     if constexpr (GROUPED && !ACC) {
 #pragma unroll
         for (int i = 0; i < SCL; ++i) {
-            const int idx = (int)threadIdx.x + i * (int)blockDim.x;
+            const int idx = (int)threadIdx.x + i * nthr;
             if (idx < nsc) sc_l[idx] = scv[i];
         }
     }
@@ -609,7 +612,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
         // 5. group combine, in group order for every (token, row): t = fmaf((float)acc_g, s[r,g], t); the
         // result does not depend on how the steps were split over waves.
         __syncthreads();
-        for (int c = threadIdx.x; c < TR * a.M; c += blockDim.x) {
+        for (int c = threadIdx.x; c < TR * a.M; c += nthr) {
             const int tok = c / TR, r = c % TR, orow = row0 + r;
             if (orow >= a.N) continue;
             const int32_t *ap = acc_l + (tok * TR + r) * gld;
@@ -1298,18 +1301,25 @@ struct GemvHot {
     int i0, i1;
 };
 
-GemvHot gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares)
+// ks: waves per row tile (1..16). Returns false when a field does not fit its bits (the launch is refused).
+bool gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares, int ks, GemvHot *h)
 {
+    if (ks < 1 || ks > 16) return false;
+    const unsigned kb = (unsigned)ks << 27;
     if (shares) {
         const float *o = p.sh_o;
-        return {o, p.sh_ml, p.signs ? p.signs : o, p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : o, p.K, p.sh_hd};
-    }
-    if (fused) {
+        if (p.sh_hd < 0 || p.sh_hd >= (1 << 27)) return false;
+        *h = {o, p.sh_ml, p.signs ? p.signs : o, p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : o, p.K,
+              (int)((unsigned)p.sh_hd | kb)};
+    } else if (fused) {
         const float *x = p.x;
-        return {x, p.signs ? p.signs : x, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 : x,
-                p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : x, p.K, p.ldx};
+        *h = {x, p.signs ? p.signs : x, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 : x,
+              p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : x, p.K, (int)kb};
+    } else {
+        if (a.ldq < 0 || a.ldq >= (1 << 20) || a.mw < 0 || a.mw > 127) return false;
+        *h = {a.xq, a.xs, a.xq, a.xq, a.M, (int)((unsigned)a.ldq | ((unsigned)a.mw << 20) | kb)};
     }
-    return {a.xq, a.xs, a.xq, a.xq, a.M, a.ldq | (a.mw << 24)};
+    return true;
 }
 
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT>
@@ -1318,8 +1328,8 @@ int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipSt
     const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
     QArgs ag = a;
     const int grid = gemv_grid(ag, rows_pad / (16 * RT));
-    if (E == 0 && ((ag.ldq >> 24) || ag.mw < 0 || ag.mw > 127)) return EIF_HIP_E_LIMIT;   // packed into i1
-    const GemvHot h = gemv_hot(ag, p, E > 0, false);
+    GemvHot h;
+    if (!gemv_hot(ag, p, E > 0, false, ks, &h)) return EIF_HIP_E_LIMIT;   // a field beyond its packed bits
     qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT, TT><<<grid, 64 * RT * ks, lds, st>>>(
         h.r0, h.r1, h.r2, h.r3, ag.W, ag.wld, ag.nsteps, h.i0, h.i1, ag, p);
     EIF_HIP_LAUNCHED();
@@ -1333,7 +1343,8 @@ int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipS
 {
     if constexpr (FMT == kTern && !ACC && (E == 4 || E == 8) && RT == 1) {
         const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
-        const GemvHot h = gemv_hot(a, p, true, true);
+        GemvHot h;
+        if (!gemv_hot(a, p, true, true, ks, &h)) return EIF_HIP_E_LIMIT;
         qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true><<<rows_pad / 16, 64 * ks, lds, st>>>(
             h.r0, h.r1, h.r2, h.r3, a.W, a.wld, a.nsteps, h.i0, h.i1, a, p);
         EIF_HIP_LAUNCHED();
