@@ -1410,8 +1410,11 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     auto scales_fit = [&](int k) { return !GROUPED || ACC || a.G <= gemv_scl<FMT, UD, GROUPED>() * 4 * k; };
     auto lds_fit = [&](int k) { return gemv_lds_bytes(GROUPED, a, p.ldl, rt, k) <= gemv_max_lds(); };
     if (p.x) {
-        // E columns per thread: the fewest that let at most 16 waves cover the padded row (short per-thread
-        // chains), and a WHT block within one wave.
+        // E columns per thread: the fewest that let at most 16 waves cover the padded row, and a WHT block within
+        // one wave. The prep is a chain of dependent steps per wave (cross-lane butterflies, reductions), so the
+        // shortest chains win: E = 16 on 3 waves measured slower than E = 4 on 10 for K = 2560 (QKV 4.8 against
+        // 4.1 us), E = 16 slower than E = 8 for K = 6912 (down 7.2 against 6.6 us). The standalone prep kernel
+        // and the persistent decode step take the same E, so a pre-op's sum of squares has the same order there.
         for (int e = 4; e <= 16; e *= 2) {
             if (64 * e < p.block || e < g_gemv_prep_cols) continue;
             if (p.sh_ml && (e > 8 || p.sh_hd % e != 0)) continue;
