@@ -59,6 +59,7 @@ _SIGS = {
     "eif_gguf_bitnet_get_globals": (_i, [_vp, C.POINTER(BitnetGlobals)]),
     "eif_hip_bitnet_load_gguf": (_i, [_vp, C.c_char_p, _i]),
     "eif_hip_qlinear_prep": (_i, [_vp, C.POINTER(PrepSpec), _vp, _vp, _i, _i, _vp]),
+    "eif_hip_qlinear_prep_glu": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _i, _vp]),
     "eif_hip_qlinear_prep_acc": (_i, [_vp, C.POINTER(PrepSpec), _vp, _i, _vp]),
     "eif_hip_prep_spec_rows": (_i, [C.POINTER(PrepSpec), _i, _vp, _i, _vp, _i, _vp]),
     "eif_hip_quant_rows": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp]),

@@ -356,37 +356,31 @@ __global__ void prefill_state_kernel(int *state, int *seq, const int *prompt, in
     if (threadIdx.x == 0) state[0] = pos0 + n - 1;
 }
 
-// Greedy token: first index of the largest logit (NaN never wins), from the head GEMV's per-tile maxima (value,
-// row) pairs; while the prompt lasts the next token is the prompt's. The made token is stored at position
-// pos + 1 of the sequence, the position advances, and x becomes the next token's embedding row.
-__global__ __launch_bounds__(1024) void sample_kernel(const float *part_v, const int *part_i, int n_part, int *state,
-                                                      const int *prompt, int *seq, int seq_len, const int8_t *emb,
+// Greedy token: first index of the largest logit (NaN never wins), from the head GEMV's argmax slots (atomic max of
+// eif_argmax_key over its tiles; folded here by the first wave and reset to 0 for the next step); while the prompt
+// lasts the next token is the prompt's. The made token is stored at position pos + 1 of the sequence, the position advances, and x becomes
+// the next token's embedding row.
+__global__ __launch_bounds__(1024) void sample_kernel(unsigned long long *amax_key, int *state, const int *prompt,
+                                                      int *seq, int seq_len, const int8_t *emb,
                                                       const float *emb_scale, float *x, int dim, int vocab, int *bar)
 {
     // the persistent step's barrier words back to zero for the next step (that step ended before this launch)
     if (bar && (int)threadIdx.x < eif::kPersistBarWords) bar[(size_t)eif::kPersistBarStride * threadIdx.x] = 0;
-    __shared__ float bv[16];
-    __shared__ int bi[16];
     __shared__ int next_l;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x;
-    float v = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = t; i < n_part; i += nt) {
-        const float pv = part_v[i];
-        const int pi = part_i[i];
-        if (pv > v || (pv == v && pi < idx)) v = pv, idx = pi;
-    }
+    const int t = threadIdx.x, nt = blockDim.x;
+    static_assert(kArgmaxSlots == 64, "one slot per lane of the first wave");
+    unsigned long long key = 0;
+    if (t < 64) {
+        key = amax_key[(size_t)kArgmaxStride * t];
+        amax_key[(size_t)kArgmaxStride * t] = 0ull;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (ov > v || (ov == v && oi < idx)) v = ov, idx = oi;
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(key, off, 64);
+            key = o > key ? o : key;
+        }
     }
-    if (lane == 0) bv[wave] = v, bi[wave] = idx;
-    __syncthreads();
     if (t == 0) {
-        for (int w = 1; w < nt / 64; ++w)
-            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) v = bv[w], idx = bi[w];
+        int idx = eif_argmax_key_row(key);
         if (idx < 0 || idx >= vocab) idx = 0;   // every logit NaN or -inf
         const int pos = state[0], np = state[2];
         const int next = pos + 1 < np ? prompt[pos + 1] : idx;
@@ -450,8 +444,7 @@ struct eif_hip_bitnet {
     float *sh_ml = nullptr;          // and their maxima, then sums [n_heads][2 kAttnShares]
     int8_t *hq = nullptr;            // the head's prepped input row [head_kpad] and its scale
     float *hs = nullptr;
-    float *amax_v = nullptr;         // the head's per-tile maxima [head_tiles]
-    int *amax_i = nullptr;
+    unsigned long long *amax_key = nullptr;   // the head's greedy argmax slots (eif_argmax_key), 0 between steps
     int head_kpad = 0, head_tiles = 0;
     int hpos = 0;                    // host copy of the position (steps are deterministic)
     int n_prompt = 0;                // host copy of the prompt length
@@ -509,9 +502,15 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         sp = eif_hip_prep_spec{};
         sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_ffn[l], sp.eps = c.rms_eps;
         sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
-        if ((rc = eif_hip_qlinear_prep(m->w13[l], &sp, nullptr, m->hb, 2 * c.hidden, 1, st))) return rc;
+        // h = SiLU(gate) * up in the gate|up launch (its GLU form) where the shape allows, then the down projection
+        // with the sub-RMSNorm alone: the same bits as both halves and the SwiGLU pre-op
+        rc = eif_hip_qlinear_prep_glu(m->w13[l], &sp, m->hb, c.hidden, 1, st);
+        const bool glu = rc == EIF_HIP_OK;
+        if (!glu && (rc != EIF_HIP_E_LIMIT || (rc = eif_hip_qlinear_prep(m->w13[l], &sp, nullptr, m->hb, 2 * c.hidden, 1, st))))
+            return rc;
         sp = eif_hip_prep_spec{};
-        sp.x = m->hb, sp.x2 = m->hb + c.hidden, sp.ldx = c.hidden, sp.pre = EIF_HIP_PRE_SWIGLU_RMS;
+        sp.x = m->hb, sp.x2 = m->hb + c.hidden, sp.ldx = c.hidden;
+        sp.pre = glu ? EIF_HIP_PRE_RMS : EIF_HIP_PRE_SWIGLU_RMS;
         sp.norm_w = m->rms_sub_ffn[l], sp.eps = c.sub_eps;
         sp.signs = m->signs_hidden, sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
         if ((rc = eif_hip_qlinear_prep(m->w2[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += W2 h
@@ -536,9 +535,8 @@ int enqueue_head_gemv(eif_hip_bitnet *m, hipStream_t st)
 {
     const eif_hip_bitnet_config &c = m->c;
     int rc;
-    if ((rc = eif::qlinear_argmax(m->head, m->hq, m->head_kpad, m->hs, m->logits, m->amax_v, m->amax_i, st)))
-        return rc;
-    sample_kernel<<<1, 1024, 0, st>>>(m->amax_v, m->amax_i, m->head_tiles, m->state, m->prompt, m->seq, c.seq_len,
+    if ((rc = eif::qlinear_argmax(m->head, m->hq, m->head_kpad, m->hs, m->logits, m->amax_key, st))) return rc;
+    sample_kernel<<<1, 1024, 0, st>>>(m->amax_key, m->state, m->prompt, m->seq, c.seq_len,
                                       m->emb, m->emb_scale, m->x, c.dim, c.vocab, eif::persist_bar(m->plan));
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
@@ -876,8 +874,8 @@ int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *
     m->head_kpad = kp;
     m->head_tiles = eif::qweight_row_tiles(m->head);
     if (hipMalloc(&m->hq, (size_t)kp) != hipSuccess || hipMalloc(&m->hs, sizeof(float) * 4) != hipSuccess ||
-        hipMalloc(&m->amax_v, sizeof(float) * m->head_tiles) != hipSuccess ||
-        hipMalloc(&m->amax_i, sizeof(int) * m->head_tiles) != hipSuccess)
+        hipMalloc(&m->amax_key, sizeof(unsigned long long) * kArgmaxSlots * kArgmaxStride) != hipSuccess ||
+        hipMemset(m->amax_key, 0, sizeof(unsigned long long) * kArgmaxSlots * kArgmaxStride) != hipSuccess)
         return EIF_HIP_E_NOMEM;
     return EIF_HIP_OK;
 }
@@ -1056,7 +1054,7 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
     for (void *p : {(void *)m->rms_final, (void *)m->signs_dim, (void *)m->signs_q, (void *)m->signs_hidden,
                     (void *)m->emb, (void *)m->emb_scale, (void *)m->x, (void *)m->qkv, (void *)m->hb,
                     (void *)m->logits, (void *)m->kc, (void *)m->vc, (void *)m->state, (void *)m->prompt,
-                    (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_v, (void *)m->amax_i,
+                    (void *)m->seq, (void *)m->hq, (void *)m->hs, (void *)m->amax_key,
                     (void *)m->rope, (void *)m->sh_o, (void *)m->sh_ml})
         if (p) (void)hipFree(p);
     delete m;

@@ -43,6 +43,27 @@ EIF_DEV float eif_wave_sum(float v)
     return v;
 }
 
+// Greedy argmax of a row-scaled GEMV's outputs as one 64-bit key, folded over the workgroups by atomic max:
+// the high word orders the value (IEEE order mapped to unsigned; -0 taken as +0; NaN taken as -inf, so it never
+// beats a number), the low word is ~row, so of equal values the first row wins. The key of a row past the
+// matrix (row 0x7fffffff, value -inf) loses to every real row.
+EIF_DEV unsigned long long eif_argmax_key(float v, int row)
+{
+    if (v != v) v = -INFINITY;
+    if (v == 0.0f) v = 0.0f;
+    const uint32_t u = __float_as_uint(v);
+    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)row);
+}
+inline __host__ __device__ int eif_argmax_key_row(unsigned long long key)
+{
+    return (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+}
+// The keys are folded into kArgmaxSlots slots kArgmaxStride keys (256 bytes) apart, a tile's into slot tile %
+// kArgmaxSlots: device-scope atomics on one address serialise (8,016 tiles of a 128,256-row head on one key took
+// 61 us more than the GEMV), on separate lines they proceed in parallel; the reader folds the slots.
+constexpr int kArgmaxSlots = 64, kArgmaxStride = 32;
+
 // Decode attention: the positions of a head are split into at most kAttnShares chunks, each leaving a share
 // (unnormalized output, running maximum, sum) that the next linear's prep combines.
 constexpr int kAttnShares = 8;
@@ -96,8 +117,8 @@ int scratch_init(int device, float **out, int **cnt = nullptr);
 // sums L_s (a share with M_s = -inf weighs 0). spec->x and spec->ldx are ignored; ternary weights only.
 int qlinear_prep_shares(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *sh_o,
                         const float *sh_ml, int hd, const float *bias, float *y, int ldy, hipStream_t st);
-int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y, float *amax_v,
-                   int *amax_i, hipStream_t st);
+int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y,
+                   unsigned long long *amax_key, hipStream_t st);
 
 // FP32-activation GEMVs on the row-tile layout (f32linear.hip). Formats of the resident copy and the reference
 // layouts it is made from.

@@ -56,8 +56,8 @@ struct QArgs {
     int M, N, nsteps;
     float *part;           // GEMM split along K: partial sums [split][tile][thread][4 TT]
     int *cnt;              // GEMM split along K: one arrival counter per output tile, zero between launches
-    float *amax_v;         // row-scaled GEMV, M = 1: per 16-row tile, the largest output and its row
-    int *amax_i;           //   (first of equal maxima; NaN never wins), or NULL
+    unsigned long long *amax_key;   // row-scaled GEMV, M = 1: the largest output and its first row, atomic max of
+                                    // eif_argmax_key over the 16-row tiles into kArgmaxSlots slots, or NULL
     int mw;                // GEMV: token rows per workgroup (0: all M in one workgroup)
     int nrb;               // GEMV with token chunks: row blocks (workgroups along the rows per chunk)
 };
@@ -373,13 +373,22 @@ constexpr int gemv_scl() { return FMT == kTern && GROUPED && (UD == 3 || UD == 4
 //           a kernel-argument fetch, and the weight steps of a wave depend on it).
 // Loads are issued in the order activations, weights, scales, each group with a count known at compile time,
 // so the prep waits for the activations alone.
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT = 1, bool SH = false>
+//
+// GLU (gated form, grouped FP32 outputs): the matrix stacks a gate half (rows 0 .. h - 1) over an up half (rows
+// h .. 2h - 1), h = 16 * (i1 bits 0..26); a workgroup's first RT / 2 row tiles are gate tiles and its last RT / 2
+// the matching up tiles, and it writes h rows y[r] = SiLU(gate_r) * up_r = (g * (1 / (1 + expf(-g)))) * u, the
+// SwiGLU of the reference's FFN (src/eif_tinyllm.c:774-780) and the same expression as the SwiGLU pre-op of
+// prep_finish, so a down projection fed with these rows and the RMSNorm pre-op gives the bits of one fed with
+// the two halves and the SwiGLU pre-op.
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT = 1, bool SH = false,
+          bool GLU = false>
 __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0, const void *__restrict__ r1,
                                                      const void *__restrict__ r2, const void *__restrict__ r3,
                                                      const uint8_t *__restrict__ W, int wld, int nsteps, int i0,
                                                      int i1, QArgs a, PrepArgs p)
 {
     static_assert(TT == 1 || E == 0, "token tiles with staged activations only");
+    static_assert(!GLU || (GROUPED && !ACC && !SH && RT % 2 == 0), "the gated form: grouped FP32 outputs, paired tiles");
     using GE = Geo<FMT, UD>;
     constexpr int NW = GE::SB / 4;
     constexpr int EV = E > 0 ? E : 4;
@@ -416,7 +425,9 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     const int rt = wv % RT, kw = wv / RT;
     const int r16 = lane & 15, s = lane >> 4;
     const int row0 = rb * TR;
-    const int row = row0 + 16 * rt + r16;
+    constexpr int RH = RT / 2;   // GLU: gate tiles per workgroup
+    const int glu_t = GLU ? (i1 & 0x7FFFFFF) : 0;   // GLU: tiles of one half
+    const int row = GLU ? (rt < RH ? rb * RH + rt : glu_t + rb * RH + rt - RH) * 16 + r16 : row0 + 16 * rt + r16;
     const int kpad = nsteps * GE::SC;
     const int nj = (nsteps - kw + ks - 1) / ks;
     int8_t *lds_x = smem;
@@ -488,12 +499,15 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     float *sc_l = reinterpret_cast<float *>(acc_l + a.M * TR * gld);
     constexpr int SCL = gemv_scl<FMT, UD, GROUPED>();
     float scv[SCL];
-    const int nsc = TR * a.G, last_sc = a.N * a.G - 1, sc0 = min(row0 * a.G, last_sc);
+    // GLU: the gate tiles' block, then the up tiles' block (each RH * 16 rows, contiguous in [N, G])
+    const int sbase = GLU ? rb * RH * 16 * a.G : row0 * a.G, shalf = RH * 16 * a.G, sup = glu_t * 16 * a.G;
+    const int nsc = TR * a.G, last_sc = a.N * a.G - 1, sc0 = min(sbase, last_sc);
     if constexpr (GROUPED && !ACC) {
 #pragma unroll
         for (int i = 0; i < SCL; ++i) {
-            const int idx = row0 * a.G + (int)threadIdx.x + i * nthr;
-            scv[i] = a.scales[idx <= last_sc && idx < row0 * a.G + nsc ? idx : sc0];
+            const int l = (int)threadIdx.x + i * nthr;
+            const int idx = sbase + l + (GLU && l >= shalf ? sup - shalf : 0);
+            scv[i] = a.scales[idx <= last_sc && l < nsc ? idx : sc0];
         }
     }
     float rs_raw = 0.0f, bb_raw = 0.0f;
@@ -612,9 +626,8 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
         // 5. group combine, in group order for every (token, row): t = fmaf((float)acc_g, s[r,g], t); the
         // result does not depend on how the steps were split over waves.
         __syncthreads();
-        for (int c = threadIdx.x; c < TR * a.M; c += nthr) {
-            const int tok = c / TR, r = c % TR, orow = row0 + r;
-            if (orow >= a.N) continue;
+        // the group sums of (token, local row r) combined with the row's scales
+        auto combine = [&](int tok, int r) -> float {
             const int32_t *ap = acc_l + (tok * TR + r) * gld;
             const float *sp = sc_l + r * a.G;
             float t = 0.0f;
@@ -653,7 +666,22 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
                 t = fmaf((float)a4.w, sp[g + 3], t);
             }
             for (; g < a.G; ++g) t = fmaf((float)ap[g], sp[g], t);
-            float out = t * xs_l[tok];
+            return t;
+        };
+        if constexpr (GLU) {
+            constexpr int TH = TR / 2;
+            for (int c = threadIdx.x; c < TH * a.M; c += nthr) {
+                const int tok = c / TH, r = c % TH, orow = rb * RH * 16 + r;
+                if (orow >= 16 * glu_t) continue;
+                const float g = combine(tok, r) * xs_l[tok], u = combine(tok, r + TH) * xs_l[tok];
+                a.y[(size_t)tok * a.ldy + orow] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+            }
+            return;
+        }
+        for (int c = threadIdx.x; c < TR * a.M; c += nthr) {
+            const int tok = c / TR, r = c % TR, orow = row0 + r;
+            if (orow >= a.N) continue;
+            float out = combine(tok, r) * xs_l[tok];
             if (a.bias) out = out + gb_raw;
             a.y[(size_t)tok * a.ldy + orow] = out;
         }
@@ -695,19 +723,16 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
             }
         }
         if constexpr (!ACC) {
-            if (a.amax_v) {   // M = 1: lanes 0..15 (s = 0) hold the tile's rows; the tile's first largest
-                float bv = s == 0 && out0 == out0 ? out0 : -INFINITY;
-                int bi = s == 0 && row_ok ? row : 0x7fffffff;
+            if (a.amax_key) {   // M = 1: lanes 0..15 (s = 0) hold the tile's rows; the tile's first largest
+                unsigned long long key = eif_argmax_key(s == 0 ? out0 : -INFINITY, s == 0 && row_ok ? row : 0x7fffffff);
 #pragma unroll
                 for (int off = 1; off < 16; off <<= 1) {
-                    const float ov = __shfl_xor(bv, off, 64);
-                    const int oi = __shfl_xor(bi, off, 64);
-                    if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+                    const unsigned long long ok = __shfl_xor(key, off, 64);
+                    key = ok > key ? ok : key;
                 }
-                if (lane == 0) {
-                    a.amax_v[rb * RT + rt] = bv;
-                    a.amax_i[rb * RT + rt] = bi;
-                }
+                if (lane == 0)
+                    __hip_atomic_fetch_max(a.amax_key + (size_t)kArgmaxStride * ((rb * RT + rt) % kArgmaxSlots), key,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
@@ -955,19 +980,16 @@ __global__ __launch_bounds__(kRowPairThreads) void qrowpair_kernel(const int8_t 
         }
     }
     if constexpr (!ACC) {
-        if (a.amax_v) {
-            float bv = out == out ? out : -INFINITY;
-            int bi = row_ok ? orow : 0x7fffffff;
+        if (a.amax_key) {
+            unsigned long long key = eif_argmax_key(out, row_ok ? orow : 0x7fffffff);
 #pragma unroll
             for (int off = 4; off < 64; off <<= 1) {
-                const float ov = __shfl_xor(bv, off, 64);
-                const int oi = __shfl_xor(bi, off, 64);
-                if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+                const unsigned long long ok = __shfl_xor(key, off, 64);
+                key = ok > key ? ok : key;
             }
-            if (lane == 0) {
-                a.amax_v[tile] = bv;
-                a.amax_i[tile] = bi;
-            }
+            if (lane == 0)
+                __hip_atomic_fetch_max(a.amax_key + (size_t)kArgmaxStride * (tile % kArgmaxSlots), key, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -1336,6 +1358,34 @@ int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipSt
     return EIF_HIP_OK;
 }
 
+// The gated form (qgemv_kernel's GLU): fused prep, ternary g128 layout, four row tiles per workgroup (two gate,
+// two up), `half` output rows. E and the waves per tile follow launch_gemv_tiles' rules.
+constexpr int kGluRT = 4;
+
+template <int E, int SPW, int LB>
+int launch_glu_s(const QArgs &a, const PrepArgs &p, int half, int ks, hipStream_t st)
+{
+    const size_t lds = gemv_lds_bytes(true, a, p.ldl, kGluRT, ks);
+    GemvHot h;
+    if (!gemv_hot(a, p, true, false, ks, &h)) return EIF_HIP_E_LIMIT;
+    h.i1 |= half / 16;   // bits 0..26: the tiles of one half
+    qgemv_kernel<kTern, 4, true, false, E, SPW, LB, kGluRT, 1, false, true><<<half / (16 * kGluRT / 2), 64 * kGluRT * ks,
+                                                                              lds, st>>>(
+        h.r0, h.r1, h.r2, h.r3, a.W, a.wld, a.nsteps, h.i0, h.i1, a, p);
+    EIF_HIP_LAUNCHED();
+    return EIF_HIP_OK;
+}
+
+template <int E, int LB>
+int launch_glu_e(const QArgs &a, const PrepArgs &p, int half, int ks, hipStream_t st)
+{
+    const int steps = eif_ceil_div(a.nsteps, ks);
+    if (steps <= 1) return launch_glu_s<E, 1, LB>(a, p, half, ks, st);
+    if (steps <= 2) return launch_glu_s<E, 2, LB>(a, p, half, ks, st);
+    if (steps <= 4) return launch_glu_s<E, 4, LB>(a, p, half, ks, st);
+    return launch_glu_s<E, 8, LB>(a, p, half, ks, st);
+}
+
 // The shares-combining form (one row, ternary weights, E = 4 or 8, one row tile per workgroup, one step per
 // wave held at once).
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
@@ -1491,7 +1541,7 @@ int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t s
     if constexpr (FMT == kTern || GROUPED) {
         return 1;
     } else {
-        if (g_gemv_stream < 0 || p.x || p.sh_ml || a.amax_v || a.M > 32 || rows_pad / 16 < kBigTiles) return 1;
+        if (g_gemv_stream < 0 || p.x || p.sh_ml || a.amax_key || a.M > 32 || rows_pad / 16 < kBigTiles) return 1;
         if (a.M < 4 && g_gemv_stream == 0) return 1;   // up to 3 token rows: the tiled GEMV measured as fast or faster
         if (a.M <= 16) {
             if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 1>(a, rows_pad, st);
@@ -1759,20 +1809,20 @@ int qweight_view(const eif_hip_qweight *w, QView *v)
     return EIF_HIP_OK;
 }
 
-// Row-scaled GEMV of one prepped token row with, per 16-row tile, the largest output and its row (first of
-// equal maxima) in amax_v / amax_i [qweight_row_tiles(w)]: the greedy argmax's first stage.
-int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y, float *amax_v,
-                   int *amax_i, hipStream_t st)
+// Row-scaled GEMV of one prepped token row that also folds the largest output and its first row into amax_key
+// (atomic max of eif_argmax_key over the 16-row tiles into kArgmaxSlots slots, kArgmaxStride keys apart): the
+// greedy argmax is the largest slot. The slots must hold 0 (or smaller keys) before the launch.
+int qlinear_argmax(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, float *y,
+                   unsigned long long *amax_key, hipStream_t st)
 {
     int rc = check_linear_args(w, xq, ldq, 1);
     if (rc) return rc;
-    if (!xs || !y || !amax_v || !amax_i || (w->fmt == kTern && w->group > 0)) return EIF_HIP_E_ARG;
+    if (!xs || !y || !amax_key || (w->fmt == kTern && w->group > 0)) return EIF_HIP_E_ARG;
     QArgs a = make_args(w, xq, ldq, 1);
     a.xs = xs;
     a.y = y;
     a.ldy = w->rows;
-    a.amax_v = amax_v;
-    a.amax_i = amax_i;
+    a.amax_key = amax_key;
     rc = gemv_rowscaled(w, a, st);
     return rc == 1 ? EIF_HIP_E_LIMIT : rc;
 }
@@ -1881,6 +1931,38 @@ extern "C" int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep
         }
     }
     return dispatch<false>(w, a, p, EIF_HIP_PATH_GEMV, st);
+}
+
+// y[m, r] = SiLU(gate_r) * up_r for r < rows / 2 (gate = rows 0 .. rows/2 - 1 of w, up = the rest), one GEMV launch
+// with the prep fused (qgemv_kernel's GLU form).
+extern "C" int eif_hip_qlinear_prep_glu(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, float *y, int ldy,
+                                        int M, void *stream)
+{
+    PrepArgs p;
+    int rc = make_prep_spec(w, spec, M, &p);
+    if (rc) return rc;
+    const int half = w->rows / 2;
+    if (!y || ldy < half || w->rows % 2) return EIF_HIP_E_ARG;
+    // the form's shapes: ternary g128, whole pairs of gate tiles per workgroup, the WHT-128 or none
+    if (w->fmt != kTern || w->group != 128 || half % (16 * kGluRT / 2) || (p.block != 128 && p.block != 0))
+        return EIF_HIP_E_LIMIT;
+    QArgs a = make_args(w, nullptr, 0, M);
+    a.y = y;
+    a.ldy = ldy;
+    p.ldl = a.nsteps * Geo<kTern, 4>::SC + 16;
+    const int kpad = a.nsteps * Geo<kTern, 4>::SC, maxks = 16 / kGluRT;
+    int ks = std::min(g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(w->rows_pad / 16, a.nsteps), maxks);
+    const hipStream_t st = (hipStream_t)stream;
+    for (int e = 4; e <= 8; e *= 2) {
+        if (64 * e < p.block || e < g_gemv_prep_cols) continue;
+        int k = ks;
+        while (k < maxks && (64 * kGluRT * k * e < kpad || a.G > gemv_scl<kTern, 4, true>() * 4 * k)) ++k;
+        if (64 * kGluRT * k * e < kpad || a.G > gemv_scl<kTern, 4, true>() * 4 * k) continue;
+        if (gemv_lds_bytes(true, a, p.ldl, kGluRT, k) > gemv_max_lds()) return EIF_HIP_E_LIMIT;
+        if (e == 4) return p.block == 128 ? launch_glu_e<4, 7>(a, p, half, k, st) : launch_glu_e<4, 0>(a, p, half, k, st);
+        return p.block == 128 ? launch_glu_e<8, 7>(a, p, half, k, st) : launch_glu_e<8, 0>(a, p, half, k, st);
+    }
+    return EIF_HIP_E_LIMIT;
 }
 
 extern "C" int eif_hip_prep_spec_rows(const eif_hip_prep_spec *spec, int K, int8_t *xq, int ldq, float *xs, int M,

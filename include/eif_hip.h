@@ -145,6 +145,16 @@ typedef struct eif_hip_prep_spec {
 int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias, float *y,
                          int ldy, int M, void *stream);
 
+/* The gated FFN input of one layer in one launch: w stacks the gate projection (rows 0 .. rows/2 - 1) over the up
+ * projection (rows rows/2 .. rows - 1); y[m, r] = SiLU(g) * u = (g * (1 / (1 + expf(-g)))) * u for r < rows / 2,
+ * g and u the outputs eif_hip_qlinear_prep gives for rows r and rows/2 + r (src/eif_tinyllm.c:774-780). Fed to a
+ * down projection with EIF_HIP_PRE_RMS, these rows give the bits of EIF_HIP_PRE_SWIGLU_RMS on the two halves.
+ * M <= 8; a ternary g128 matrix whose half is a multiple of 32 rows, the WHT-128 or none; other shapes return
+ * EIF_HIP_E_LIMIT (use eif_hip_qlinear_prep and the SwiGLU pre-op). No counterpart in the reference, which
+ * computes the two halves and then SiLU(g) * u in its token loop.                                       */
+int eif_hip_qlinear_prep_glu(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, float *y, int ldy, int M,
+                             void *stream);
+
 /* The prep of a spec on its own, for any M (e.g. a prompt batch before the MFMA GEMM of eif_hip_qlinear):
  * M rows of K columns (K % 32 == 0) -> xq [M, ldq] int8 (ldq >= K, a multiple of 16, zeros past K) and
  * xs [M]. The codes and scales equal those the fused prep of eif_hip_qlinear_prep stages.              */

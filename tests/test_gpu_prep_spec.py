@@ -154,3 +154,51 @@ def test_vocab_head_two_step(gpu, oracle, fmt, N, K):
     fn(P(w), P(s), P(hq), qw.kpad, P(hs), None, P(oy), N, 1, N, K)
     assert np.array_equal(y1.view(np.uint32), oy.view(np.uint32))
     qw.close()
+
+
+@pytest.mark.parametrize("N,K,M", [(13824, 2560, 1), (512, 640, 3)])
+def test_glu_form(gpu, oracle, N, K, M):
+    """eif_hip_qlinear_prep_glu: SiLU(gate) * up of the stacked gate|up matrix in one launch. Fed to the next linear
+    with the RMSNorm pre-op, its rows give the bits of the two halves with the SwiGLU pre-op; against the two halves
+    it is the SwiGLU of src/eif_tinyllm.c:774-780 to float32 rounding."""
+    import torch
+    dev = torch.device("cuda:0")
+    lib = gpu.load()
+    h = N // 2
+    w, s = synth.ternary_weight((66, N, K), N, K, 128)
+    qw = gpu.QWeight(gpu.W_TERNARY, N, K, 128, w, s)
+    wd, sd = synth.ternary_weight((67, K, h), K, h, 128 if h % 128 == 0 else 64)
+    gd = 128 if h % 128 == 0 else 64
+    qd = gpu.QWeight(gpu.W_TERNARY, K, h, gd, wd, sd)
+    r = synth.rng(68, N, K)
+    x = torch.from_numpy(r.standard_normal((M, K)).astype(np.float32)).to(dev)
+    nw = torch.from_numpy((1.0 + 0.1 * r.standard_normal(K)).astype(np.float32)).to(dev)
+    nw2 = torch.from_numpy((1.0 + 0.1 * r.standard_normal(h)).astype(np.float32)).to(dev)
+    sp = gpu.prep_spec(x, pre=1, norm_w=nw, eps=1e-5, block=128, norm=gpu.wht_norm(128))
+    yg = torch.full((M, h), float("nan"), dtype=torch.float32, device=dev)
+    gpu.check(lib.eif_hip_qlinear_prep_glu(qw.h, C.byref(sp), gpu.ptr(yg), h, M, gpu.stream_ptr()),
+              "eif_hip_qlinear_prep_glu")
+    y2 = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    gpu.check(lib.eif_hip_qlinear_prep(qw.h, C.byref(sp), None, gpu.ptr(y2), N, M, gpu.stream_ptr()),
+              "eif_hip_qlinear_prep")
+    torch.cuda.synchronize()
+    g, u = y2[:, :h].cpu().numpy(), y2[:, h:].cpu().numpy()
+    want = (g * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g)))) * u
+    got = yg.cpu().numpy()
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-30 + 1e-6 * np.abs(want).max())) <= 1e-5
+    # the down projection: RMSNorm pre-op on the GLU rows == SwiGLU pre-op on the two halves, bit for bit
+    blk = 128 if h % 128 == 0 else 64
+    ya = torch.full((M, K), float("nan"), dtype=torch.float32, device=dev)
+    yb = torch.full((M, K), float("nan"), dtype=torch.float32, device=dev)
+    spa = gpu.prep_spec(yg, pre=1, norm_w=nw2, eps=1e-5, block=blk, norm=gpu.wht_norm(blk))
+    spb = gpu.prep_spec(y2[:, :h], pre=2, x2=y2[:, h:], norm_w=nw2, eps=1e-5, block=blk, norm=gpu.wht_norm(blk))
+    gpu.check(lib.eif_hip_qlinear_prep(qd.h, C.byref(spa), None, gpu.ptr(ya), K, M, gpu.stream_ptr()), "down a")
+    gpu.check(lib.eif_hip_qlinear_prep(qd.h, C.byref(spb), None, gpu.ptr(yb), K, M, gpu.stream_ptr()), "down b")
+    torch.cuda.synchronize()
+    assert np.array_equal(ya.cpu().numpy().view(np.uint32), yb.cpu().numpy().view(np.uint32))
+    # a shape outside the form is refused (the caller takes the two-step path)
+    w3, s3 = synth.ternary_weight((69, 96, K), 96, K, 128)
+    q3 = gpu.QWeight(gpu.W_TERNARY, 96, K, 128, w3, s3)
+    assert lib.eif_hip_qlinear_prep_glu(q3.h, C.byref(sp), gpu.ptr(yg), h, M, gpu.stream_ptr()) == -4   # LIMIT
+    for q in (qw, qd, q3):
+        q.close()
