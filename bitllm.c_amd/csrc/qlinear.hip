@@ -346,8 +346,13 @@ constexpr int kGemvMaxTT = 4;    // token tiles per workgroup
 // slower than 32-row chunks on every shape tried.
 constexpr int kGemvDefaultWgM = 32;
 constexpr int kFusedMaxM = 8;    // token rows of the fused-prep GEMV (each workgroup preps them one by one)
-constexpr int kMaxPieces = 4;
+constexpr int kMaxPieces = 8;   // 16-byte pieces of the staged int8 rows per thread (a count read at run time)
 constexpr int kMaxScLoads = 8;
+
+// Group sums staged in LDS as int16 where they fit: |sum| <= 128 * group <= 16384 for groups up to 128 columns
+// (UD <= 4). That halves their LDS and lets 16 token rows of the g96 2560x6912 down projection fit one workgroup.
+template <int FMT, int UD>
+constexpr bool gemv_gs16() { return FMT == kTern && UD <= 4; }
 
 // Scale loads per thread of the GEMV's group scales (a fixed count, so the waits count loads exactly): two for the
 // BitNet layouts (g96, g128: up to 8 x the waves' groups per row), kMaxScLoads for the other group sizes.
@@ -434,19 +439,21 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
 
     // 1. activation loads (preloaded pointers only)
     float v[EV], sg[EV], v2[EV], nwv[EV];
-    int4 pc0, pc1, pc2, pc3;   // up to kMaxPieces 16-byte pieces of the int8 rows per thread
+    v4i pc[kMaxPieces];   // the thread's 16-byte pieces of the int8 rows (np of them; a native vector type: an
+                          // array of it stays in registers)
     const int pieces = kpad / 16;
-    auto piece_at = [&](int i) -> const int4 * {
+    const int np = E == 0 ? (a.M * pieces + nthr - 1) / nthr : 0;
+    auto piece_at = [&](int i) -> const v4i * {
         const int idx = threadIdx.x + i * nthr;
         const int ic = idx < a.M * pieces ? idx : a.M * pieces - 1;
         const int m = ic / pieces, c = ic - m * pieces;
-        return reinterpret_cast<const int4 *>(a.xq + (size_t)m * a.ldq + 16 * c);
+        return reinterpret_cast<const v4i *>(a.xq + (size_t)m * a.ldq + 16 * c);
     };
-    auto piece_store = [&](int i, const int4 &val) {
+    auto piece_store = [&](int i, const v4i &val) {
         const int idx = threadIdx.x + i * nthr;
         if (idx < a.M * pieces) {
             const int m = idx / pieces, c = idx - m * pieces;
-            *reinterpret_cast<int4 *>(lds_x + m * p.ldl + 16 * c) = val;
+            *reinterpret_cast<v4i *>(lds_x + m * p.ldl + 16 * c) = val;
         }
     };
     float xs_v = 0.0f;
@@ -459,10 +466,9 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
         prep_load_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
                           static_cast<const float *>(r2), static_cast<const float *>(r3), i0, v, sg, v2, nwv);
     } else {
-        pc0 = *piece_at(0);
-        pc1 = *piece_at(1);
-        pc2 = *piece_at(2);
-        pc3 = *piece_at(3);
+#pragma unroll
+        for (int i = 0; i < kMaxPieces; ++i)
+            if (i < np) pc[i] = *piece_at(i);   // a uniform count: the loads after these stay fixed in number
         xs_v = a.xs[(int)threadIdx.x < a.M ? threadIdx.x : 0];
     }
 
@@ -493,9 +499,10 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     // activation and weight loads are in flight.
     __builtin_amdgcn_sched_barrier(0);
     const bool row_ok = row < a.N;
-    const int gld = (a.G + 3) & ~3;
+    using GS = std::conditional_t<gemv_gs16<FMT, UD>(), int16_t, int32_t>;   // staged group sums
+    const int gld = gemv_gs16<FMT, UD>() ? (a.G + 7) & ~7 : (a.G + 3) & ~3;   // 16-byte rows of sums
     int32_t *red = reinterpret_cast<int32_t *>(smem + a.M * p.ldl);
-    int32_t *acc_l = red;
+    GS *acc_l = reinterpret_cast<GS *>(red);
     float *sc_l = reinterpret_cast<float *>(acc_l + a.M * TR * gld);
     constexpr int SCL = gemv_scl<FMT, UD, GROUPED>();
     float scv[SCL];
@@ -537,10 +544,9 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
             prep_finish<E, LB>(p, m, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
         }
     } else {
-        piece_store(0, pc0);
-        piece_store(1, pc1);
-        piece_store(2, pc2);
-        piece_store(3, pc3);
+#pragma unroll
+        for (int i = 0; i < kMaxPieces; ++i)
+            if (i < np) piece_store(i, pc[i]);
         if ((int)threadIdx.x < a.M) xs_l[threadIdx.x] = xs_v;
         __syncthreads();
     }
@@ -573,7 +579,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
                 const int8_t *xl = lds_x + (tok_ok ? tb + r16 : 0) * p.ldl;
                 if constexpr (FMT == kTern) {
                     const int ntok = min(4, a.M - tb - 4 * s);
-                    int32_t *accp = acc_l + ((tb + 4 * s) * TR + 16 * rt + r16) * gld;
+                    GS *accp = acc_l + ((tb + 4 * s) * TR + 16 * rt + r16) * gld;
                     auto group = [&](auto grp_c) __attribute__((always_inline)) {
                         constexpr int grp = decltype(grp_c)::value;
                         long aop[UD];
@@ -595,10 +601,10 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
                                                 a.acc[((size_t)(tb + 4 * s + vv) * a.N + row) * a.G + gi] = c[vv] >> GE::SHIFT;
                                     }
                                 } else {
-                                    accp[gi] = c[0] >> GE::SHIFT;
+                                    accp[gi] = (GS)(c[0] >> GE::SHIFT);
 #pragma unroll
                                     for (int vv = 1; vv < 4; ++vv)
-                                        if (vv < ntok) accp[vv * TR * gld + gi] = c[vv] >> GE::SHIFT;
+                                        if (vv < ntok) accp[vv * TR * gld + gi] = (GS)(c[vv] >> GE::SHIFT);
                                 }
                             }
                         } else {
@@ -628,8 +634,17 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
         __syncthreads();
         // the group sums of (token, local row r) combined with the row's scales
         auto combine = [&](int tok, int r) -> float {
-            const int32_t *ap = acc_l + (tok * TR + r) * gld;
+            const GS *ap = acc_l + (tok * TR + r) * gld;
             const float *sp = sc_l + r * a.G;
+            // four groups' sums as one 8-byte (int16) or 16-byte (int32) LDS load
+            auto sums4 = [&](int g) {
+                if constexpr (gemv_gs16<FMT, UD>()) {
+                    const int2 h = *reinterpret_cast<const int2 *>(ap + g);
+                    return int4{(int)(int16_t)(h.x & 0xFFFF), h.x >> 16, (int)(int16_t)(h.y & 0xFFFF), h.y >> 16};
+                } else {
+                    return *reinterpret_cast<const int4 *>(ap + g);
+                }
+            };
             float t = 0.0f;
             int g = 0;
             if ((a.G & 3) == 0) {   // the row's scales 16-byte aligned: 16 groups' sums and scales per LDS round trip
@@ -638,7 +653,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
                     float4 sv[4];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        av[q] = *reinterpret_cast<const int4 *>(ap + g + 4 * q);
+                        av[q] = sums4(g + 4 * q);
                         sv[q] = *reinterpret_cast<const float4 *>(sp + g + 4 * q);
                     }
 #pragma unroll
@@ -650,7 +665,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
                     }
                 }
                 for (; g + 4 <= a.G; g += 4) {
-                    const int4 a4 = *reinterpret_cast<const int4 *>(ap + g);
+                    const int4 a4 = sums4(g);
                     const float4 s4 = *reinterpret_cast<const float4 *>(sp + g);
                     t = fmaf((float)a4.x, s4.x, t);
                     t = fmaf((float)a4.y, s4.y, t);
@@ -659,7 +674,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
                 }
             }
             for (; g + 4 <= a.G; g += 4) {
-                const int4 a4 = *reinterpret_cast<const int4 *>(ap + g);
+                const int4 a4 = sums4(g);
                 t = fmaf((float)a4.x, sp[g], t);
                 t = fmaf((float)a4.y, sp[g + 1], t);
                 t = fmaf((float)a4.z, sp[g + 2], t);
@@ -1282,10 +1297,11 @@ int gemv_tt(const QArgs &a)
 
 // Dynamic LDS of qgemv_kernel: the staged int8 rows, then the group sums and scales (grouped) or the K-split
 // partials (row-scaled).
-size_t gemv_lds_bytes(bool grouped, const QArgs &a, int ldl, int rt, int ks)
+size_t gemv_lds_bytes(bool grouped, bool gs16, const QArgs &a, int ldl, int rt, int ks)
 {
-    const size_t tr = 16 * (size_t)rt, gld = (size_t)((a.G + 3) & ~3), m = (size_t)gemv_wg_m(a);
-    const size_t tail = grouped ? (m * tr * gld + tr * (size_t)a.G) * 4
+    const size_t tr = 16 * (size_t)rt, m = (size_t)gemv_wg_m(a);
+    const size_t gld = (size_t)(gs16 ? (a.G + 7) & ~7 : (a.G + 3) & ~3), gsb = gs16 ? 2 : 4;
+    const size_t tail = grouped ? m * tr * gld * gsb + tr * (size_t)a.G * 4
                                 : (size_t)(ks - 1) * rt * gemv_tt(a) * 4 * 64 * 4;
     return m * ldl + tail;
 }
@@ -1347,7 +1363,7 @@ bool gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares, int ks
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT>
 int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
-    const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
+    const size_t lds = gemv_lds_bytes(GROUPED, gemv_gs16<FMT, UD>(), a, p.ldl, RT, ks);
     QArgs ag = a;
     const int grid = gemv_grid(ag, rows_pad / (16 * RT));
     GemvHot h;
@@ -1365,7 +1381,7 @@ constexpr int kGluRT = 4;
 template <int E, int SPW, int LB>
 int launch_glu_s(const QArgs &a, const PrepArgs &p, int half, int ks, hipStream_t st)
 {
-    const size_t lds = gemv_lds_bytes(true, a, p.ldl, kGluRT, ks);
+    const size_t lds = gemv_lds_bytes(true, true, a, p.ldl, kGluRT, ks);
     GemvHot h;
     if (!gemv_hot(a, p, true, false, ks, &h)) return EIF_HIP_E_LIMIT;
     h.i1 |= half / 16;   // bits 0..26: the tiles of one half
@@ -1392,7 +1408,7 @@ template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
 int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
     if constexpr (FMT == kTern && !ACC && (E == 4 || E == 8) && RT == 1) {
-        const size_t lds = gemv_lds_bytes(GROUPED, a, p.ldl, RT, ks);
+        const size_t lds = gemv_lds_bytes(GROUPED, gemv_gs16<FMT, UD>(), a, p.ldl, RT, ks);
         GemvHot h;
         if (!gemv_hot(a, p, true, true, ks, &h)) return EIF_HIP_E_LIMIT;
         qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true><<<rows_pad / 16, 64 * ks, lds, st>>>(
@@ -1449,7 +1465,10 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
 {
     const int kpad = a.nsteps * Geo<FMT, UD>::SC;
     const int maxks = 16 / rt;
-    int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(rows_pad / 16, a.nsteps);
+    // fused prep over four row tiles: four steps per wave (the row's coverage by the prep raises it as needed);
+    // fewer waves measured faster there (gate+up 13824x2560 at one token 6.70 us with 12 waves, 6.96 with 16)
+    int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit
+                               : (p.x && rt == 4 ? eif_ceil_div(a.nsteps, 4) : pick_ks_gemv(rows_pad / 16, a.nsteps));
     if (!GROUPED && !p.x && rows_pad / 16 >= kBigTiles && g_gemv_ksplit <= 0) {
         // row-scaled, many tiles, prepped activations: about 10 KiB of weights per wave
         const int row_bytes = a.nsteps * 4 * Geo<FMT, UD>::SB;
@@ -1458,7 +1477,7 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     }
     if (ks > maxks) ks = maxks;
     auto scales_fit = [&](int k) { return !GROUPED || ACC || a.G <= gemv_scl<FMT, UD, GROUPED>() * 4 * k; };
-    auto lds_fit = [&](int k) { return gemv_lds_bytes(GROUPED, a, p.ldl, rt, k) <= gemv_max_lds(); };
+    auto lds_fit = [&](int k) { return gemv_lds_bytes(GROUPED, gemv_gs16<FMT, UD>(), a, p.ldl, rt, k) <= gemv_max_lds(); };
     if (p.x) {
         // E columns per thread: the fewest that let at most 16 waves cover the padded row, and a WHT block within
         // one wave. The prep is a chain of dependent steps per wave (cross-lane butterflies, reductions), so the
@@ -1480,8 +1499,12 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     }
     const int wm = gemv_wg_m(a);
     if (wm > kGemvTileM * kGemvMaxTT) return 1;
-    while (ks < maxks && (wm * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks))) ++ks;
-    if (wm * (kpad / 16) > kMaxPieces * 64 * rt * ks || !scales_fit(ks) || !lds_fit(ks)) return 1;
+    // pieces per thread: kMaxPieces for one token tile (16 rows of the long down projections fit), 4 for more
+    // rows, so that a 32-row batch of the layer shapes runs as two 16-row chunks (two workgroups a row block):
+    // ternary 6912x2560 at 32 tokens 12.7 us as one 32-row chunk, 8.9 as two
+    const int maxp = wm <= kGemvTileM ? kMaxPieces : 4;
+    while (ks < maxks && (wm * (kpad / 16) > maxp * 64 * rt * ks || !scales_fit(ks))) ++ks;
+    if (wm * (kpad / 16) > maxp * 64 * rt * ks || !scales_fit(ks) || !lds_fit(ks)) return 1;
     switch (gemv_tt(a)) {
     case 1: return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0, 1>(a, p, rows_pad, rt, ks, st);
     case 2: return launch_gemv_rt<FMT, UD, GROUPED, ACC, 0, 0, 2>(a, p, rows_pad, rt, ks, st);
@@ -1736,17 +1759,24 @@ int check_linear_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M
 // Whether one GEMV workgroup can stage a full token tile (16 rows) of the weight's activations and sums.
 bool gemv_fits_tile(const eif_hip_qweight *w)
 {
-    const bool grouped = w->fmt == kTern && w->group > 0;
-    const size_t m = kGemvTileM, ldl = (size_t)w->kpad + 16, gld = (size_t)((w->ngroups + 3) & ~3);
-    const size_t lds = m * ldl + (grouped ? (m * 16 * gld + 16 * (size_t)w->ngroups) * 4 : 0);
+    const bool grouped = w->fmt == kTern && w->group > 0, gs16 = w->fmt == kTern && w->ud <= 4;
+    const size_t m = kGemvTileM, ldl = (size_t)w->kpad + 16;
+    const size_t gld = (size_t)(gs16 ? (w->ngroups + 7) & ~7 : (w->ngroups + 3) & ~3), gsb = gs16 ? 2 : 4;
+    const size_t lds = m * ldl + (grouped ? m * 16 * gld * gsb + 16 * (size_t)w->ngroups * 4 : 0);
     return m * (size_t)(w->kpad / 16) <= (size_t)kMaxPieces * 1024 && lds <= gemv_max_lds();
 }
 
-// Auto path: the GEMV up to kFusedMaxM tokens; below eif_hip_gemm_min_tokens() also where a token tile fits one
-// workgroup and the batch is at most two tiles, or the matrix has under 32 tiles of 64 rows (few GEMM
-// workgroups, each with a long chain along K); else the GEMM. Measured at 48 and 63 tokens: ternary 3840x2560
-// GEMV 8.5 / 8.5 us, GEMM 6.5 / 6.5; 2560x2560 6.5 / 8.3 against 6.1 / 6.1; INT4 3584x1024 5.6 / 5.7 against
-// 4.7 / 4.7; INT4 1024x3584 5.5 / 5.5 against 6.3 / 6.6.
+// Auto path (measured on MI355X, weights rotated past the Infinity Cache; us, GEMV / GEMM):
+// * up to kFusedMaxM tokens: the GEMV;
+// * 9 .. 16 tokens: the GEMV where a 16-row token tile fits one workgroup (every BitNet, INT8 and INT4 layer
+//   shape: ternary 3840x2560 5.5 / 6.2, 6912x2560 7.0 / 7.5, g96 2560x6912 9.0 / 8.6, INT8 896x4864 7.0 / 7.8);
+// * 17 .. 63 tokens, row-scaled matrices (INT8, INT4): the GEMV up to 32 tokens, and above that for matrices of
+//   fewer than 32 tiles of 64 rows (INT8 896x4864 at 48 / 63 tokens 7.8 / 7.6 against 8.2 / 9.4; INT4 1024x3584
+//   6.1 / 6.0 against 6.3 / 6.7; INT4 3584x1024 at 48 tokens 6.3 against 4.7);
+// * 17 .. 63 tokens, group-scaled ternary: the GEMM. The GEMV streams the weights once per 16- or 32-row token
+//   chunk and stages every chunk's int8 rows and group sums in LDS, and at these batches it lost on every layer
+//   shape (32 tokens: 3840x2560 7.5 / 6.3, 6912x2560 8.0 / 7.6, g96 2560x6912 17.3 / 9.6; 48 tokens:
+//   10.6 / 6.4, 13.5 / 8.4, 17.6 / 10.7), so the dense contraction takes them below the 64-token line.
 constexpr int kGemvFewRows = 32 * 64;
 
 int resolve_path(const eif_hip_qweight *w, int path, int M)
@@ -1754,8 +1784,10 @@ int resolve_path(const eif_hip_qweight *w, int path, int M)
     if (path != EIF_HIP_PATH_AUTO) return path;
     if (M >= g_gemm_min_tokens) return EIF_HIP_PATH_GEMM;
     if (M <= kFusedMaxM) return EIF_HIP_PATH_GEMV;
-    return gemv_fits_tile(w) && (M <= 2 * kGemvTileM || w->rows_pad < kGemvFewRows) ? EIF_HIP_PATH_GEMV
-                                                                                     : EIF_HIP_PATH_GEMM;
+    if (!gemv_fits_tile(w)) return EIF_HIP_PATH_GEMM;
+    if (M <= kGemvTileM) return EIF_HIP_PATH_GEMV;
+    const bool grouped = w->fmt == kTern && w->group > 0;
+    return !grouped && (M <= 2 * kGemvTileM || w->rows_pad < kGemvFewRows) ? EIF_HIP_PATH_GEMV : EIF_HIP_PATH_GEMM;
 }
 
 QArgs make_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
@@ -1951,14 +1983,14 @@ extern "C" int eif_hip_qlinear_prep_glu(const eif_hip_qweight *w, const eif_hip_
     a.ldy = ldy;
     p.ldl = a.nsteps * Geo<kTern, 4>::SC + 16;
     const int kpad = a.nsteps * Geo<kTern, 4>::SC, maxks = 16 / kGluRT;
-    int ks = std::min(g_gemv_ksplit > 0 ? g_gemv_ksplit : pick_ks_gemv(w->rows_pad / 16, a.nsteps), maxks);
+    int ks = std::min(g_gemv_ksplit > 0 ? g_gemv_ksplit : eif_ceil_div(a.nsteps, 4), maxks);   // as launch_gemv_tiles
     const hipStream_t st = (hipStream_t)stream;
     for (int e = 4; e <= 8; e *= 2) {
         if (64 * e < p.block || e < g_gemv_prep_cols) continue;
         int k = ks;
         while (k < maxks && (64 * kGluRT * k * e < kpad || a.G > gemv_scl<kTern, 4, true>() * 4 * k)) ++k;
         if (64 * kGluRT * k * e < kpad || a.G > gemv_scl<kTern, 4, true>() * 4 * k) continue;
-        if (gemv_lds_bytes(true, a, p.ldl, kGluRT, k) > gemv_max_lds()) return EIF_HIP_E_LIMIT;
+        if (gemv_lds_bytes(true, true, a, p.ldl, kGluRT, k) > gemv_max_lds()) return EIF_HIP_E_LIMIT;
         if (e == 4) return p.block == 128 ? launch_glu_e<4, 7>(a, p, half, k, st) : launch_glu_e<4, 0>(a, p, half, k, st);
         return p.block == 128 ? launch_glu_e<8, 7>(a, p, half, k, st) : launch_glu_e<8, 0>(a, p, half, k, st);
     }

@@ -54,7 +54,9 @@ TERN_GROUPED = [
     (64, 512, 256, 2, GEMV),
     (6912, 2560, 128, 16, GEMV),    # 9 .. 63 tokens: the GEMV in token chunks
     (3840, 2560, 128, 32, GEMV),
-    (2560, 6912, 96, 63, GEMV),     # g96 down: 8-row chunks (16 rows of sums do not fit the LDS)
+    (2560, 6912, 96, 16, GEMV),     # g96 down: one 16-row token tile per workgroup (int16 group sums in LDS)
+    (2560, 6912, 96, 32, GEMV),     #   two 16-row chunks
+    (2560, 6912, 96, 63, GEMV),     #   four chunks, the last of 15 rows
     (130, 200, 32, 63, GEMV),
     (70, 640, 64, 17, GEMV),
     (70, 640, 64, 17, GEMM),
@@ -236,6 +238,7 @@ def test_ternary_rowscale_bit_exact(gpu, oracle, N, K, M, path, with_bias):
     ("int8", 4864, 896, 1, GEMV), ("int8", 896, 4864, 1, GEMV), ("int8", 128, 896, 3, GEMV),
     ("int8", 4864, 896, 128, GEMM), ("int8", 77, 100, 20, GEMM),
     ("int8", 4864, 896, 32, GEMV), ("int8", 896, 4864, 63, GEMV), ("int8", 77, 100, 20, GEMV),
+    ("int8", 896, 4864, 16, GEMV), ("int8", 896, 4864, 32, GEMV),   # 16 staged rows of 4864 columns: 8 pieces a thread
     ("int4", 3584, 1024, 1, GEMV), ("int4", 1024, 3584, 1, GEMV), ("int4", 3584, 1024, 32, GEMM),
     ("int4", 3584, 1024, 32, GEMV), ("int4", 1024, 3584, 16, GEMV),
     ("int4", 50, 333, 4, GEMV), ("int4", 50, 333, 40, GEMM), ("int4", 50, 333, 40, GEMV),
