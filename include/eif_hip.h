@@ -117,7 +117,7 @@ int eif_hip_qlinear_f32_acc(const eif_hip_qweight *w, const float *x, int ldx, c
  *   EIF_HIP_PRE_NONE        the rows as given;
  *   EIF_HIP_PRE_RMS         RMSNorm: (x * (1 / sqrtf(sum(x^2) / K + eps))) * norm_w, the decoder's pre-norm
  *                           (src/eif_tinyllm.c:196-330, weight NULL = 1);
- *   EIF_HIP_PRE_SWIGLU_RMS  h = (x * (1 / (1 + expf(-x)))) * x2 (SiLU gate times up, src/eif_tinyllm.c:774-780), then
+ *   EIF_HIP_PRE_SWIGLU_RMS  h = (x * (1 / (1 + expf(-x)))) * x2 (SiLU gate times up, src/eif_tinyllm.c:776-780), then
  *                           RMSNorm of h (the BitNet sub-norm before the down projection).            */
 #define EIF_HIP_PRE_NONE 0
 #define EIF_HIP_PRE_RMS 1
@@ -139,7 +139,7 @@ typedef struct eif_hip_prep_spec {
  * matrix of 65536 rows or more at M = 1, e.g. a vocabulary head: a prep launch, then the GEMV of the prepped row,
  * with the same output bits); the bias may then be the residual stream itself (y == bias: each output reads its
  * own bias element first). More rows (a prompt batch): the prep of eif_hip_prep_spec_rows into a per-stream
- * workspace, then eif_hip_qlinear on the auto path (the streaming GEMV below 64 rows, the int8-MFMA GEMM from 64),
+ * workspace, then eif_hip_qlinear on the auto path (the GEMV or the int8-MFMA GEMM by token count and shape),
  * the same bits as those two calls; the bias must not overlap y, and a stream's first such call must be made
  * outside graph capture (it allocates the workspace; inside a capture it returns EIF_HIP_E_LIMIT).      */
 int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec, const float *bias, float *y,
@@ -147,7 +147,7 @@ int eif_hip_qlinear_prep(const eif_hip_qweight *w, const eif_hip_prep_spec *spec
 
 /* The gated FFN input of one layer in one launch: w stacks the gate projection (rows 0 .. rows/2 - 1) over the up
  * projection (rows rows/2 .. rows - 1); y[m, r] = SiLU(g) * u = (g * (1 / (1 + expf(-g)))) * u for r < rows / 2,
- * g and u the outputs eif_hip_qlinear_prep gives for rows r and rows/2 + r (src/eif_tinyllm.c:774-780). Fed to a
+ * g and u the outputs eif_hip_qlinear_prep gives for rows r and rows/2 + r (src/eif_tinyllm.c:776-780). Fed to a
  * down projection with EIF_HIP_PRE_RMS, these rows give the bits of EIF_HIP_PRE_SWIGLU_RMS on the two halves.
  * M <= 8; a ternary g128 matrix whose half is a multiple of 32 rows, the WHT-128 or none; other shapes return
  * EIF_HIP_E_LIMIT (use eif_hip_qlinear_prep and the SwiGLU pre-op). No counterpart in the reference, which

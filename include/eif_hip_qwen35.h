@@ -96,8 +96,8 @@ const eif_hip_qweight *eif_hip_qwen35_head(const eif_hip_qwen35 *m);
  * prefill_chunk calls it, :1067-1153): y [M, ldy] = the matrix of layer `layer`, kind EIF_Q35_* (EIF_Q35_HEAD: the
  * tied head), times the M FP32 rows of spec (device memory; the engine's Hadamard rotation either applied by the
  * caller, as prefill_chunk's had_rows does, or asked of the prep through spec->signs / wht_block), on the
- * INT8-activation contract: each row quantised to INT8 (absmax), then the streaming GEMV below 64 rows or the
- * int8-MFMA GEMM from 64 (eif_hip_qlinear_prep). EIF_HIP_E_ARG for a kind the layer lacks or an FP32 matrix. */
+ * INT8-activation contract: each row quantised to INT8 (absmax), then the GEMV or the int8-MFMA GEMM by token
+ * count and shape (eif_hip_qlinear_prep). EIF_HIP_E_ARG for a kind the layer lacks or an FP32 matrix. */
 int eif_hip_qwen35_linear_batch(const eif_hip_qwen35 *m, int layer, int kind, const eif_hip_prep_spec *spec,
                                 const float *bias, float *y, int ldy, int M, void *stream);
 /* Device copy of an FP32 vector of the norms region (norms, sub-norms, Hadamard signs) by its layout offset;
