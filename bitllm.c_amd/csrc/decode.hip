@@ -341,6 +341,12 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const int8_t *emb, cons
     for (int c = threadIdx.x; c < dim; c += blockDim.x) x[(size_t)i * dim + c] = (float)row[c] * sc;
 }
 
+// out = a * b over n floats (an RMSNorm weight times +-1 rotation signs: exact).
+__global__ void mul_rows_kernel(float *out, const float *a, const float *b, int n)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) out[i] = a[i] * b[i];
+}
+
 // Prefill: the residual stream x += y over n floats.
 __global__ void add_rows_kernel(float *x, const float *y, size_t n)
 {
@@ -434,6 +440,10 @@ struct eif_hip_bitnet {
     eif_hip_qweight *head = nullptr;
     std::vector<float *> rms_att, rms_ffn, rms_sub_att, rms_sub_ffn;
     float *rms_final = nullptr, *signs_dim = nullptr, *signs_q = nullptr, *signs_hidden = nullptr;
+    // Each RMSNorm weight times its input's rotation signs ((v w) s = v (w s) exactly for +-1 signs), so the
+    // fused prep of a token step reads one column multiplier instead of two; null where nothing is folded.
+    std::vector<float *> mul_att, mul_ffn, mul_sub_att, mul_sub_ffn;
+    bool fold_dim = false, fold_q = false, fold_hidden = false;   // signs present, all +-1, inputs rotated
     int8_t *emb = nullptr;
     float *emb_scale = nullptr;
     float *x = nullptr, *qkv = nullptr, *hb = nullptr, *logits = nullptr;
@@ -471,6 +481,41 @@ int enqueue_head(eif_hip_bitnet *m, hipStream_t st);
 
 int enqueue_head_gemv(eif_hip_bitnet *m, hipStream_t st);
 
+// The folded multipliers of layer l (eif_hip_bitnet::mul_att ...), made once its norm weights and the signs are
+// both set.
+int fold_signs(eif_hip_bitnet *m, int l)
+{
+    const eif_hip_bitnet_config &c = m->c;
+    struct Fold {
+        std::vector<float *> *dst;
+        const float *nw, *sg;
+        bool ok;
+        int n;
+    } const f[4] = {{&m->mul_att, m->rms_att[l], m->signs_dim, m->fold_dim, c.dim},
+                    {&m->mul_ffn, m->rms_ffn[l], m->signs_dim, m->fold_dim, c.dim},
+                    {&m->mul_sub_att, m->rms_sub_att[l], m->signs_q, m->fold_q, m->q_dim},
+                    {&m->mul_sub_ffn, m->rms_sub_ffn[l], m->signs_hidden, m->fold_hidden, c.hidden}};
+    for (const Fold &d : f) {
+        if (!d.ok || !d.nw || !d.sg || (*d.dst)[l]) continue;
+        float *out = nullptr;
+        if (hipMalloc(&out, sizeof(float) * d.n) != hipSuccess) return EIF_HIP_E_NOMEM;
+        mul_rows_kernel<<<(d.n + 255) / 256, 256>>>(out, d.nw, d.sg, d.n);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+            (void)hipFree(out);
+            return EIF_HIP_E_DEVICE;
+        }
+        (*d.dst)[l] = out;
+    }
+    return EIF_HIP_OK;
+}
+
+// A prep spec's norm weight and signs: the folded multiplier where there is one.
+void spec_norm(eif_hip_prep_spec &sp, const float *mul, const float *nw, const float *signs)
+{
+    sp.norm_w = mul ? mul : nw;
+    sp.signs = mul ? nullptr : signs;
+}
+
 int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
 {
     if (m->plan && m->use_persist) {   // the layer stack and the head's prep as one launch, then head and sampler
@@ -482,8 +527,9 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
     const float inv_sqrt_hd = 1.0f / sqrtf((float)c.head_dim);
     for (int l = 0; l < c.n_layers; ++l) {
         eif_hip_prep_spec sp{};
-        sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_att[l], sp.eps = c.rms_eps;
-        sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
+        sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.eps = c.rms_eps;
+        spec_norm(sp, m->mul_att[l], m->rms_att[l], m->signs_dim);
+        sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
         int rc = eif_hip_qlinear_prep(m->wqkv[l], &sp, nullptr, m->qkv, m->q_dim + 2 * m->kv_dim, 1, st);
         if (rc) return rc;
         const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
@@ -494,14 +540,16 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
                                                            c.seq_len, inv_sqrt_hd);
         EIF_HIP_LAUNCHED();
         sp = eif_hip_prep_spec{};
-        sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_sub_att[l], sp.eps = c.sub_eps;
-        sp.signs = m->signs_q, sp.wht_block = c.wht_q, sp.wht_norm = c.wht_norm_q;
+        sp.pre = EIF_HIP_PRE_RMS, sp.eps = c.sub_eps;
+        spec_norm(sp, m->mul_sub_att[l], m->rms_sub_att[l], m->signs_q);
+        sp.wht_block = c.wht_q, sp.wht_norm = c.wht_norm_q;
         // x += O attention (the shares combined in the prep)
         if ((rc = eif::qlinear_prep_shares(m->wo[l], &sp, m->sh_o, m->sh_ml, c.head_dim, m->x, m->x, c.dim, st)))
             return rc;
         sp = eif_hip_prep_spec{};
-        sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.norm_w = m->rms_ffn[l], sp.eps = c.rms_eps;
-        sp.signs = m->signs_dim, sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
+        sp.x = m->x, sp.ldx = c.dim, sp.pre = EIF_HIP_PRE_RMS, sp.eps = c.rms_eps;
+        spec_norm(sp, m->mul_ffn[l], m->rms_ffn[l], m->signs_dim);
+        sp.wht_block = c.wht_dim, sp.wht_norm = c.wht_norm_dim;
         // h = SiLU(gate) * up in the gate|up launch (its GLU form) where the shape allows, then the down projection
         // with the sub-RMSNorm alone: the same bits as both halves and the SwiGLU pre-op
         rc = eif_hip_qlinear_prep_glu(m->w13[l], &sp, m->hb, c.hidden, 1, st);
@@ -511,8 +559,9 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         sp = eif_hip_prep_spec{};
         sp.x = m->hb, sp.x2 = m->hb + c.hidden, sp.ldx = c.hidden;
         sp.pre = glu ? EIF_HIP_PRE_RMS : EIF_HIP_PRE_SWIGLU_RMS;
-        sp.norm_w = m->rms_sub_ffn[l], sp.eps = c.sub_eps;
-        sp.signs = m->signs_hidden, sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
+        sp.eps = c.sub_eps;
+        spec_norm(sp, m->mul_sub_ffn[l], m->rms_sub_ffn[l], m->signs_hidden);
+        sp.wht_block = c.wht_hidden, sp.wht_norm = c.wht_norm_hidden;
         if ((rc = eif_hip_qlinear_prep(m->w2[l], &sp, m->x, m->x, c.dim, 1, st))) return rc;   // x += W2 h
     }
     return enqueue_head(m, st);
@@ -746,6 +795,8 @@ int eif_hip_bitnet_create(eif_hip_bitnet **out, const eif_hip_bitnet_config *cfg
     m->w13.assign(c.n_layers, nullptr), m->w2.assign(c.n_layers, nullptr);
     m->rms_att.assign(c.n_layers, nullptr), m->rms_ffn.assign(c.n_layers, nullptr);
     m->rms_sub_att.assign(c.n_layers, nullptr), m->rms_sub_ffn.assign(c.n_layers, nullptr);
+    m->mul_att.assign(c.n_layers, nullptr), m->mul_ffn.assign(c.n_layers, nullptr);
+    m->mul_sub_att.assign(c.n_layers, nullptr), m->mul_sub_ffn.assign(c.n_layers, nullptr);
     if (hipMalloc(&m->x, sizeof(float) * c.dim) != hipSuccess ||
         hipMalloc(&m->qkv, sizeof(float) * (m->q_dim + 2 * m->kv_dim)) != hipSuccess ||
         hipMalloc(&m->hb, sizeof(float) * 2 * c.hidden) != hipSuccess ||
@@ -848,7 +899,7 @@ int eif_hip_bitnet_set_layer(eif_hip_bitnet *m, int l, const eif_hip_bitnet_laye
     m->wqkv[l] = qkv, m->wo[l] = wo, m->w13[l] = w13, m->w2[l] = w2;
     m->rms_att[l] = n_att, m->rms_ffn[l] = n_ffn, m->rms_sub_att[l] = n_sa, m->rms_sub_ffn[l] = n_sf;
     m->weight_bytes += bytes + sizeof(float) * (2 * c.dim + m->q_dim + c.hidden);
-    return EIF_HIP_OK;
+    return m->head ? fold_signs(m, l) : EIF_HIP_OK;   // the signs are set (eif_hip_bitnet_set_globals)
 }
 
 int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *g)
@@ -873,6 +924,17 @@ int eif_hip_bitnet_set_globals(eif_hip_bitnet *m, const eif_hip_bitnet_globals *
     m->weight_bytes += b + sizeof(float) * c.dim;
     m->head_kpad = kp;
     m->head_tiles = eif::qweight_row_tiles(m->head);
+    auto pm1 = [](const float *s, int n, int block) {
+        if (!s || block <= 0) return false;
+        for (int i = 0; i < n; ++i)
+            if (s[i] != 1.0f && s[i] != -1.0f) return false;
+        return true;
+    };
+    m->fold_dim = pm1(g->signs_dim, c.dim, c.wht_dim);
+    m->fold_q = pm1(g->signs_q, m->q_dim, c.wht_q);
+    m->fold_hidden = pm1(g->signs_hidden, c.hidden, c.wht_hidden);
+    for (int l = 0; l < c.n_layers; ++l)
+        if (m->rms_att[l] && (rc = fold_signs(m, l))) return rc;
     if (hipMalloc(&m->hq, (size_t)kp) != hipSuccess || hipMalloc(&m->hs, sizeof(float) * 4) != hipSuccess ||
         hipMalloc(&m->amax_key, sizeof(unsigned long long) * kArgmaxSlots * kArgmaxStride) != hipSuccess ||
         hipMemset(m->amax_key, 0, sizeof(unsigned long long) * kArgmaxSlots * kArgmaxStride) != hipSuccess)
@@ -1048,7 +1110,8 @@ void eif_hip_bitnet_destroy(eif_hip_bitnet *m)
     for (auto *v : {&m->wqkv, &m->wo, &m->w13, &m->w2})
         for (eif_hip_qweight *q : *v) eif_hip_qweight_destroy(q);
     eif_hip_qweight_destroy(m->head);
-    for (auto *v : {&m->rms_att, &m->rms_ffn, &m->rms_sub_att, &m->rms_sub_ffn})
+    for (auto *v : {&m->rms_att, &m->rms_ffn, &m->rms_sub_att, &m->rms_sub_ffn, &m->mul_att, &m->mul_ffn,
+                    &m->mul_sub_att, &m->mul_sub_ffn})
         for (float *p : *v)
             if (p) (void)hipFree(p);
     for (void *p : {(void *)m->rms_final, (void *)m->signs_dim, (void *)m->signs_q, (void *)m->signs_hidden,

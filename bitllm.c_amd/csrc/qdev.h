@@ -239,44 +239,69 @@ EIF_DEV void load4(const float *base, int idx, float (&v)[E])
     }
 }
 
-// Thread t holds columns [E*t, E*t + E) of token row m (zeros past K); tid is the thread's index in the workgroup. The loads are unconditional (clamped to
-// the row) and nothing consumes them here, so the weight loads issued next are not held behind them; the
-// pre-op, the sign flip and the zeroing past K happen in prep_finish.
-//   v: x; sg: signs; v2: x2 (SwiGLU); nw: the RMSNorm weight (operands that are absent hold x).
-template <int E, bool COH = false>
+// Thread t holds columns [E*t, E*t + E) of token row m (zeros past K); tid is the thread's index in the workgroup.
+// The loads are clamped to the row and nothing consumes them here, so the weight loads a GEMV issues next are not
+// held behind them; the pre-op, the sign flip and the zeroing past K happen in prep_finish.
+//   v: x; sg: signs; v2: x2 (SwiGLU); nw: the RMSNorm weight. An absent operand (a null row) is not loaded: its
+//   registers hold 1 (signs, weight) or 0 (x2). Each activation load costs address-unit time that the weight
+//   loads issued after it wait for, so only the operands present are read (uniform branches, all of them before
+//   the caller's weight loads; prep_finish holds every operand on every path, so none is sunk behind those).
+// The per-column operands a fused prep reads, a compile-time choice of the launch:
+//   kOpsX    x alone (no signs, no norm weight, no x2);
+//   kOpsMul  x and one column multiplier, applied after the pre-op's sum of squares and before the rotation: the
+//            norm weight, the signs, or their product (exact for +-1 signs: (v w) s = v (w s));
+//   kOpsAny  every operand the rows name (signs, x2, norm weight), each read where present.
+enum { kOpsX = 0, kOpsMul = 1, kOpsAny = 2 };
+
+template <int E>
+EIF_DEV void fill(float (&v)[E], float c)
+{
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = c;
+}
+
+// OPS (kOpsX ...): kOpsAny reads what is present (uniform branches); kOpsMul reads x and the multiplier at nwr
+// into nw; kOpsX reads x alone. Every load count is then fixed, and the code before the caller's weight loads
+// has no branch.
+template <int E, bool COH = false, int OPS = kOpsAny>
 EIF_DEV void prep_load_rows(const float *xr, const float *sgr, const float *x2r, const float *nwr, int K,
                             float (&v)[E], float (&sg)[E], float (&v2)[E], float (&nw)[E], int tid = threadIdx.x)
 {
     const int i0 = E * tid;
     const int ic = i0 < K ? i0 : 0;
     load4<E, COH>(xr, ic, v);
-    load4<E>(sgr, ic, sg);
-    load4<E, COH>(x2r, ic, v2);
-    load4<E>(nwr, ic, nw);
+    if constexpr (OPS == kOpsAny) {
+        if (sgr) load4<E>(sgr, ic, sg); else fill(sg, 1.0f);
+        if (x2r) load4<E, COH>(x2r, ic, v2); else fill(v2, 0.0f);
+        if (nwr) load4<E>(nwr, ic, nw); else fill(nw, 1.0f);
+    } else {
+        fill(sg, 1.0f);
+        fill(v2, 0.0f);
+        if constexpr (OPS == kOpsMul) load4<E>(nwr, ic, nw); else fill(nw, 1.0f);
+    }
 }
 
-// Every load is issued, from x where an operand is absent (scalar pointer selects, no branches): a load count
-// that is the same on every path lets the compiler wait for these loads alone, behind which the weight and scale
-// loads stay in flight. prep_load_rows takes the four rows as given (a kernel's preloaded arguments).
+// prep_load_rows on the rows PrepArgs names (prep_load_rows itself takes them as given: a kernel's preloaded
+// arguments).
 template <int E, bool COH = false>
 EIF_DEV void prep_load(const PrepArgs &p, int m, float (&v)[E], float (&sg)[E], float (&v2)[E], float (&nw)[E],
                        int tid = threadIdx.x)
 {
-    const float *xr = p.x + (size_t)m * p.ldx;
-    prep_load_rows<E, COH>(xr, p.signs ? p.signs : xr, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 + (size_t)m * p.ldx : xr,
-                           p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : xr, p.K, v, sg, v2, nw, tid);
+    prep_load_rows<E, COH>(p.x + (size_t)m * p.ldx, p.signs,
+                           p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 + (size_t)m * p.ldx : nullptr,
+                           p.pre != EIF_HIP_PRE_NONE ? p.nw : nullptr, p.K, v, sg, v2, nw, tid);
 }
 
 // The attention shares of thread t's columns [E t, E t + E) (head h = E t / sh_hd, dims from E t % sh_hd): every
-// share's outputs and the head's maxima and sums, loaded unconditionally like prep_load (signs and the norm
-// weight too, from the outputs where absent).
+// share's outputs and the head's maxima and sums, loaded unconditionally; the signs and the norm weight as in
+// prep_load_rows (null: not loaded).
 template <int E>
 struct Shares {
     float o[kAttnShares][E];
     float ml[2 * kAttnShares];
 };
 
-template <int E, bool COH = false>
+template <int E, bool COH = false, int OPS = kOpsAny>
 EIF_DEV void prep_load_sh_rows(const float *sh_o, const float *sh_ml, const float *sgr, const float *nwr, int K,
                                int sh_hd, Shares<E> &sh, float (&sg)[E], float (&nw)[E], int tid = threadIdx.x)
 {
@@ -287,15 +312,20 @@ EIF_DEV void prep_load_sh_rows(const float *sh_o, const float *sh_ml, const floa
     const int o = h * kAttnShares * sh_hd + d;
 #pragma unroll
     for (int s = 0; s < kAttnShares; ++s) load4<E, COH>(sh_o, o + s * sh_hd, sh.o[s]);
-    load4<E>(sgr, ic, sg);
-    load4<E>(nwr, ic, nw);
+    if constexpr (OPS == kOpsAny) {
+        if (sgr) load4<E>(sgr, ic, sg); else fill(sg, 1.0f);
+        if (nwr) load4<E>(nwr, ic, nw); else fill(nw, 1.0f);
+    } else {
+        fill(sg, 1.0f);
+        if constexpr (OPS == kOpsMul) load4<E>(nwr, ic, nw); else fill(nw, 1.0f);
+    }
 }
 
 template <int E, bool COH = false>
 EIF_DEV void prep_load_sh(const PrepArgs &p, Shares<E> &sh, float (&sg)[E], float (&nw)[E], int tid = threadIdx.x)
 {
-    prep_load_sh_rows<E, COH>(p.sh_o, p.sh_ml, p.signs ? p.signs : p.sh_o,
-                              p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : p.sh_o, p.K, p.sh_hd, sh, sg, nw, tid);
+    prep_load_sh_rows<E, COH>(p.sh_o, p.sh_ml, p.signs, p.pre != EIF_HIP_PRE_NONE ? p.nw : nullptr, p.K, p.sh_hd,
+                              sh, sg, nw, tid);
 }
 
 // v = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s, M = max_s M_s (share 0 always holds rows, so M is finite).
@@ -321,14 +351,25 @@ EIF_DEV void sh_combine(const Shares<E> &sh, float (&v)[E])
 
 // Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
 // LB = log2 of the WHT block when it is fixed at compile time (0: no rotation), -1: block read from p.block.
-template <int E, int LB, int BAR = 0>
+// OPS: the operands loaded (kOpsX ...); kOpsMul holds its multiplier in nwv.
+template <int E, int LB, int BAR = 0, int OPS = kOpsAny>
 EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], const float (&sg)[E],
                          const float (&v2)[E], const float (&nwv)[E], int8_t *lds_x, float *xs_l, float *red,
                          float *red_ss, int tid = threadIdx.x)
 {
     const int t = tid, i0 = E * t, nw = blockDim.x >> 6;
     const int block = LB >= 0 ? (LB > 0 ? 1 << LB : 0) : p.block;
-    const bool live = i0 < p.K, flip = block > 0 && p.signs;
+    const bool live = i0 < p.K, flip = OPS == kOpsAny && block > 0 && p.signs;
+    // Every operand is held here, on every path. An operand that only a branch below reads (the norm weight, x2,
+    // the signs) would otherwise have its load sunk into that branch, issued after a GEMV's weight loads and
+    // waited for together with them (vmcnt counts in issue order): the prep would start when the weights land.
+    if constexpr (OPS == kOpsAny) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) asm volatile("" ::"v"(sg[e]), "v"(v2[e]), "v"(nwv[e]));
+    } else if constexpr (OPS == kOpsMul) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) asm volatile("" ::"v"(nwv[e]));
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e) v[e] = live ? v[e] : 0.0f;
     // RMSNorm over the K columns, (v * r) * weight with r = 1 / sqrtf(sum(v^2) / K + eps): r > 0 is one factor of
@@ -338,16 +379,20 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
     const bool rms = p.pre != EIF_HIP_PRE_NONE;
     float ss = 0.0f;
     if (rms) {   // uniform
-        if (p.pre == EIF_HIP_PRE_SWIGLU_RMS) {
+        if (OPS == kOpsAny && p.pre == EIF_HIP_PRE_SWIGLU_RMS) {
 #pragma unroll
             for (int e = 0; e < E; ++e) v[e] = (v[e] * (1.0f / (1.0f + expf(-v[e])))) * (live ? v2[e] : 0.0f);
         }
 #pragma unroll
         for (int e = 0; e < E; ++e) ss = fmaf(v[e], v[e], ss);
-        if (p.nw) {
+        if (OPS == kOpsAny && p.nw) {
 #pragma unroll
             for (int e = 0; e < E; ++e) v[e] = v[e] * nwv[e];
         }
+    }
+    if constexpr (OPS == kOpsMul) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = v[e] * nwv[e];
     }
     if (flip) {
 #pragma unroll

@@ -369,15 +369,15 @@ constexpr int gemv_scl() { return FMT == kTern && GROUPED && (UD == 3 || UD == 4
 // The leading arguments are what the first loads need, so they are preloaded into SGPRs at wave launch
 // (-amdgpu-kernarg-preload-count, qlinear.hip's build line; struct arguments are not preloaded) and the
 // activation and weight loads issue before any kernel-argument fetch returns (gemv_hot() builds them):
-//   E > 0:  r0 = x row 0, r1 = signs (x where absent), r2 = x2 (SwiGLU up rows; x where absent), r3 = the norm
-//           weight (x where absent), i0 = K;
-//   SH:     r0 = shares' outputs, r1 = shares' maxima and sums, r2 = signs, r3 = norm weight (absent: r0),
+//   E > 0:  r0 = x row 0, r1 = signs, r2 = x2 (SwiGLU up rows), r3 = the norm weight (each null where absent:
+//           not loaded), i0 = K;
+//   SH:     r0 = shares' outputs, r1 = shares' maxima and sums, r2 = signs, r3 = norm weight (null where absent),
 //           i0 = K, i1 bits 0..26 = the shares' head dim;
 //   E = 0:  r0 = xq, r1 = xs, r2 = r3 unused, i0 = M, i1 bits 0..19 = ldq, bits 20..26 = token rows per workgroup;
 //   every form: i1 bits 27..31 = ks, the waves per row tile (blockDim.x / 64 / RT: the workgroup size is itself
 //           a kernel-argument fetch, and the weight steps of a wave depend on it).
-// Loads are issued in the order activations, weights, scales, each group with a count known at compile time,
-// so the prep waits for the activations alone.
+// Loads are issued in the order activations, weights, scales, the weights and scales with a count known at
+// compile time, so the prep waits for the activations alone.
 //
 // GLU (gated form, grouped FP32 outputs): the matrix stacks a gate half (rows 0 .. h - 1) over an up half (rows
 // h .. 2h - 1), h = 16 * (i1 bits 0..26); a workgroup's first RT / 2 row tiles are gate tiles and its last RT / 2
@@ -386,7 +386,7 @@ constexpr int gemv_scl() { return FMT == kTern && GROUPED && (UD == 3 || UD == 4
 // prep_finish, so a down projection fed with these rows and the RMSNorm pre-op gives the bits of one fed with
 // the two halves and the SwiGLU pre-op.
 template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT = 1, bool SH = false,
-          bool GLU = false>
+          bool GLU = false, int OPS = kOpsAny>
 __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0, const void *__restrict__ r1,
                                                      const void *__restrict__ r2, const void *__restrict__ r3,
                                                      const uint8_t *__restrict__ W, int wld, int nsteps, int i0,
@@ -459,12 +459,13 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     float xs_v = 0.0f;
     [[maybe_unused]] Shares<SH ? EV : 1> shv;
     if constexpr (SH) {
-        prep_load_sh_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
-                             static_cast<const float *>(r2), static_cast<const float *>(r3), i0, i1 & 0x7FFFFFF, shv,
-                             sg, nwv);
+        prep_load_sh_rows<E, false, OPS>(static_cast<const float *>(r0), static_cast<const float *>(r1),
+                                         static_cast<const float *>(r2), static_cast<const float *>(r3), i0,
+                                         i1 & 0x7FFFFFF, shv, sg, nwv);
     } else if constexpr (E > 0) {
-        prep_load_rows<E>(static_cast<const float *>(r0), static_cast<const float *>(r1),
-                          static_cast<const float *>(r2), static_cast<const float *>(r3), i0, v, sg, v2, nwv);
+        prep_load_rows<E, false, OPS>(static_cast<const float *>(r0), static_cast<const float *>(r1),
+                                      static_cast<const float *>(r2), static_cast<const float *>(r3), i0, v, sg, v2,
+                                      nwv);
     } else {
 #pragma unroll
         for (int i = 0; i < kMaxPieces; ++i)
@@ -531,17 +532,25 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
         gb_raw = *(a.bias ? a.bias + br : a.scales + sc0);
     }
 
+    // The scale and bias loads stay ahead of the prep (the attention shares' combine would otherwise be
+    // scheduled first, and these loads issued only when the shares have landed).
+    __builtin_amdgcn_sched_barrier(0);
+
     // 3. activations -> LDS
     if constexpr (SH) {
         sh_combine<E>(shv, v);
 #pragma unroll
         for (int e = 0; e < E; ++e) v2[e] = 0.0f;
-        prep_finish<E, LB>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
+        prep_finish<E, LB, 0, OPS>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
     } else if constexpr (E > 0) {
-        prep_finish<E, LB>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
+        prep_finish<E, LB, 0, OPS>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
         for (int m = 1; m < a.M; ++m) {
-            prep_load<E>(p, m, v, sg, v2, nwv);
-            prep_finish<E, LB>(p, m, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
+            if constexpr (OPS == kOpsAny)
+                prep_load<E>(p, m, v, sg, v2, nwv);
+            else
+                prep_load_rows<E, false, OPS>(p.x + (size_t)m * p.ldx, nullptr, nullptr,
+                                              static_cast<const float *>(r3), p.K, v, sg, v2, nwv);
+            prep_finish<E, LB, 0, OPS>(p, m, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
         }
     } else {
 #pragma unroll
@@ -1339,20 +1348,37 @@ struct GemvHot {
     int i0, i1;
 };
 
-// ks: waves per row tile (1..16). Returns false when a field does not fit its bits (the launch is refused).
-bool gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares, int ks, GemvHot *h)
+// The operand set of a fused prep (kOpsX ...) and, for kOpsMul, its multiplier: the signs count where the rows
+// are rotated, the norm weight where a pre-op reads it.
+int gemv_ops(const PrepArgs &p, const float **mul)
+{
+    const float *sg = p.block > 0 ? p.signs : nullptr, *nw = p.pre != EIF_HIP_PRE_NONE ? p.nw : nullptr;
+    if (p.pre == EIF_HIP_PRE_SWIGLU_RMS || (sg && nw)) return kOpsAny;
+    *mul = sg ? sg : nw;
+    return *mul ? kOpsMul : kOpsX;
+}
+
+// ks: waves per row tile (1..16); ops: the kernel's operand set. Returns false when a field does not fit its
+// bits (the launch is refused).
+bool gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares, int ks, GemvHot *h, int ops = kOpsAny)
 {
     if (ks < 1 || ks > 16) return false;
     const unsigned kb = (unsigned)ks << 27;
+    const float *mul = nullptr;
+    if (ops != kOpsAny && gemv_ops(p, &mul) != ops) return false;
     if (shares) {
         const float *o = p.sh_o;
         if (p.sh_hd < 0 || p.sh_hd >= (1 << 27)) return false;
-        *h = {o, p.sh_ml, p.signs ? p.signs : o, p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : o, p.K,
-              (int)((unsigned)p.sh_hd | kb)};
+        if (ops == kOpsAny)
+            *h = {o, p.sh_ml, p.signs, p.pre != EIF_HIP_PRE_NONE ? p.nw : nullptr, p.K, (int)((unsigned)p.sh_hd | kb)};
+        else
+            *h = {o, p.sh_ml, nullptr, mul, p.K, (int)((unsigned)p.sh_hd | kb)};
     } else if (fused) {
-        const float *x = p.x;
-        *h = {x, p.signs ? p.signs : x, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 : x,
-              p.pre != EIF_HIP_PRE_NONE && p.nw ? p.nw : x, p.K, (int)kb};
+        if (ops == kOpsAny)
+            *h = {p.x, p.signs, p.pre == EIF_HIP_PRE_SWIGLU_RMS ? p.x2 : nullptr,
+                  p.pre != EIF_HIP_PRE_NONE ? p.nw : nullptr, p.K, (int)kb};
+        else
+            *h = {p.x, nullptr, nullptr, mul, p.K, (int)kb};
     } else {
         if (a.ldq < 0 || a.ldq >= (1 << 20) || a.mw < 0 || a.mw > 127) return false;
         *h = {a.xq, a.xs, a.xq, a.xq, a.M, (int)((unsigned)a.ldq | ((unsigned)a.mw << 20) | kb)};
@@ -1360,15 +1386,15 @@ bool gemv_hot(const QArgs &a, const PrepArgs &p, bool fused, bool shares, int ks
     return true;
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int SPW, int LB, int RT, int TT, int OPS = kOpsAny>
 int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
     const size_t lds = gemv_lds_bytes(GROUPED, gemv_gs16<FMT, UD>(), a, p.ldl, RT, ks);
     QArgs ag = a;
     const int grid = gemv_grid(ag, rows_pad / (16 * RT));
     GemvHot h;
-    if (!gemv_hot(ag, p, E > 0, false, ks, &h)) return EIF_HIP_E_LIMIT;   // a field beyond its packed bits
-    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT, TT><<<grid, 64 * RT * ks, lds, st>>>(
+    if (!gemv_hot(ag, p, E > 0, false, ks, &h, OPS)) return EIF_HIP_E_LIMIT;   // a field beyond its packed bits
+    qgemv_kernel<FMT, UD, GROUPED, ACC, E, SPW, LB, RT, TT, false, false, OPS><<<grid, 64 * RT * ks, lds, st>>>(
         h.r0, h.r1, h.r2, h.r3, ag.W, ag.wld, ag.nsteps, h.i0, h.i1, ag, p);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
@@ -1378,40 +1404,46 @@ int launch_gemv_s(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipSt
 // two up), `half` output rows. E and the waves per tile follow launch_gemv_tiles' rules.
 constexpr int kGluRT = 4;
 
-template <int E, int SPW, int LB>
+template <int E, int SPW, int LB, int OPS>
 int launch_glu_s(const QArgs &a, const PrepArgs &p, int half, int ks, hipStream_t st)
 {
     const size_t lds = gemv_lds_bytes(true, true, a, p.ldl, kGluRT, ks);
     GemvHot h;
-    if (!gemv_hot(a, p, true, false, ks, &h)) return EIF_HIP_E_LIMIT;
+    if (!gemv_hot(a, p, true, false, ks, &h, OPS)) return EIF_HIP_E_LIMIT;
     h.i1 |= half / 16;   // bits 0..26: the tiles of one half
-    qgemv_kernel<kTern, 4, true, false, E, SPW, LB, kGluRT, 1, false, true><<<half / (16 * kGluRT / 2), 64 * kGluRT * ks,
-                                                                              lds, st>>>(
+    qgemv_kernel<kTern, 4, true, false, E, SPW, LB, kGluRT, 1, false, true, OPS>
+        <<<half / (16 * kGluRT / 2), 64 * kGluRT * ks, lds, st>>>(
         h.r0, h.r1, h.r2, h.r3, a.W, a.wld, a.nsteps, h.i0, h.i1, a, p);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
 
-template <int E, int LB>
+template <int E, int LB, int OPS = kOpsAny>
 int launch_glu_e(const QArgs &a, const PrepArgs &p, int half, int ks, hipStream_t st)
 {
+    if constexpr (LB == 7 && OPS == kOpsAny) {   // the BitNet rotation: the operand set compiled in
+        const float *mul = nullptr;
+        const int ops = gemv_ops(p, &mul);
+        if (ops == kOpsX) return launch_glu_e<E, LB, kOpsX>(a, p, half, ks, st);
+        if (ops == kOpsMul) return launch_glu_e<E, LB, kOpsMul>(a, p, half, ks, st);
+    }
     const int steps = eif_ceil_div(a.nsteps, ks);
-    if (steps <= 1) return launch_glu_s<E, 1, LB>(a, p, half, ks, st);
-    if (steps <= 2) return launch_glu_s<E, 2, LB>(a, p, half, ks, st);
-    if (steps <= 4) return launch_glu_s<E, 4, LB>(a, p, half, ks, st);
-    return launch_glu_s<E, 8, LB>(a, p, half, ks, st);
+    if (steps <= 1) return launch_glu_s<E, 1, LB, OPS>(a, p, half, ks, st);
+    if (steps <= 2) return launch_glu_s<E, 2, LB, OPS>(a, p, half, ks, st);
+    if (steps <= 4) return launch_glu_s<E, 4, LB, OPS>(a, p, half, ks, st);
+    return launch_glu_s<E, 8, LB, OPS>(a, p, half, ks, st);
 }
 
 // The shares-combining form (one row, ternary weights, E = 4 or 8, one row tile per workgroup, one step per
 // wave held at once).
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT, int OPS = kOpsAny>
 int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
     if constexpr (FMT == kTern && !ACC && (E == 4 || E == 8) && RT == 1) {
         const size_t lds = gemv_lds_bytes(GROUPED, gemv_gs16<FMT, UD>(), a, p.ldl, RT, ks);
         GemvHot h;
-        if (!gemv_hot(a, p, true, true, ks, &h)) return EIF_HIP_E_LIMIT;
-        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true><<<rows_pad / 16, 64 * ks, lds, st>>>(
+        if (!gemv_hot(a, p, true, true, ks, &h, OPS)) return EIF_HIP_E_LIMIT;
+        qgemv_kernel<FMT, UD, GROUPED, ACC, E, 1, LB, RT, 1, true, false, OPS><<<rows_pad / 16, 64 * ks, lds, st>>>(
             h.r0, h.r1, h.r2, h.r3, a.W, a.wld, a.nsteps, h.i0, h.i1, a, p);
         EIF_HIP_LAUNCHED();
         return EIF_HIP_OK;
@@ -1420,28 +1452,29 @@ int launch_gemv_sh(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipS
     }
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT, int TT = 1>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int RT, int TT = 1, int OPS = kOpsAny>
 int launch_gemv_e(const QArgs &a, const PrepArgs &p, int rows_pad, int ks, hipStream_t st)
 {
-    if (p.sh_ml) return launch_gemv_sh<FMT, UD, GROUPED, ACC, E, LB, RT>(a, p, rows_pad, ks, st);
+    if (p.sh_ml) return launch_gemv_sh<FMT, UD, GROUPED, ACC, E, LB, RT, OPS>(a, p, rows_pad, ks, st);
     constexpr int SMAX = Geo<FMT, UD>::SB >= 32 ? 4 : 8;   // 8-dword steps: half the registers per chunk
     const int steps = eif_ceil_div(a.nsteps, ks);
     if constexpr (ACC || !gemv_tuned<FMT, UD, GROUPED>()) {
-        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT, TT>(a, p, rows_pad, ks, st);
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT, TT, OPS>(a, p, rows_pad, ks, st);
     } else {
-        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1, LB, RT, TT>(a, p, rows_pad, ks, st);
-        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2, LB, RT, TT>(a, p, rows_pad, ks, st);
-        if (steps <= 4 || SMAX == 4) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4, LB, RT, TT>(a, p, rows_pad, ks, st);
-        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT, TT>(a, p, rows_pad, ks, st);
+        if (steps <= 1) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 1, LB, RT, TT, OPS>(a, p, rows_pad, ks, st);
+        if (steps <= 2) return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 2, LB, RT, TT, OPS>(a, p, rows_pad, ks, st);
+        if (steps <= 4 || SMAX == 4)
+            return launch_gemv_s<FMT, UD, GROUPED, ACC, E, 4, LB, RT, TT, OPS>(a, p, rows_pad, ks, st);
+        return launch_gemv_s<FMT, UD, GROUPED, ACC, E, SMAX, LB, RT, TT, OPS>(a, p, rows_pad, ks, st);
     }
 }
 
-template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int TT = 1>
+template <int FMT, int UD, bool GROUPED, bool ACC, int E, int LB, int TT = 1, int OPS = kOpsAny>
 int launch_gemv_rt(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int ks, hipStream_t st)
 {
     if constexpr (gemv_tuned<FMT, UD, GROUPED>())
-        if (rt == 4) return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 4, TT>(a, p, rows_pad, ks, st);
-    return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 1, TT>(a, p, rows_pad, ks, st);
+        if (rt == 4) return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 4, TT, OPS>(a, p, rows_pad, ks, st);
+    return launch_gemv_e<FMT, UD, GROUPED, ACC, E, LB, 1, TT, OPS>(a, p, rows_pad, ks, st);
 }
 
 // Fused prep: E columns per thread. The WHT-128 of the BitNet configurations and no rotation (the INT8 head)
@@ -1450,7 +1483,18 @@ template <int FMT, int UD, bool GROUPED, bool ACC, int E>
 int launch_gemv_fused(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, int ks, hipStream_t st)
 {
     if constexpr (E <= 8 && gemv_tuned<FMT, UD, GROUPED>()) {
-        if (p.block == 128) return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 7>(a, p, rows_pad, rt, ks, st);
+        if (p.block == 128) {
+            // the BitNet rotation, the configurations that run it: the operand set compiled in, so the prep
+            // reads only the columns it needs and the code before the weight loads has no branch
+            if constexpr (!ACC && FMT == kTern) {
+                const float *mul = nullptr;
+                const int ops = gemv_ops(p, &mul);
+                if (ops == kOpsX) return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 7, 1, kOpsX>(a, p, rows_pad, rt, ks, st);
+                if (ops == kOpsMul)
+                    return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 7, 1, kOpsMul>(a, p, rows_pad, rt, ks, st);
+            }
+            return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 7>(a, p, rows_pad, rt, ks, st);
+        }
         if (p.block == 0 && !ACC) return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, 0>(a, p, rows_pad, rt, ks, st);
     }
     return launch_gemv_rt<FMT, UD, GROUPED, ACC, E, -1>(a, p, rows_pad, rt, ks, st);
