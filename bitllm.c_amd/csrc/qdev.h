@@ -351,11 +351,17 @@ EIF_DEV void sh_combine(const Shares<E> &sh, float (&v)[E])
 
 // Rotation, absmax over the workgroup, INT8 codes of token m into LDS (row m, columns [0, kpad)).
 // LB = log2 of the WHT block when it is fixed at compile time (0: no rotation), -1: block read from p.block.
-// OPS: the operands loaded (kOpsX ...); kOpsMul holds its multiplier in nwv.
-template <int E, int LB, int BAR = 0, int OPS = kOpsAny>
+struct NoHook {
+    EIF_DEV void operator()() const {}
+};
+
+// OPS: the operands loaded (kOpsX ...); kOpsMul holds its multiplier in nwv. mid(): called once the row's
+// maxima are reduced within each wave, before the workgroup barrier (a caller's loads that may wait for the
+// struct arguments, issued where that wait costs nothing).
+template <int E, int LB, int BAR = 0, int OPS = kOpsAny, class Mid = NoHook>
 EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], const float (&sg)[E],
                          const float (&v2)[E], const float (&nwv)[E], int8_t *lds_x, float *xs_l, float *red,
-                         float *red_ss, int tid = threadIdx.x)
+                         float *red_ss, int tid = threadIdx.x, Mid &&mid = Mid{})
 {
     const int t = tid, i0 = E * t, nw = blockDim.x >> 6;
     const int block = LB >= 0 ? (LB > 0 ? 1 << LB : 0) : p.block;
@@ -423,6 +429,7 @@ EIF_DEV void prep_finish(const PrepArgs &p, int m, int kpad, float (&v)[E], cons
     }
     amax = wave_max_dpp(amax);
     if (rms) ss = wave_sum_dpp(ss);
+    mid();
     if ((t & 63) == 0) red[t >> 6] = amax, red_ss[t >> 6] = ss;
     wg_sync<BAR>();
     // the per-wave maxima (and sums), one per lane, reduced again across the wave

@@ -510,40 +510,42 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
     // GLU: the gate tiles' block, then the up tiles' block (each RH * 16 rows, contiguous in [N, G])
     const int sbase = GLU ? rb * RH * 16 * a.G : row0 * a.G, shalf = RH * 16 * a.G, sup = glu_t * 16 * a.G;
     const int nsc = TR * a.G, last_sc = a.N * a.G - 1, sc0 = min(sbase, last_sc);
-    if constexpr (GROUPED && !ACC) {
+    float rs_raw = 0.0f, bb_raw = 0.0f, gb_raw = 0.0f;
+    // The scale and bias loads address the matrix through the struct arguments (not preloaded), so issuing them
+    // waits for the argument fetch. They are needed only by the epilogue: a fused prep issues them from its
+    // middle (prep_finish's hook, by then the fetch has returned) rather than letting the fetch hold back its
+    // start; the prepped form issues them here.
+    auto issue_scales = [&]() __attribute__((always_inline)) {
+        if constexpr (GROUPED && !ACC) {
 #pragma unroll
-        for (int i = 0; i < SCL; ++i) {
-            const int l = (int)threadIdx.x + i * nthr;
-            const int idx = sbase + l + (GLU && l >= shalf ? sup - shalf : 0);
-            scv[i] = a.scales[idx <= last_sc && l < nsc ? idx : sc0];
+            for (int i = 0; i < SCL; ++i) {
+                const int l = (int)threadIdx.x + i * nthr;
+                const int idx = sbase + l + (GLU && l >= shalf ? sup - shalf : 0);
+                scv[i] = a.scales[idx <= last_sc && l < nsc ? idx : sc0];
+            }
+            // the bias of the row this thread combines (row0 + threadIdx % TR for every token)
+            const int br = min(row0 + (int)threadIdx.x % TR, a.N - 1);
+            gb_raw = *(a.bias ? a.bias + br : a.scales + sc0);
         }
-    }
-    float rs_raw = 0.0f, bb_raw = 0.0f;
-    if constexpr (!GROUPED && !ACC) {
-        const int rc = row_ok ? row : a.N - 1;
-        const float *sp0 = a.scales ? a.scales + rc : reinterpret_cast<const float *>(wp);
-        rs_raw = *sp0;
-        bb_raw = *(a.bias ? a.bias + rc : sp0);
-    }
-    // grouped: the bias of the row this thread combines (row0 + threadIdx % TR for every token), loaded now
-    float gb_raw = 0.0f;
-    if constexpr (GROUPED && !ACC) {
-        const int br = min(row0 + (int)threadIdx.x % TR, a.N - 1);
-        gb_raw = *(a.bias ? a.bias + br : a.scales + sc0);
-    }
-
-    // The scale and bias loads stay ahead of the prep (the attention shares' combine would otherwise be
-    // scheduled first, and these loads issued only when the shares have landed).
-    __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!GROUPED && !ACC) {
+            const int rc = row_ok ? row : a.N - 1;
+            const float *sp0 = a.scales ? a.scales + rc : reinterpret_cast<const float *>(wp);
+            rs_raw = *sp0;
+            bb_raw = *(a.bias ? a.bias + rc : sp0);
+        }
+    };
+    if constexpr (E == 0) issue_scales();
 
     // 3. activations -> LDS
     if constexpr (SH) {
         sh_combine<E>(shv, v);
 #pragma unroll
         for (int e = 0; e < E; ++e) v2[e] = 0.0f;
-        prep_finish<E, LB, 0, OPS>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
+        prep_finish<E, LB, 0, OPS>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss, (int)threadIdx.x,
+                                   issue_scales);
     } else if constexpr (E > 0) {
-        prep_finish<E, LB, 0, OPS>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss);
+        prep_finish<E, LB, 0, OPS>(p, 0, kpad, v, sg, v2, nwv, lds_x, xs_l, red_max, red_ss, (int)threadIdx.x,
+                                   issue_scales);
         for (int m = 1; m < a.M; ++m) {
             if constexpr (OPS == kOpsAny)
                 prep_load<E>(p, m, v, sg, v2, nwv);
@@ -558,13 +560,6 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
             if (i < np) piece_store(i, pc[i]);
         if ((int)threadIdx.x < a.M) xs_l[threadIdx.x] = xs_v;
         __syncthreads();
-    }
-    if constexpr (GROUPED && !ACC) {
-#pragma unroll
-        for (int i = 0; i < SCL; ++i) {
-            const int idx = (int)threadIdx.x + i * nthr;
-            if (idx < nsc) sc_l[idx] = scv[i];
-        }
     }
 
     // 4. MFMAs. Token tile t: a lane's accumulator C[t] holds tokens 16t + 4s .. 16t + 4s + 3 (ntok of them live)
@@ -639,7 +634,13 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
 
     if constexpr (GROUPED) {
         // 5. group combine, in group order for every (token, row): t = fmaf((float)acc_g, s[r,g], t); the
-        // result does not depend on how the steps were split over waves.
+        // result does not depend on how the steps were split over waves. The scales are staged now, the
+        // MFMAs above having waited for the weights alone.
+#pragma unroll
+        for (int i = 0; i < SCL; ++i) {
+            const int idx = (int)threadIdx.x + i * nthr;
+            if (idx < nsc) sc_l[idx] = scv[i];
+        }
         __syncthreads();
         // the group sums of (token, local row r) combined with the row's scales
         auto combine = [&](int tok, int r) -> float {
