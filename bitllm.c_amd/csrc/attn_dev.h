@@ -75,8 +75,12 @@ EIF_DEV void attend(AttnLds<HD, NT> &L, int t, bool live, const float *q_l, cons
             float d = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) d = fmaf(qv[i], k8[i], d);
-#pragma unroll
-            for (int off = 1; off < DPR; off <<= 1) d += __shfl_xor(d, off, 64);
+            // the row's DPR lanes summed by DPP butterflies (lane exchanges inside 16-lane rows; DPR <= 16)
+            static_assert(DPR <= 16, "a key row within one 16-lane row");
+            if constexpr (DPR > 1) d += xlane<1>(d);
+            if constexpr (DPR > 2) d += xlane<2>(d);
+            if constexpr (DPR > 4) d += xlane<4>(d);
+            if constexpr (DPR > 8) d += xlane<8>(d);
             return d * inv_sqrt_hd;
         };
         for (int base = 0; base < n_cache; base += RG * UNR) {

@@ -67,7 +67,9 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
 // first query head of the kv head, appends them to the cache. Each writes its share (attend's partial form):
 // outputs sh_o[h][s][HD], maximum sh_ml[h][s], sum sh_ml[h][kAttnShares + s]; the O projection combines them,
 //   M = max_s M_s, out = sum_s e^(M_s - M) O_s / sum_s e^(M_s - M) L_s.
-// Cache layout: [kv_head][seq_len][HD] fp16 per layer.
+// Cache layout: [kv_head][seq_len][HD] fp16 per layer. Grid (kAttnShares, heads): workgroup ids run over the
+// chunks of a head first, so the dispatcher, which deals ids round-robin over the eight XCDs, puts chunk s of
+// every head on one XCD, and the query heads of a kv head read that chunk's keys and values through one L2.
 template <int HD>
 constexpr int attn_chunk() { return (256 / (HD / 8)) * 8; }
 
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __hal
     constexpr int HALF = HD / 2, UNIT = attn_chunk<HD>();
     __shared__ float q_l[HD], k_l[HD], v_l[HD];
     __shared__ AttnLds<HD, 256> att_l;
-    const int h = blockIdx.x, sc = blockIdx.y, kv_mul = n_heads / n_kv, g = h / kv_mul;
+    const int h = blockIdx.y, sc = blockIdx.x, kv_mul = n_heads / n_kv, g = h / kv_mul;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
     const int t = threadIdx.x;
     const int pos = state[0];
@@ -535,7 +537,7 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
         auto attn = c.head_dim == 128 ? attn_split_kernel<128>
                     : (c.head_dim == 64 ? attn_split_kernel<64> : attn_split_kernel<32>);
-        attn<<<dim3(c.n_heads, kAttnShares), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
+        attn<<<dim3(kAttnShares, c.n_heads), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
                                                            m->rope, m->sh_o, m->sh_ml, c.n_heads, c.n_kv_heads,
                                                            c.seq_len, inv_sqrt_hd);
         EIF_HIP_LAUNCHED();
