@@ -34,7 +34,8 @@ struct AttnLds {
 // kcg / vcg) and, when k_x is not NULL, one more row (k_x, v_x in LDS) after them, as a share of the query's
 // attention (below). NT threads, t = 0 .. NT - 1 this thread's index among them; L the call's LDS. A thread holds
 // 8 of the HD dimensions of a key / value row: DPR = HD / 8 threads per row and RG row groups; row group r takes
-// rows r, r + RG, r + 2 RG, ... in batches of UNR rows whose keys and values are loaded together, and keeps a
+// rows r, r + RG, r + 2 RG, ... in batches of UNR = 2048 / NT rows whose keys and values are loaded together
+// (a batch covers 2048 / DPR rows whatever NT: more threads hold fewer rows each), and keeps a
 // running softmax over them (max m, sum l, the weighted value sums o of its dims):
 //   s_t = (q . k_t) / sqrt(HD), m' = max(m, s_t), l = l e^(m - m') + sum e^(s_t - m'),
 //   o = o e^(m - m') + sum e^(s_t - m') v_t;
@@ -52,7 +53,8 @@ EIF_DEV void attend(AttnLds<HD, NT> &L, int t, bool live, const float *q_l, cons
                     Pro &&pro)
 {
     using A = AttnLds<HD, NT>;
-    constexpr int DPR = A::DPR, RG = A::RG, UNR = 8, PARTS = A::PARTS;
+    constexpr int DPR = A::DPR, RG = A::RG, UNR = 2048 / NT, PARTS = A::PARTS;
+    static_assert(UNR >= 1 && RG * UNR == 2048 / DPR, "a batch of 2048 / DPR rows");
     const int sub = t % DPR, r0 = t / DPR;
     uint4 kr[UNR], vr[UNR];
     auto load_batch = [&](int base) {

@@ -60,7 +60,7 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
 }
 
 // Decode, split over the positions: workgroup (h, s) takes query head h (kv head g = h / kv_mul) over the
-// positions of chunk s, [s CH, (s + 1) CH), CH = the fewest whole UNITs (the rows one batch of attend<HD, 256>
+// positions of chunk s, [s CH, (s + 1) CH), CH = the fewest whole UNITs (the rows one batch of attend<HD, 512>
 // covers) that cover positions 0 .. pos in kAttnShares chunks; cache rows below pos, and row pos itself in the
 // chunk holding it. A chunk past pos sets its share's maximum to -inf and exits. Every workgroup rotates q_h (RoPE
 // from the table); the workgroup of the chunk holding pos also rotates k_g, rounds k and v to fp16 and, for the
@@ -71,16 +71,17 @@ __global__ void rope_table_kernel(float2 *tab, int seq_len, int hd, float theta)
 // chunks of a head first, so the dispatcher, which deals ids round-robin over the eight XCDs, puts chunk s of
 // every head on one XCD, and the query heads of a kv head read that chunk's keys and values through one L2.
 template <int HD>
-constexpr int attn_chunk() { return (256 / (HD / 8)) * 8; }
+constexpr int attn_chunk() { return 2048 / (HD / 8); }
+constexpr int kAttnThreads = 512;   // two waves per SIMD: each thread holds 4 rows of a batch
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __half *kc, __half *vc, const int *state,
+__global__ __launch_bounds__(kAttnThreads) void attn_split_kernel(const float *qkv, __half *kc, __half *vc, const int *state,
                                                          const float2 *rope, float *sh_o, float *sh_ml, int n_heads,
                                                          int n_kv, int seq_len, float inv_sqrt_hd)
 {
     constexpr int HALF = HD / 2, UNIT = attn_chunk<HD>();
     __shared__ float q_l[HD], k_l[HD], v_l[HD];
-    __shared__ AttnLds<HD, 256> att_l;
+    __shared__ AttnLds<HD, kAttnThreads> att_l;
     const int h = blockIdx.y, sc = blockIdx.x, kv_mul = n_heads / n_kv, g = h / kv_mul;
     const int q_dim = n_heads * HD, kv_dim = n_kv * HD;
     const int t = threadIdx.x;
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *qkv, __hal
     };
     const size_t base = ((size_t)g * seq_len + c0) * HD;
     const int rows = (last ? pos : c0 + ch) - c0;
-    attend<HD, 256>(att_l, t, true, q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr,
+    attend<HD, kAttnThreads>(att_l, t, true, q_l, kc + base, vc + base, rows, last ? k_l : nullptr, last ? v_l : nullptr,
                     inv_sqrt_hd, sh_o + ((size_t)h * kAttnShares + sc) * HD, ml, rotate);
 }
 
@@ -537,7 +538,7 @@ int enqueue_step(eif_hip_bitnet *m, hipStream_t st)
         const size_t cache_l = (size_t)l * c.n_kv_heads * c.seq_len * c.head_dim;
         auto attn = c.head_dim == 128 ? attn_split_kernel<128>
                     : (c.head_dim == 64 ? attn_split_kernel<64> : attn_split_kernel<32>);
-        attn<<<dim3(kAttnShares, c.n_heads), 256, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
+        attn<<<dim3(kAttnShares, c.n_heads), kAttnThreads, 0, st>>>(m->qkv, m->kc + cache_l, m->vc + cache_l, m->state,
                                                            m->rope, m->sh_o, m->sh_ml, c.n_heads, c.n_kv_heads,
                                                            c.seq_len, inv_sqrt_hd);
         EIF_HIP_LAUNCHED();

@@ -13,7 +13,7 @@
 // helpers, attn_dev.h attention) and the same reduction trees: the workgroup's 16 waves hold the columns the
 // separate launch's threads hold (threads past the row hold zeros, which leave every sum and maximum unchanged),
 // each row tile's exact per-group int32 sums are combined in group order, and the attention runs per (head,
-// chunk) on 256 threads as there. So the step gives the same bits as the separate launches.
+// chunk) on 512 threads as there. So the step gives the same bits as the separate launches.
 //
 // Work: the 16-row tiles of a linear go round-robin over the workgroups (tile j to workgroup j mod G); waves 0-13
 // run the MFMAs of a workgroup's (tile, step) pairs. Waves 14 and 15 are loaders: wave 14 streams the QKV and
@@ -47,7 +47,8 @@ constexpr int kLoadA = 14;         // loader wave of the QKV and gate|up tiles
 constexpr int kLoadB = 15;         // loader wave of the O and down tiles
 constexpr int kMW = 14;            // MFMA waves 0 .. kMW - 1
 constexpr int kPrepMaxThreads = 64 * kMW;   // a prep's live columns must lie in the non-loader waves
-constexpr int kAttnSubs = 3;       // attention items per workgroup, 256 threads each (waves 0-11)
+constexpr int kAttnSubs = 1;       // attention items per workgroup, 512 threads each (waves 0-7)
+constexpr int kAttnNT = 512;       // threads of an attention item (attn_split_kernel's)
 constexpr int kBarGroups = 8;
 constexpr long kSpinMax = 1L << 21;   // barrier polls before giving up (far beyond any stage's time)
 constexpr int kLdsLane = 16;          // LDS bytes per lane of a weight step (12- and 16-byte loads alike)
@@ -334,20 +335,21 @@ EIF_DEV void head_prep(const PArgs &a, PScratch &ps, bool loader, int tid)
 template <int HD>
 struct PAttn {
     float q_l[HD], k_l[HD], v_l[HD];
-    AttnLds<HD, 256> att;
+    AttnLds<HD, kAttnNT> att;
 };
 
 template <int HD>
-constexpr int attn_unit() { return (256 / (HD / 8)) * 8; }
+constexpr int attn_unit() { return 2048 / (HD / 8); }
 
-// S2: items (h, chunk) = 3 b + sub for sub < kAttnSubs (threads 256 sub .. 256 sub + 255); the decode attention of
-// attn_split_kernel (decode.hip) on each: RoPE of q (and of k in the chunk holding pos), fp16 KV append by the
-// kv head's first query head, attention over the chunk, the chunk's share.
+// S2: items (h, chunk) = kAttnSubs b + sub for sub < kAttnSubs (threads kAttnNT sub .. kAttnNT (sub + 1) - 1); the
+// decode attention of attn_split_kernel (decode.hip) on each: RoPE of q (and of k in the chunk holding pos), fp16
+// KV append by the kv head's first query head, attention over the chunk, the chunk's share. The other non-loader
+// waves take part in the items' barriers without work.
 template <int HD>
 EIF_DEV void attn_stage(const PArgs &a, int l, int pos, uint8_t *smem, int tid)
 {
     constexpr int HALF = HD / 2, UNIT = attn_unit<HD>();
-    const int sub = __builtin_amdgcn_readfirstlane(tid >> 8), t = tid & 255;
+    const int sub = __builtin_amdgcn_readfirstlane(tid / kAttnNT), t = tid % kAttnNT;
     const int it = kAttnSubs * (int)blockIdx.x + sub;
     const bool valid = sub < kAttnSubs && it < a.n_heads * kAttnShares;
     const int h = valid ? it / kAttnShares : 0, sc = valid ? it % kAttnShares : 0;
@@ -387,7 +389,7 @@ EIF_DEV void attn_stage(const PArgs &a, int l, int pos, uint8_t *smem, int tid)
     };
     const size_t base = cache_l + ((size_t)g * a.seq_len + c0) * HD;
     const int rows = (last ? pos : c0 + ch) - c0;
-    attend<HD, 256, 1, true>(S.att, t, live, S.q_l, a.kc + base, a.vc + base, rows, last ? S.k_l : nullptr,
+    attend<HD, kAttnNT, 1, true>(S.att, t, live, S.q_l, a.kc + base, a.vc + base, rows, last ? S.k_l : nullptr,
                              last ? S.v_l : nullptr, a.inv_sqrt_hd, a.sh_o + ((size_t)h * kAttnShares + sc) * HD, ml,
                              rotate);
 }
@@ -560,6 +562,7 @@ int persist_create(PersistPlan **out, const PersistModel &pm)
         hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || cus <= 0)
         return EIF_HIP_E_DEVICE;
     const int G = cus;
+    if (pm.n_heads * kAttnShares > kAttnSubs * G) return EIF_HIP_E_LIMIT;   // one round of attention items
     PArgs a{};
     int off = 0;
     int n_load[4];
