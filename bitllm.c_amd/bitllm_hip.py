@@ -119,6 +119,8 @@ _SIGS = {
     "eif_hip_set_gemv_prep_cols": (_i, [_i]),
     "eif_hip_set_gemm_split": (_i, [_i]),
     "eif_hip_set_gemm_token_tiles": (_i, [_i]),
+    "eif_hip_set_gemm_prefetch": (_i, [_i]),
+    "eif_hip_set_gemm_panel": (_i, [_i]),
     "eif_hip_forget_host_weights": (None, [_vp]),
     # host-pointer drop-in ABI
     "eif_unpack_ternary": (C.c_int8, [C.c_uint8, _i]),

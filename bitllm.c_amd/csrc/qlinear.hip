@@ -66,22 +66,130 @@ struct QArgs {
 //
 // Workgroup: 4 waves, 64 rows x 16*TT tokens; wave w owns rows 16w..16w+15 for all TT token tiles and walks
 // every step of K in order. Per step the workgroup stages the activation block [16*TT tokens x SC columns] in
-// LDS (double-buffered, two steps of loads in flight), each wave loads its own weight codes and scales two
-// steps ahead, decodes them once and reuses them for the TT token tiles. Grouped ternary: each group's exact
-// int32 sum is combined at once, in group order, into FP32 accumulators (the same sequence as the oracle);
-// row-scaled: one int32 sum over K.
+// LDS (double-buffered), each wave loads its own weight codes and scales, decodes them once and reuses them for
+// the TT token tiles. The loads of a step are issued PF - 1 steps before it is staged (a ring of PF register
+// buffers): a workgroup's steps form a dependent chain, and with one step of loads in flight each step waits
+// out a whole memory latency. Grouped ternary: each group's exact int32 sum is combined at once, in group
+// order, into FP32 accumulators (the same sequence as the oracle); row-scaled: one int32 sum over K.
 constexpr int kGemmThreads = 256;
 
 // Waves per SIMD the register budget is cut for: four for the g128 ternary and INT formats (their MFMA sums
-// would otherwise sit in accumulation registers, at three waves), the compiler's choice for the other group sizes
-// (g32 at four waves spilled).
-template <int FMT, int UD>
-constexpr int gemm_waves() { return FMT == kTern && UD != 4 ? 1 : 4; }
+// would otherwise sit in accumulation registers, at three waves), two with a deeper prefetch ring (launched
+// when the workgroups are few), the compiler's choice for the other group sizes (g32 at four waves spilled).
+template <int FMT, int UD, int PF>
+constexpr int gemm_waves() { return FMT == kTern && UD != 4 ? 1 : (PF > 2 ? 2 : 4); }
 
+// The GEMM's epilogue for one thread's outputs (rows `row`, tokens m0 + 16 tt + 4 s + v): xs_l holds the
+// workgroup's token scales (index tok - m0); rs and bb the row's scale (row-scaled) and bias, loaded at the
+// kernel's start so that the epilogue waits for no load. Unsplit: the outputs. Split along K (gridDim.z > 1):
+// each split stores its partial sums (the FP32 group combines, or the exact int32 sums) for this thread's
+// outputs, value-major (part[split][tile][4 TT values][256 threads]: every store and load instruction covers
+// 256 contiguous bytes), with device-coherent stores (sc1: past the XCDs' non-coherent L2s), waits for them, and
+// counts the workgroup's arrival on the tile's counter. The last split to arrive reads every split's partials
+// back with device-coherent loads, adds them in split order, writes the epilogue and resets the counter for the
+// next launch.
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
+__device__ __forceinline__ void gemm_finish(const QArgs &a, const float (&F)[TT][4], const v4i (&C)[TT], int row,
+                                            bool row_ok, int m0, int s, const float *xs_l, float rs, float bb)
+{
+    using GE = Geo<FMT, UD>;
+    if (gridDim.z > 1) {
+        const int ntile = gridDim.x * gridDim.y, tile = blockIdx.y * gridDim.x + blockIdx.x, nz = gridDim.z;
+        auto pz = [&](int z) { return a.part + ((size_t)z * ntile + tile) * (4 * TT * kGemmThreads) + threadIdx.x; };
+        float *own = pz(blockIdx.z);
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                st_coh(own + (4 * tt + v) * kGemmThreads, GROUPED ? F[tt][v] : __int_as_float(C[tt][v] >> GE::SHIFT));
+        __builtin_amdgcn_s_waitcnt(0);
+        __shared__ int last_l;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last_l = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nz - 1;
+        __syncthreads();
+        if (!last_l) return;
+        if (threadIdx.x == 0) st_coh_i(a.cnt + tile, 0);
+        // split order, the loads of four splits in flight at once (indices past the last split read it again)
+        float fs[TT][4];
+        int is[TT][4];
+        for (int z0 = 0; z0 < nz; z0 += 4) {
+            float q[4][4 * TT];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float *p = pz(min(z0 + j, nz - 1));
+#pragma unroll
+                for (int i = 0; i < 4 * TT; ++i) q[j][i] = ld_coh(p + i * kGemmThreads);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (z0 + j >= nz) break;
+#pragma unroll
+                for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float f = q[j][4 * tt + v];
+                        if constexpr (GROUPED)
+                            fs[tt][v] = z0 + j == 0 ? f : fs[tt][v] + f;
+                        else
+                            is[tt][v] = (z0 + j == 0 ? 0 : is[tt][v]) + __float_as_int(f);
+                    }
+            }
+        }
+        if (!row_ok) return;
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int lt = 16 * tt + 4 * s + v, tok = m0 + lt;
+                if (tok >= a.M) continue;
+                float out = GROUPED ? fs[tt][v] * xs_l[lt] : ((float)is[tt][v] * xs_l[lt]) * rs;
+                if (a.bias) out = out + bb;
+                a.y[(size_t)tok * a.ldy + row] = out;
+            }
+        return;
+    }
+
+    if (!row_ok) return;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int lt = 16 * tt + 4 * s + v, tok = m0 + lt;
+            if (tok >= a.M) continue;
+            float out;
+            if constexpr (GROUPED) {
+                out = F[tt][v] * xs_l[lt];
+            } else {
+                const int isum = C[tt][v] >> GE::SHIFT;
+                if constexpr (ACC) {
+                    a.acc[(size_t)tok * a.N + row] = isum;
+                    continue;
+                }
+                out = ((float)isum * xs_l[lt]) * rs;
+            }
+            if (a.bias) out = out + bb;
+            a.y[(size_t)tok * a.ldy + row] = out;
+        }
+}
+
+// The epilogue's operands of a GEMM thread, loaded at the kernel's start: the row's scale (row-scaled, else 1)
+// and bias (else 0), rows past N clamped to the last; and one token scale of the workgroup's batch (token
+// m0 + tid mod TM, clamped into the batch), which threads 0 .. TM - 1 stage in LDS.
+template <bool GROUPED, int TM>
+__device__ __forceinline__ void gemm_epilogue_loads(const QArgs &a, int row, int m0, float &rs, float &bb, float &xsv)
+{
+    const int rc = row < a.N ? row : a.N - 1;
+    rs = (!GROUPED && a.scales) ? a.scales[rc] : 1.0f;
+    bb = a.bias ? a.bias[rc] : 0.0f;
+    const int xt = m0 + (int)(threadIdx.x & (TM - 1));
+    xsv = a.xs ? a.xs[xt < a.M ? xt : a.M - 1] : 0.0f;
+}
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int TT, int PF>
 // The leading arguments (preloaded into SGPRs at wave launch, as qgemv_kernel's) duplicate the QArgs fields the
 // first loads need.
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<FMT, UD>())))
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(gemm_waves<FMT, UD, PF>())))
 void qgemm_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W, const float *__restrict__ scales,
                   int wld, int ldq, int M, int nsteps, int G, int N, QArgs a)
 {
@@ -94,6 +202,7 @@ void qgemm_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W, 
     constexpr int LDA = GE::SC + 16;               // LDS row stride of the staged block
     __shared__ __align__(16) int8_t xa[2][TM * LDA];
     __shared__ float scl[2][GROUPED ? 256 : 1];    // grouped: the step's two group scales of the 64 rows, [grp][row]
+    __shared__ float xs_l[TM];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, s = lane >> 4;
     const int row = blockIdx.x * 64 + wave * 16 + r16;   // < rows_pad
@@ -102,10 +211,15 @@ void qgemm_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W, 
     // split along K (gridDim.z > 1): this workgroup's steps [s0, s0 + ns)
     const int s0 = (int)(blockIdx.z * a.nsteps / gridDim.z);
     const int ns = (int)((blockIdx.z + 1) * a.nsteps / gridDim.z) - s0;
+    // the epilogue's operands, loaded first (the first step's wait covers them)
+    float rs, bb, xsv;
+    gemm_epilogue_loads<GROUPED, TM>(a, row, m0, rs, bb, xsv);
+    __builtin_amdgcn_sched_barrier(0);
 
-    v4i ra[2][PPT];   // a clang vector type: an array of HIP's int4 structs would live in scratch
-    uint32_t wb[2][NW];
-    float sc[2];      // grouped: the scale this thread stages, of row (tid & 63) and group (tid >> 6) of the step
+    static_assert(PF >= 2 && PF % 2 == 0, "register buffers in pairs: a step's LDS buffer is its parity");
+    v4i ra[PF][PPT];   // a clang vector type: an array of HIP's int4 structs would live in scratch
+    uint32_t wb[PF][NW];
+    float sc[PF];      // grouped: the scale this thread stages, of row (tid & 63) and group (tid >> 6) of the step
     // 32-bit byte offsets from the uniform bases (the launcher keeps the batch's int8 rows and the weights below
     // 4 GiB): the loads take the scalar-base form and a step adds st * SC (st * 4 * SB) to them.
     const uint32_t wo = (uint32_t)row * (uint32_t)a.wld + (uint32_t)(s * GE::SB);
@@ -200,120 +314,216 @@ void qgemm_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W, 
         }
     };
 
-    // The loop runs whole pairs of steps (buffer 0, then buffer 1) and has one exit, at its head; an odd last step
-    // follows it from buffer 0. Every prefetch is issued, past the split's last step as a reload of that step, and
-    // every staging store is made (past the last step into a buffer no later step reads). A load or store skipped
-    // on some path, or an exit in the middle of the loop, gives the loop head an entry with other loads in flight,
-    // and the compiler then waits there for nearly all of them.
+    // The loop runs whole rounds of PF steps (register buffer k holds step PF * p + k; LDS buffer k & 1) and has
+    // one exit, at its head; the last ns % PF steps follow it from buffers 0, 1, ... Every prefetch is issued, past
+    // the split's last step as a reload of that step, and every staging store is made (past the last step into a
+    // buffer no later step reads). A load or store skipped on some path, or an exit in the middle of the loop,
+    // gives the loop head an entry with other loads in flight, and the compiler then waits there for nearly all
+    // of them.
     const int s_last = s0 + ns - 1;
     auto clamp_step = [&](int st) { return st < s_last ? st : s_last; };
-    load_step(s0, ra[0], wb[0], sc[0]);
-    load_step(clamp_step(s0 + 1), ra[1], wb[1], sc[1]);
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load_step(clamp_step(s0 + k), ra[k], wb[k], sc[k]);
     store_step(0, s0, ra[0], sc[0]);
+    if ((int)threadIdx.x < TM) xs_l[threadIdx.x] = xsv;
+    asm volatile("" :: "v"(rs), "v"(bb));   // keeps the loads here: the compiler sinks them to their use
     __syncthreads();
-    const int npairs = ns >> 1;
-    for (int p = 0; p < npairs; ++p) {
-        const int st = s0 + 2 * p;
-        compute(0, st, wb[0]);
-        load_step(clamp_step(st + 2), ra[0], wb[0], sc[0]);
-        store_step(1, clamp_step(st + 1), ra[1], sc[1]);
-        __syncthreads();
-        compute(1, st + 1, wb[1]);
-        load_step(clamp_step(st + 3), ra[1], wb[1], sc[1]);
-        store_step(0, clamp_step(st + 2), ra[0], sc[0]);
-        __syncthreads();
-    }
-    if (ns & 1) compute(0, s_last, wb[0]);
-    if constexpr (GROUPED && ACC) return;
-
-    if (gridDim.z > 1) {
-        // Split along K. Each split stores its partial sums (the FP32 group combines, or the exact int32 sums) for
-        // this thread's outputs, value-major (part[split][tile][4 TT values][256 threads]: every store and load
-        // instruction covers 256 contiguous bytes), with device-coherent stores (sc1: past the XCDs' non-coherent
-        // L2s), waits for them, and counts the workgroup's arrival on the tile's counter. The last split to arrive
-        // reads every split's partials back with device-coherent loads, adds them in split order, writes the
-        // epilogue and resets the counter for the next launch.
-        const int ntile = gridDim.x * gridDim.y, tile = blockIdx.y * gridDim.x + blockIdx.x, nz = gridDim.z;
-        auto pz = [&](int z) { return a.part + ((size_t)z * ntile + tile) * (4 * TT * kGemmThreads) + threadIdx.x; };
-        float *own = pz(blockIdx.z);
+    const int nrounds = ns / PF;
+    for (int p = 0; p < nrounds; ++p) {
+        const int st = s0 + PF * p;
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                st_coh(own + (4 * tt + v) * kGemmThreads, GROUPED ? F[tt][v] : __int_as_float(C[tt][v] >> GE::SHIFT));
-        __builtin_amdgcn_s_waitcnt(0);
-        __shared__ int last_l;
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last_l = __hip_atomic_fetch_add(a.cnt + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nz - 1;
-        __syncthreads();
-        if (!last_l) return;
-        if (threadIdx.x == 0) st_coh_i(a.cnt + tile, 0);
-        // split order, the loads of four splits in flight at once (indices past the last split read it again)
-        float fs[TT][4];
-        int is[TT][4];
-        for (int z0 = 0; z0 < nz; z0 += 4) {
-            float q[4][4 * TT];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float *p = pz(min(z0 + j, nz - 1));
-#pragma unroll
-                for (int i = 0; i < 4 * TT; ++i) q[j][i] = ld_coh(p + i * kGemmThreads);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (z0 + j >= nz) break;
-#pragma unroll
-                for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const float f = q[j][4 * tt + v];
-                        if constexpr (GROUPED)
-                            fs[tt][v] = z0 + j == 0 ? f : fs[tt][v] + f;
-                        else
-                            is[tt][v] = (z0 + j == 0 ? 0 : is[tt][v]) + __float_as_int(f);
-                    }
-            }
+        for (int k = 0; k < PF; ++k) {
+            compute(k & 1, st + k, wb[k]);
+            load_step(clamp_step(st + k + PF), ra[k], wb[k], sc[k]);
+            store_step((k + 1) & 1, clamp_step(st + k + 1), ra[(k + 1) % PF], sc[(k + 1) % PF]);
+            __syncthreads();
         }
-        if (!row_ok) return;
-        const float rs = (!GROUPED && a.scales) ? a.scales[row] : 1.0f;
-        const float bb = a.bias ? a.bias[row] : 0.0f;
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int tok = m0 + 16 * tt + 4 * s + v;
-                if (tok >= a.M) continue;
-                float out = GROUPED ? fs[tt][v] * a.xs[tok] : ((float)is[tt][v] * a.xs[tok]) * rs;
-                if (a.bias) out = out + bb;
-                a.y[(size_t)tok * a.ldy + row] = out;
-            }
-        return;
     }
-
-    if (!row_ok) return;
-    const float rs = (!GROUPED && a.scales) ? a.scales[row] : 1.0f;
-    const float bb = a.bias ? a.bias[row] : 0.0f;
+    {
+        // buffer k holds step st + k; the first is staged in LDS buffer 0
+        const int rem = ns - PF * nrounds, st = s0 + PF * nrounds;
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int tok = m0 + 16 * tt + 4 * s + v;
-            if (tok >= a.M) continue;
-            float out;
-            if constexpr (GROUPED) {
-                out = F[tt][v] * a.xs[tok];
-            } else {
-                const int isum = C[tt][v] >> GE::SHIFT;
-                if constexpr (ACC) {
-                    a.acc[(size_t)tok * a.N + row] = isum;
-                    continue;
+        for (int k = 0; k + 1 < PF; ++k) {
+            if (k < rem) {
+                compute(k & 1, st + k, wb[k]);
+                if (k + 1 < rem) {
+                    store_step((k + 1) & 1, st + k + 1, ra[k + 1], sc[k + 1]);
+                    __syncthreads();
                 }
-                out = ((float)isum * a.xs[tok]) * rs;
             }
-            if (a.bias) out = out + bb;
-            a.y[(size_t)tok * a.ldy + row] = out;
         }
+    }
+    if constexpr (GROUPED && ACC) return;
+    gemm_finish<FMT, UD, GROUPED, ACC, TT>(a, F, C, row, row_ok, m0, s, xs_l, rs, bb);
+}
+
+// ---- token-batch GEMM with the activation panel resident in LDS (launches of few workgroups) ----
+//
+// In qgemm_kernel each step of K is a chain: the activation block's loads, its LDS stores, a barrier, the LDS
+// reads, the MFMAs. With one or two workgroups per CU nothing hides that chain (a step of 256 columns took about
+// 350 ns at one workgroup per CU). This form stages the workgroup's whole activation panel [16*TT tokens x the
+// split's columns] and, grouped, the 64 rows' group scales of those columns in LDS once, then each wave streams
+// its weight codes through a ring of PF steps of loads in flight and reads its operands from LDS, with no barrier
+// in the K loop. Tiles, MFMAs, the order of the group combine and the epilogue are qgemm_kernel's: the same bits.
+constexpr int kPanelBatch = 8;   // group scales a thread has in flight at once
+
+template <int FMT, int UD, bool GROUPED, int TT>
+size_t panel_lds_bytes(int ns)
+{
+    return (size_t)16 * TT * (ns * Geo<FMT, UD>::SC + 16) + (GROUPED ? (size_t)2 * ns * 64 * sizeof(float) : 0);
+}
+
+template <int FMT, int UD, bool GROUPED, bool ACC, int TT, int PF>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void qgemm_panel_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W,
+                        const float *__restrict__ scales, int wld, int ldq, int M, int nsteps, int G, int N, QArgs a)
+{
+    a.xq = xq, a.W = W, a.scales = scales, a.wld = wld, a.ldq = ldq, a.M = M, a.nsteps = nsteps, a.G = G, a.N = N;
+    using GE = Geo<FMT, UD>;
+    constexpr int NW = GE::SB / 4;
+    constexpr int TM = 16 * TT;
+    constexpr int PR = GE::SC / 16;                // 16-byte pieces per token per step
+    extern __shared__ __align__(16) int8_t pan[];  // [TM][ldp] int8 activations, then grouped [2 ns][64] scales
+    __shared__ float xs_l[TM];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, s = lane >> 4;
+    const int row = blockIdx.x * 64 + wave * 16 + r16;   // < rows_pad
+    const bool row_ok = row < a.N;
+    const int m0 = blockIdx.y * TM;
+    const int s0 = (int)(blockIdx.z * a.nsteps / gridDim.z);
+    const int ns = (int)((blockIdx.z + 1) * a.nsteps / gridDim.z) - s0;
+    const int ldp = ns * GE::SC + 16;              // panel row stride: 16-byte aligned rows, 16 bytes apart in bank
+    float *spn = reinterpret_cast<float *>(pan + TM * ldp);
+
+    float rs, bb, xsv;
+    gemm_epilogue_loads<GROUPED, TM>(a, row, m0, rs, bb, xsv);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the weight codes of the first PF steps (32-bit offsets from the uniform base, as qgemm_kernel)
+    const uint32_t wo = (uint32_t)row * (uint32_t)a.wld + (uint32_t)(s * GE::SB);
+    const int s_last = s0 + ns - 1;
+    auto clamp_step = [&](int st) { return st < s_last ? st : s_last; };
+    uint32_t wb[PF][NW];
+    auto load_w = [&](int st, uint32_t (&w)[NW]) __attribute__((always_inline)) {
+        load_words<NW>(a.W + (wo + (uint32_t)(st * 4 * GE::SB)), w);
+    };
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load_w(clamp_step(s0 + k), wb[k]);
+
+    // the panel: thread t takes pieces t, t + 256, ... of every token row, the TM rows' loads in flight at once
+    // (pieces past the row re-read its last one and are not stored; token rows past the batch repeat its last)
+    constexpr int TR = TM < 32 ? TM : 32;   // token rows per pass (a 64-token panel takes two)
+    const int prow = ns * PR;
+    for (int q0 = 0; q0 < prow; q0 += kGemmThreads) {
+        const int q = q0 + (int)threadIdx.x, qc = q < prow ? q : prow - 1;
+#pragma unroll
+        for (int t0 = 0; t0 < TM; t0 += TR) {
+            v4i v[TR];
+#pragma unroll
+            for (int t = 0; t < TR; ++t) {
+                const int tok = m0 + t0 + t < a.M ? m0 + t0 + t : a.M - 1;
+                v[t] = *reinterpret_cast<const v4i *>(a.xq + ((uint32_t)tok * (uint32_t)a.ldq +
+                                                              (uint32_t)(s0 * GE::SC + 16 * qc)));
+            }
+            if (q < prow) {
+#pragma unroll
+                for (int t = 0; t < TR; ++t) *reinterpret_cast<v4i *>(pan + (t0 + t) * ldp + 16 * q) = v[t];
+            }
+        }
+    }
+    // grouped: spn[lg][r] = scale of row 64 blockIdx.x + r, group 2 s0 + lg, times 2^-SHIFT (0 past the row's
+    // last group, which then adds nothing: F + 0 * x == F). Thread t reads row t / 4, groups t % 4 + 4 i.
+    constexpr float kUnshift = 1.0f / (float)(1 << GE::SHIFT);
+    if constexpr (GROUPED) {
+        const int ng = 2 * ns, r = (int)threadIdx.x >> 2, sr = blockIdx.x * 64 + r;
+        const uint32_t so = (uint32_t)(sr < a.N ? sr : a.N - 1) * (uint32_t)a.G;
+        for (int l0 = (int)threadIdx.x & 3; l0 < ng; l0 += 4 * kPanelBatch) {
+            float c[kPanelBatch];
+#pragma unroll
+            for (int i = 0; i < kPanelBatch; ++i) {
+                const int gi = 2 * s0 + l0 + 4 * i;
+                c[i] = a.scales[so + (uint32_t)(gi < a.G ? gi : a.G - 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < kPanelBatch; ++i) {
+                const int lg = l0 + 4 * i;
+                if (lg < ng) spn[lg * 64 + r] = 2 * s0 + lg < a.G ? c[i] * kUnshift : 0.0f;
+            }
+        }
+    }
+    if ((int)threadIdx.x < TM) xs_l[threadIdx.x] = xsv;
+    asm volatile("" :: "v"(rs), "v"(bb));   // keeps the loads here: the compiler sinks them to their use
+    __syncthreads();
+
+    float F[TT][4];
+    v4i C[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        C[tt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) F[tt][v] = 0.0f;
+    }
+    auto compute = [&](int st, const uint32_t (&w)[NW]) __attribute__((always_inline)) {
+        long bop[GE::NMF];
+        decode<FMT, UD>(w, bop);
+        const int ls = st - s0;
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+            const int8_t *xl = pan + (16 * tt + r16) * ldp + ls * GE::SC;
+            if constexpr (FMT == kTern) {
+                auto group = [&](auto grp_c) __attribute__((always_inline)) {
+                    constexpr int grp = decltype(grp_c)::value;
+                    long aop[UD];
+                    load_ops<UD, (UD % 2 == 0)>(xl + 32 * UD * grp + 8 * UD * s, aop);
+                    v4i cc = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C[tt]);
+                    if constexpr (GROUPED) {
+                        const int gi = 2 * st + grp;
+                        if constexpr (ACC) {
+                            if (gi < a.G) {
+#pragma unroll
+                                for (int v = 0; v < 4; ++v) {
+                                    const int tok = m0 + 16 * tt + 4 * s + v;
+                                    if (row_ok && tok < a.M)
+                                        a.acc[((size_t)tok * a.N + row) * a.G + gi] = cc[v] >> GE::SHIFT;
+                                }
+                            }
+                        } else {
+                            const float cu = spn[(2 * ls + grp) * 64 + 16 * wave + r16];
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
+                        }
+                    } else {
+                        C[tt] = cc;
+                    }
+                };
+                group(std::integral_constant<int, 0>{});
+                group(std::integral_constant<int, 1>{});
+            } else {
+                long aop[GE::NMF];
+                load_ops<GE::NMF, true>(xl + (GE::SC / 4) * s, aop);
+                C[tt] = mfma_ops<0>(aop, bop, C[tt]);
+            }
+        }
+    };
+    // whole rounds of PF steps (register buffer k holds step PF * p + k), then the last ns % PF steps; every
+    // prefetch is issued (past the split's last step a reload of it), so the loop head has one set of loads in flight
+    const int nrounds = ns / PF;
+    for (int p = 0; p < nrounds; ++p) {
+        const int st = s0 + PF * p;
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            compute(st + k, wb[k]);
+            load_w(clamp_step(st + k + PF), wb[k]);
+        }
+    }
+    {
+        const int rem = ns - PF * nrounds, st = s0 + PF * nrounds;
+#pragma unroll
+        for (int k = 0; k + 1 < PF; ++k)
+            if (k < rem) compute(st + k, wb[k]);
+    }
+    if constexpr (GROUPED && ACC) return;
+    gemm_finish<FMT, UD, GROUPED, ACC, TT>(a, F, C, row, row_ok, m0, s, xs_l, rs, bb);
 }
 
 // ---- small-batch GEMV (M <= kGemvMaxM): RT 16-row tiles per workgroup, ks waves per tile ----
@@ -1252,6 +1462,42 @@ int pick_split(QArgs &a, int tiles, int nv, hipStream_t st)
     return ks;
 }
 
+int g_gemm_pf = 0;   // register buffers of the GEMM's prefetch ring (2, 4, 8), 0 = chosen from the launch
+int g_gemm_panel = 0;   // the GEMM's panel form: 0 = for few workgroups, 1 = wherever its LDS fits, -1 = off
+
+// LDS a workgroup may allocate on the current device (160 KiB on gfx950), read once per process.
+size_t gemm_max_lds()
+{
+    static const size_t bytes = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            return (size_t)65536;
+        return (size_t)v;
+    }();
+    return bytes;
+}
+
+// Form and prefetch ring of a GEMM launch of `wgs` workgroups (tiles x splits) whose K loops take up to ns steps
+// (pf > 0: the tiled form with that ring; pf < 0: the panel form with ring -pf). Measured per linear (µs, a launch
+// in a graph of launches, weights rotated past the Infinity Cache):
+// - more than two workgroups per CU: tiled, ring 2 (their four waves per SIMD hide each other's latency);
+// - grouped ternary split along K, or with a K loop of 20 steps or more: panel, ring 4 (down 2560x6912 g96 at 64
+//   tokens, three splits: 8.8 against 10.7 tiled; unsplit 11.2 against 15.8); else tiled, ring 4 while the
+//   workgroups number at most one per CU (QKV 3840x2560 at 64 tokens 5.6 against 6.2 with ring 2, 6.4 as a
+//   panel), ring 2 above (gate+up 13824x2560 at 64 tokens 10.0 against 10.9, 14.6 as a panel);
+// - row-scaled INT8 / INT4: an unsplit launch of one to four workgroups per CU: panel, ring 8 (INT8 9728x896 at
+//   128 tokens 10.6 against 11.8 tiled); else tiled as above (the split INT8 896x4864 at 128 tokens 10.0 tiled,
+//   11.7 as a panel).
+int gemm_form(bool grouped, int wgs, int ks, int ns)
+{
+    const int C = device_cus();
+    if (!grouped && ks == 1 && wgs > C && wgs <= 4 * C) return -8;
+    if (wgs > 2 * C) return 2;
+    if (grouped && (ks > 1 || ns >= 20)) return -4;
+    return wgs <= C ? 4 : 2;
+}
+
 template <int FMT, int UD, bool GROUPED, bool ACC, int TT>
 int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
 {
@@ -1263,10 +1509,39 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     if (ks == -2) return EIF_HIP_E_DEVICE;
     if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
-    qgemm_kernel<FMT, UD, GROUPED, ACC, TT><<<grid, kGemmThreads, 0, st>>>(a.xq, a.W, a.scales, a.wld, a.ldq, a.M,
-                                                                           a.nsteps, a.G, a.N, a);
-    EIF_HIP_LAUNCHED();
-    return EIF_HIP_OK;
+    const int ns = eif_ceil_div(a.nsteps, ks);
+    int form = ACC ? 2 : gemm_form(GROUPED, tiles * ks, ks, ns);
+    if (g_gemm_panel != 0 && !ACC) form = g_gemm_panel > 0 ? -std::abs(form) : std::abs(form);
+    if (g_gemm_pf > 0 && !ACC) form = form < 0 ? -std::max(g_gemm_pf, 4) : g_gemm_pf;
+    if constexpr (!ACC) {
+        // the panel form where its LDS fits
+        const size_t plds = panel_lds_bytes<FMT, UD, GROUPED, TT>(ns);
+        if (form < 0 && plds + 4 * 16 * TT + 64 <= gemm_max_lds()) {
+            auto go_p = [&](auto pf_c) -> int {
+                qgemm_panel_kernel<FMT, UD, GROUPED, ACC, TT, decltype(pf_c)::value><<<grid, kGemmThreads, plds, st>>>(
+                    a.xq, a.W, a.scales, a.wld, a.ldq, a.M, a.nsteps, a.G, a.N, a);
+                EIF_HIP_LAUNCHED();
+                return EIF_HIP_OK;
+            };
+            if constexpr (TT < 4)
+                if (form == -8) return go_p(std::integral_constant<int, 8>{});
+            return go_p(std::integral_constant<int, 4>{});
+        }
+    }
+    // a ring of 8 with 64-token tiles would spill (its activation pieces take 8 registers a step): 4 there
+    const int pf = std::abs(form) > 4 && TT == 4 ? 4 : std::abs(form);
+    auto go = [&](auto pf_c) -> int {
+        qgemm_kernel<FMT, UD, GROUPED, ACC, TT, decltype(pf_c)::value><<<grid, kGemmThreads, 0, st>>>(
+            a.xq, a.W, a.scales, a.wld, a.ldq, a.M, a.nsteps, a.G, a.N, a);
+        EIF_HIP_LAUNCHED();
+        return EIF_HIP_OK;
+    };
+    if constexpr (!ACC) {
+        if (pf == 4) return go(std::integral_constant<int, 4>{});
+        if constexpr (TT < 4)
+            if (pf == 8) return go(std::integral_constant<int, 8>{});
+    }
+    return go(std::integral_constant<int, 2>{});
 }
 
 // Token tile of the GEMM: 16, 32 or 64 tokens (gemm_tt).
@@ -2108,6 +2383,20 @@ int eif_hip_set_gemv_rowpair(int mode)
 {
     const int old = g_gemv_rowpair;
     if (mode >= -1 && mode <= 1) g_gemv_rowpair = mode;
+    return old;
+}
+
+int eif_hip_set_gemm_panel(int mode)
+{
+    const int old = g_gemm_panel;
+    if (mode >= -1 && mode <= 1) g_gemm_panel = mode;
+    return old;
+}
+
+int eif_hip_set_gemm_prefetch(int pf)
+{
+    const int old = g_gemm_pf;
+    if (pf == 0 || pf == 2 || pf == 4 || pf == 8) g_gemm_pf = pf;
     return old;
 }
 

@@ -268,6 +268,18 @@ int eif_hip_set_gemm_split(int k);
  * tokens, 2 up to 32, else 4). Returns the previous setting. A tuning knob: results do not depend on it.     */
 int eif_hip_set_gemm_token_tiles(int tt);
 
+/* Steps of K whose loads the GEMM keeps in flight per workgroup (2, 4 or 8; 0 = chosen from the launch, the
+ * default: 4 or 8 for launches of few workgroups, 2 for more than two per CU; 8 is taken as 4 for 64-token
+ * tiles, and the panel form below takes at least 4). Returns the previous setting. A tuning knob: results do
+ * not depend on it.                                                                                      */
+int eif_hip_set_gemm_prefetch(int pf);
+
+/* The GEMM's panel form, which stages a workgroup's whole activation panel (and its rows' group scales) in LDS
+ * once and runs the K loop without barriers: 0 = chosen from the launch (the default: long K loops of few
+ * workgroups, and unsplit INT8 / INT4 launches of one to four workgroups per CU), 1 = wherever its LDS fits,
+ * -1 = never. Returns the previous setting. A tuning knob: results do not depend on it.                  */
+int eif_hip_set_gemm_panel(int mode);
+
 #ifdef __cplusplus
 }
 #endif

@@ -145,6 +145,75 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
         qw.close()
 
 
+@pytest.mark.parametrize("fmt,N,K,g,M", [
+    ("tern", 200, 2560, 128, 40),    # 20 steps: rounds of 8 with 4 left, of 4 with none
+    ("tern", 96, 2688, 128, 17),     # 21 steps: 5, 1 and 1 left for rings of 8, 4, 2
+    ("tern", 130, 200, 32, 20),      # g32: 2 steps, fewer than the ring
+    ("tern", 2560, 6912, 96, 64),    # g96 down projection, 72 steps
+    ("tern", 70, 640, 64, 33),
+    ("int8", 896, 4864, 0, 70),
+    ("int4", 512, 1024, 0, 48),
+])
+def test_gemm_forms(gpu, oracle, fmt, N, K, g, M):
+    """The GEMM's tiled form with each prefetch ring (2, 4, 8 steps of loads in flight) and its panel form
+    (activation panel resident in LDS; rings of 4 and 8), with every token tile, unsplit and split: integer sums
+    exact; unsplit outputs bit-exact against the oracle, split ones within tolerance and the same bits in every
+    form."""
+    lib = gpu.load()
+    if fmt == "tern":
+        w, s = synth.ternary_weight((65, N, K, g), N, K, g)
+        qw = gpu.QWeight(gpu.W_TERNARY, N, K, g, w, s)
+    elif fmt == "int8":
+        w, s = synth.int8_weight((66, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT8, N, K, 0, w, s)
+    else:
+        w, s = synth.int4_weight((67, N, K), N, K)
+        qw = gpu.QWeight(gpu.W_INT4, N, K, 0, w, s)
+    x = synth.activations((68, M, K), M, K)
+    xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+    bias = synth.rng(69, N).standard_normal(N).astype(np.float32)
+    oy = np.zeros((M, N), np.float32)
+    if fmt == "tern":
+        ng = -(-K // g)
+        oacc = np.zeros((M, N, ng), np.int32)
+        oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+        oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+        mag = np.einsum("mng,ng->mn", np.abs(oacc).astype(np.float64), s.astype(np.float64)) * xs[:, None]
+        mag = mag + np.abs(bias)[None, :]
+    else:
+        wi = w.astype(np.int64) if fmt == "int8" else synth.unpack_int4(w, K).astype(np.int64)
+        oacc = (xq[:, :K].astype(np.int64) @ wi.T).astype(np.int32)
+        fn = oracle.orc_int8_gemv_i8act if fmt == "int8" else oracle.orc_int4_gemv_i8act
+        fn(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+    try:
+        for tt in (1, 2, 4):
+            lib.eif_hip_set_gemm_token_tiles(tt)
+            for ks in (1, 3):
+                lib.eif_hip_set_gemm_split(ks)
+                first = None
+                for panel, pf in [(-1, 2), (-1, 4), (-1, 8), (1, 4), (1, 8)]:
+                    lib.eif_hip_set_gemm_panel(panel)
+                    lib.eif_hip_set_gemm_prefetch(pf)
+                    y = run_linear(gpu, qw, xq_d, xs_d, M, GEMM, bias)
+                    case = (tt, ks, panel, pf)
+                    if fmt != "tern" or ks == 1:
+                        assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), case
+                    else:
+                        err = np.abs(y.astype(np.float64) - oy) / (mag + 1e-30)
+                        assert err.max() <= REL_TOL, (case, err.max())
+                    if first is None:
+                        first = y
+                    assert np.array_equal(y.view(np.uint32), first.view(np.uint32)), case
+            acc = run_acc(gpu, qw, xq_d, M, oacc.shape, GEMM)
+            assert np.array_equal(acc, oacc), tt
+    finally:
+        lib.eif_hip_set_gemm_panel(0)
+        lib.eif_hip_set_gemm_prefetch(0)
+        lib.eif_hip_set_gemm_split(0)
+        lib.eif_hip_set_gemm_token_tiles(0)
+        qw.close()
+
+
 @pytest.mark.parametrize("fmt,N,K,g,M", [("tern", 2560, 6912, 96, 64), ("tern", 640, 2560, 128, 40),
                                           ("int8", 896, 4864, 0, 128), ("int4", 512, 1024, 0, 32)])
 def test_gemm_split(gpu, oracle, fmt, N, K, g, M):
