@@ -463,19 +463,40 @@ void qgemm_panel_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict
 #pragma unroll
         for (int v = 0; v < 4; ++v) F[tt][v] = 0.0f;
     }
-    auto compute = [&](int st, const uint32_t (&w)[NW]) __attribute__((always_inline)) {
-        long bop[GE::NMF];
-        decode<FMT, UD>(w, bop);
+    // The K loop is pipelined by hand: a step's LDS operands (and group scales) are read one step ahead, and a
+    // scheduling barrier closes every step, so that the compiler does not hoist the next steps' code decodes
+    // above this step's MFMAs (it did, and then waited for every weight load in flight at each round's start).
+    constexpr int NG = FMT == kTern ? 2 : 1;          // operand groups of a step
+    constexpr int NO = FMT == kTern ? UD : GE::NMF;   // 8-byte operands of a group
+    long A[2][TT][NG][NO];
+    float cu[2][NG];
+    auto read_ops = [&](int st, long (&o)[TT][NG][NO], float (&c)[NG]) __attribute__((always_inline)) {
         const int ls = st - s0;
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
             const int8_t *xl = pan + (16 * tt + r16) * ldp + ls * GE::SC;
             if constexpr (FMT == kTern) {
+                load_ops<UD, (UD % 2 == 0)>(xl + 8 * UD * s, o[tt][0]);
+                load_ops<UD, (UD % 2 == 0)>(xl + 32 * UD + 8 * UD * s, o[tt][1]);
+            } else {
+                load_ops<GE::NMF, true>(xl + (GE::SC / 4) * s, o[tt][0]);
+            }
+        }
+        if constexpr (GROUPED && !ACC) {
+            c[0] = spn[(2 * ls) * 64 + 16 * wave + r16];
+            c[1] = spn[(2 * ls + 1) * 64 + 16 * wave + r16];
+        }
+    };
+    auto compute = [&](int st, const uint32_t (&w)[NW], const long (&o)[TT][NG][NO], const float (&c)[NG])
+        __attribute__((always_inline)) {
+        long bop[GE::NMF];
+        decode<FMT, UD>(w, bop);
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+            if constexpr (FMT == kTern) {
                 auto group = [&](auto grp_c) __attribute__((always_inline)) {
                     constexpr int grp = decltype(grp_c)::value;
-                    long aop[UD];
-                    load_ops<UD, (UD % 2 == 0)>(xl + 32 * UD * grp + 8 * UD * s, aop);
-                    v4i cc = mfma_ops<grp * UD>(aop, bop, GROUPED ? v4i{0, 0, 0, 0} : C[tt]);
+                    v4i cc = mfma_ops<grp * UD>(o[tt][grp], bop, GROUPED ? v4i{0, 0, 0, 0} : C[tt]);
                     if constexpr (GROUPED) {
                         const int gi = 2 * st + grp;
                         if constexpr (ACC) {
@@ -488,9 +509,8 @@ void qgemm_panel_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict
                                 }
                             }
                         } else {
-                            const float cu = spn[(2 * ls + grp) * 64 + 16 * wave + r16];
 #pragma unroll
-                            for (int v = 0; v < 4; ++v) F[tt][v] = fmaf((float)cc[v], cu, F[tt][v]);
+                            for (int v = 0; v < 4; ++v) F[tt][v] = fmaf((float)cc[v], c[grp], F[tt][v]);
                         }
                     } else {
                         C[tt] = cc;
@@ -499,28 +519,33 @@ void qgemm_panel_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict
                 group(std::integral_constant<int, 0>{});
                 group(std::integral_constant<int, 1>{});
             } else {
-                long aop[GE::NMF];
-                load_ops<GE::NMF, true>(xl + (GE::SC / 4) * s, aop);
-                C[tt] = mfma_ops<0>(aop, bop, C[tt]);
+                C[tt] = mfma_ops<0>(o[tt][0], bop, C[tt]);
             }
         }
     };
-    // whole rounds of PF steps (register buffer k holds step PF * p + k), then the last ns % PF steps; every
-    // prefetch is issued (past the split's last step a reload of it), so the loop head has one set of loads in flight
+    // whole rounds of PF steps (register buffer k holds step PF * p + k; operand buffer k & 1), then the last
+    // ns % PF steps; every prefetch is issued (past the split's last step a reload of it), so the loop head has
+    // one set of loads in flight
+    read_ops(s0, A[0], cu[0]);
     const int nrounds = ns / PF;
     for (int p = 0; p < nrounds; ++p) {
         const int st = s0 + PF * p;
 #pragma unroll
         for (int k = 0; k < PF; ++k) {
-            compute(st + k, wb[k]);
+            read_ops(clamp_step(st + k + 1), A[(k + 1) & 1], cu[(k + 1) & 1]);
+            compute(st + k, wb[k], A[k & 1], cu[k & 1]);
             load_w(clamp_step(st + k + PF), wb[k]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     {
         const int rem = ns - PF * nrounds, st = s0 + PF * nrounds;
 #pragma unroll
         for (int k = 0; k + 1 < PF; ++k)
-            if (k < rem) compute(st + k, wb[k]);
+            if (k < rem) {
+                read_ops(clamp_step(st + k + 1), A[(k + 1) & 1], cu[(k + 1) & 1]);
+                compute(st + k, wb[k], A[k & 1], cu[k & 1]);
+            }
     }
     if constexpr (GROUPED && ACC) return;
     gemm_finish<FMT, UD, GROUPED, ACC, TT>(a, F, C, row, row_ok, m0, s, xs_l, rs, bb);
@@ -1478,23 +1503,26 @@ size_t gemm_max_lds()
     return bytes;
 }
 
-// Form and prefetch ring of a GEMM launch of `wgs` workgroups (tiles x splits) whose K loops take up to ns steps
-// (pf > 0: the tiled form with that ring; pf < 0: the panel form with ring -pf). Measured per linear (µs, a launch
-// in a graph of launches, weights rotated past the Infinity Cache):
-// - more than two workgroups per CU: tiled, ring 2 (their four waves per SIMD hide each other's latency);
-// - grouped ternary split along K, or with a K loop of 20 steps or more: panel, ring 4 (down 2560x6912 g96 at 64
-//   tokens, three splits: 8.8 against 10.7 tiled; unsplit 11.2 against 15.8); else tiled, ring 4 while the
-//   workgroups number at most one per CU (QKV 3840x2560 at 64 tokens 5.6 against 6.2 with ring 2, 6.4 as a
-//   panel), ring 2 above (gate+up 13824x2560 at 64 tokens 10.0 against 10.9, 14.6 as a panel);
-// - row-scaled INT8 / INT4: an unsplit launch of one to four workgroups per CU: panel, ring 8 (INT8 9728x896 at
-//   128 tokens 10.6 against 11.8 tiled); else tiled as above (the split INT8 896x4864 at 128 tokens 10.0 tiled,
-//   11.7 as a panel).
-int gemm_form(bool grouped, int wgs, int ks, int ns)
+// Form and prefetch ring of a GEMM launch of `wgs` workgroups (tiles x splits ks) whose K loops take up to ns
+// steps, with `wpc` panel workgroups fitting a CU's LDS (pf > 0: the tiled form with that ring; pf < 0: the
+// panel form with ring -pf). Measured per linear (µs, a launch in a graph of launches, weights rotated past the
+// Infinity Cache):
+// - row-scaled INT8 / INT4, an unsplit launch of one to four workgroups per CU that all fit at once: panel,
+//   ring 8 (INT8 9728x896 at 128 tokens 10.4 against 11.8 tiled);
+// - more than two workgroups per CU otherwise: tiled, ring 2 (four waves per SIMD hide each other's latency);
+// - grouped ternary, every panel workgroup resident at once, and split along K, or a K loop of 20 steps or
+//   more, or more workgroups than CUs: panel, ring 4 (down 2560x6912 g96 at 64 tokens, three splits: 8.5
+//   against 10.6 tiled; gate+up 13824x2560 at 32 tokens 8.1 against 8.7);
+// - else tiled, ring 4 with at most one workgroup per CU (QKV 3840x2560 at 64 tokens 5.6 against 6.2 with
+//   ring 2), ring 2 above (gate+up at 64 tokens, whose 87 KB panels fit one a CU: 10.0 against 11.1 with ring
+//   4, 12.7 as a panel).
+int gemm_form(bool grouped, int wgs, int ks, int ns, int wpc)
 {
     const int C = device_cus();
-    if (!grouped && ks == 1 && wgs > C && wgs <= 4 * C) return -8;
+    const bool resident = wgs <= C * wpc;
+    if (!grouped && ks == 1 && wgs > C && wgs <= 4 * C && resident) return -8;
     if (wgs > 2 * C) return 2;
-    if (grouped && (ks > 1 || ns >= 20)) return -4;
+    if (grouped && resident && (ks > 1 || ns >= 20 || wgs > C)) return -4;
     return wgs <= C ? 4 : 2;
 }
 
@@ -1510,13 +1538,15 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
     const int ns = eif_ceil_div(a.nsteps, ks);
-    int form = ACC ? 2 : gemm_form(GROUPED, tiles * ks, ks, ns);
+    // panel workgroups a CU holds: by LDS, at most three (their registers)
+    const size_t plds = panel_lds_bytes<FMT, UD, GROUPED, TT>(ns), pfoot = plds + 4 * 16 * TT + 64;
+    const int wpc = (int)std::min<size_t>(3, gemm_max_lds() / pfoot);
+    int form = ACC ? 2 : gemm_form(GROUPED, tiles * ks, ks, ns, wpc);
     if (g_gemm_panel != 0 && !ACC) form = g_gemm_panel > 0 ? -std::abs(form) : std::abs(form);
     if (g_gemm_pf > 0 && !ACC) form = form < 0 ? -std::max(g_gemm_pf, 4) : g_gemm_pf;
     if constexpr (!ACC) {
         // the panel form where its LDS fits
-        const size_t plds = panel_lds_bytes<FMT, UD, GROUPED, TT>(ns);
-        if (form < 0 && plds + 4 * 16 * TT + 64 <= gemm_max_lds()) {
+        if (form < 0 && wpc >= 1) {
             auto go_p = [&](auto pf_c) -> int {
                 qgemm_panel_kernel<FMT, UD, GROUPED, ACC, TT, decltype(pf_c)::value><<<grid, kGemmThreads, plds, st>>>(
                     a.xq, a.W, a.scales, a.wld, a.ldq, a.M, a.nsteps, a.G, a.N, a);

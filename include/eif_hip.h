@@ -275,9 +275,10 @@ int eif_hip_set_gemm_token_tiles(int tt);
 int eif_hip_set_gemm_prefetch(int pf);
 
 /* The GEMM's panel form, which stages a workgroup's whole activation panel (and its rows' group scales) in LDS
- * once and runs the K loop without barriers: 0 = chosen from the launch (the default: long K loops of few
- * workgroups, and unsplit INT8 / INT4 launches of one to four workgroups per CU), 1 = wherever its LDS fits,
- * -1 = never. Returns the previous setting. A tuning knob: results do not depend on it.                  */
+ * once and runs the K loop without barriers: 0 = chosen from the launch (the default: launches whose panel
+ * workgroups all fit the CUs' LDS at once, grouped ternary split along K, with long K loops or more
+ * workgroups than CUs, and unsplit INT8 / INT4 launches of one to four workgroups per CU), 1 = wherever its
+ * LDS fits, -1 = never. Returns the previous setting. A tuning knob: results do not depend on it.          */
 int eif_hip_set_gemm_panel(int mode);
 
 #ifdef __cplusplus
