@@ -1008,7 +1008,7 @@ __global__ __launch_bounds__(1024) void qgemv_kernel(const void *__restrict__ r0
 // output bits are the same.
 constexpr int kStreamThreads = 256;
 
-template <int FMT, int UD, bool ACC, int NS, int TT>
+template <int FMT, int UD, bool ACC, int NS, int TT, bool TMJ>
 __global__ __launch_bounds__(kStreamThreads) void qstream_kernel(const int8_t *__restrict__ xq, const uint8_t *__restrict__ W,
                                                                   const float *__restrict__ scales, int wld, int ldq,
                                                                   int M, int N, int ntiles, QArgs a)
@@ -1045,8 +1045,20 @@ __global__ __launch_bounds__(kStreamThreads) void qstream_kernel(const int8_t *_
     auto load = [&](uint32_t (&w)[NS][NW], float &rs, float &bb, int tile) {
         const int row = min(tile, ntiles - 1) * 16 + r16;
         const uint8_t *wp = a.W + (size_t)row * a.wld + s * GE::SB;
+        if constexpr (TMJ) {   // W is the tile-major copy: 1 KB of whole lines a load instruction
+            const uint8_t *tp = a.W + (size_t)min(tile, ntiles - 1) * NS * 64 * GE::SB + 16 * lane;
 #pragma unroll
-        for (int st = 0; st < NS; ++st) load_words<NW>(wp + (size_t)st * 4 * GE::SB, w[st]);
+            for (int st = 0; st < NS; ++st)
+#pragma unroll
+                for (int j = 0; j < NW / 4; ++j) {
+                    const v4i v = __builtin_nontemporal_load(
+                        reinterpret_cast<const v4i *>(tp + ((size_t)st * (NW / 4) + j) * 1024));
+                    w[st][4 * j] = v[0], w[st][4 * j + 1] = v[1], w[st][4 * j + 2] = v[2], w[st][4 * j + 3] = v[3];
+                }
+        } else {
+#pragma unroll
+            for (int st = 0; st < NS; ++st) load_words<NW>(wp + (size_t)st * 4 * GE::SB, w[st]);
+        }
         const int rc = min(row, a.N - 1);
         const float *sp0 = a.scales ? a.scales + rc : reinterpret_cast<const float *>(wp);
         rs = *sp0;
@@ -1275,6 +1287,25 @@ EIF_DEV int tern_code(const uint8_t *src, int sld, int rows, int cols, int r, in
     return code == 1u ? 1 : (code == 2u ? -1 : 0);
 }
 
+// The tile-major copy of a row-scaled INT4 / INT8 matrix for the streaming GEMV: block (tile, step) holds the 64
+// lanes' code bytes of that step in SB / 16 sub-blocks of 1 KB, sub-block j holding lane L's j-th 16-byte piece at
+// L * 16, where lane L = 16 s + r reads row 16 tile + r, bytes 4 SB step + SB s + 16 j of the row-tile layout.
+// One load instruction of a wave then covers 1 KB of whole cache lines. Thread i copies 16-byte piece i.
+__global__ void tile_major_kernel(const uint4 *__restrict__ src, int wld, int nsteps, int sb, uint4 *__restrict__ dst,
+                                  size_t n)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int L = (int)(i & 63), nj = sb / 16;
+    const size_t blk = i >> 6;                       // (tile, step, j)
+    const int j = (int)(blk % nj);
+    const size_t ts = blk / nj;
+    const int step = (int)(ts % nsteps);
+    const size_t tile = ts / nsteps;
+    const size_t off = (tile * 16 + (L & 15)) * (size_t)wld + (size_t)4 * sb * step + (size_t)sb * (L >> 4) + 16 * j;
+    dst[i] = src[off / 16];
+}
+
 __global__ void repack_ternary_kernel(const uint8_t *__restrict__ src, int rows, int cols, int ud,
                                       uint32_t *__restrict__ dst, int rows_pad, int dw_per_row)
 {
@@ -1336,6 +1367,7 @@ struct eif_hip_qweight {
     int fmt, rows, cols, group, ud, kpad, rows_pad, nsteps, wld, ngroups;
     uint8_t *w;       // GPU layout
     float *scales;    // grouped [rows, ngroups] or row [rows]; NULL = 1
+    uint8_t *tm;      // vocabulary-sized row-scaled INT4 / INT8 of 8 or 16 steps: the tile-major copy, else NULL
     size_t bytes;
 };
 
@@ -1890,37 +1922,40 @@ int launch_gemv_m(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
 
 int g_gemv_rowpair = 0;   // 0 = vocabulary-sized matrices, 1 = every shape it takes, -1 = off
 int g_gemv_stream = 0;   // streaming GEMV: waves per CU (0 = the default, -1 = off)
+int g_gemv_stream_tm = 0;   // streaming GEMV: the tile-major copy where there is one (0), the row-tile layout (-1)
 constexpr int kStreamWavesPerCU = 8;
 
 template <int FMT, int UD, bool ACC, int NS, int TT>
-int launch_stream_t(const QArgs &a, int rows_pad, hipStream_t st)
+int launch_stream_t(const QArgs &a, int rows_pad, const uint8_t *wt, hipStream_t st)
 {
     const int ldl = NS * Geo<FMT, UD>::SC + 16, ntiles = rows_pad / 16;
     const int wpc = g_gemv_stream > 0 ? g_gemv_stream : kStreamWavesPerCU;
     const int waves = std::min(ntiles, device_cus() * wpc);
     const int grid = eif_ceil_div(waves, kStreamThreads / 64);
-    qstream_kernel<FMT, UD, ACC, NS, TT><<<grid, kStreamThreads, (size_t)a.M * ldl, st>>>(a.xq, a.W, a.scales, a.wld, a.ldq,
-                                                                                        a.M, a.N, ntiles, a);
+    if (wt)   // the tile-major copy
+        qstream_kernel<FMT, UD, ACC, NS, TT, true><<<grid, kStreamThreads, (size_t)a.M * ldl, st>>>(
+            a.xq, wt, a.scales, a.wld, a.ldq, a.M, a.N, ntiles, a);
+    else
+        qstream_kernel<FMT, UD, ACC, NS, TT, false><<<grid, kStreamThreads, (size_t)a.M * ldl, st>>>(
+            a.xq, a.W, a.scales, a.wld, a.ldq, a.M, a.N, ntiles, a);
     EIF_HIP_LAUNCHED();
     return EIF_HIP_OK;
 }
 
-// The streaming GEMV takes row-scaled INT4 / INT8 matrices of kBigTiles 16-row tiles or more (vocabulary heads)
-// with prepped activations, 4 to 32 token rows (1 to 3 as well when its launch size is set) and 8 or 16 steps
-// along K. Returns 1 for other shapes.
 template <int FMT, int UD, bool GROUPED, bool ACC>
-int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
+int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, const uint8_t *wt, hipStream_t st)
 {
     if constexpr (FMT == kTern || GROUPED) {
         return 1;
     } else {
         if (g_gemv_stream < 0 || p.x || p.sh_ml || a.amax_key || a.M > 32 || rows_pad / 16 < kBigTiles) return 1;
         if (a.M < 4 && g_gemv_stream == 0) return 1;   // up to 3 token rows: the tiled GEMV measured as fast or faster
+        if (g_gemv_stream_tm < 0) wt = nullptr;
         if (a.M <= 16) {
-            if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 1>(a, rows_pad, st);
-            if (a.nsteps == 16) return launch_stream_t<FMT, UD, ACC, 16, 1>(a, rows_pad, st);
+            if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 1>(a, rows_pad, wt, st);
+            if (a.nsteps == 16) return launch_stream_t<FMT, UD, ACC, 16, 1>(a, rows_pad, wt, st);
         } else {
-            if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 2>(a, rows_pad, st);
+            if (a.nsteps == 8) return launch_stream_t<FMT, UD, ACC, 8, 2>(a, rows_pad, wt, st);
         }
         return 1;
     }
@@ -1966,11 +2001,11 @@ int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t 
 // most kFusedMaxM rows; else workgroups of mw token rows (token tiles, then chunks), mw from kGemvDefaultWgM
 // (or the knob) halved until the staged rows and sums fit.
 template <int FMT, int UD, bool GROUPED, bool ACC>
-int launch_gemv(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
+int launch_gemv(const QArgs &a, const PrepArgs &p, int rows_pad, const uint8_t *wt, hipStream_t st)
 {
     const int rp = launch_rowpair<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
     if (rp != 1) return rp;
-    const int rs = launch_stream<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
+    const int rs = launch_stream<FMT, UD, GROUPED, ACC>(a, p, rows_pad, wt, st);
     if (rs != 1) return rs;
     if (p.x || p.sh_ml || a.M <= kFusedMaxM) {
         if (a.M > (p.x ? kFusedMaxM : kGemvTileM)) return 1;
@@ -1988,10 +2023,10 @@ int launch_gemv(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
 }
 
 template <int FMT, int UD, bool GROUPED, bool ACC>
-int launch_shape(const QArgs &a, const PrepArgs &p, int rows_pad, int path, hipStream_t st)
+int launch_shape(const QArgs &a, const PrepArgs &p, int rows_pad, int path, hipStream_t st, const uint8_t *wt = nullptr)
 {
     if (p.x || (path == EIF_HIP_PATH_GEMV && a.M <= kGemvMaxM)) {
-        const int rc = launch_gemv<FMT, UD, GROUPED, ACC>(a, p, rows_pad, st);
+        const int rc = launch_gemv<FMT, UD, GROUPED, ACC>(a, p, rows_pad, wt, st);
         if (rc != 1) return rc;
     }
     return launch_gemm<FMT, UD, GROUPED, ACC>(a, rows_pad, st);
@@ -2001,8 +2036,8 @@ template <bool ACC>
 int dispatch(const eif_hip_qweight *w, const QArgs &a, const PrepArgs &p, int path, hipStream_t st)
 {
     const bool grouped = w->fmt == kTern && w->group > 0;
-    if (w->fmt == kI8) return launch_shape<kI8, 0, false, ACC>(a, p, w->rows_pad, path, st);
-    if (w->fmt == kI4) return launch_shape<kI4, 0, false, ACC>(a, p, w->rows_pad, path, st);
+    if (w->fmt == kI8) return launch_shape<kI8, 0, false, ACC>(a, p, w->rows_pad, path, st, w->tm);
+    if (w->fmt == kI4) return launch_shape<kI4, 0, false, ACC>(a, p, w->rows_pad, path, st, w->tm);
     if (!grouped) return launch_shape<kTern, 4, false, ACC>(a, p, w->rows_pad, path, st);
     switch (w->ud) {
     case 1: return launch_shape<kTern, 1, true, ACC>(a, p, w->rows_pad, path, st);
@@ -2093,9 +2128,9 @@ int make_prep_spec(const eif_hip_qweight *w, const eif_hip_prep_spec *sp, int M,
 int gemv_rowscaled(const eif_hip_qweight *w, const QArgs &a, hipStream_t st)
 {
     const PrepArgs p{};
-    if (w->fmt == kI8) return launch_gemv<kI8, 0, false, false>(a, p, w->rows_pad, st);
-    if (w->fmt == kI4) return launch_gemv<kI4, 0, false, false>(a, p, w->rows_pad, st);
-    if (w->group == 0) return launch_gemv<kTern, 4, false, false>(a, p, w->rows_pad, st);
+    if (w->fmt == kI8) return launch_gemv<kI8, 0, false, false>(a, p, w->rows_pad, w->tm, st);
+    if (w->fmt == kI4) return launch_gemv<kI4, 0, false, false>(a, p, w->rows_pad, w->tm, st);
+    if (w->group == 0) return launch_gemv<kTern, 4, false, false>(a, p, w->rows_pad, nullptr, st);
     return EIF_HIP_E_ARG;
 }
 
@@ -2453,8 +2488,14 @@ int eif_hip_set_gemv_row_tiles(int rt)
 
 int eif_hip_set_gemv_stream(int wpc)
 {
-    const int old = g_gemv_stream;
-    if (wpc >= -1 && wpc <= 32) g_gemv_stream = wpc;
+    const int old = g_gemv_stream_tm < 0 && g_gemv_stream >= 0 ? -2 - g_gemv_stream : g_gemv_stream;
+    if (wpc >= -1 && wpc <= 32) {
+        g_gemv_stream = wpc;
+        g_gemv_stream_tm = 0;
+    } else if (wpc <= -2 && wpc >= -34) {   // -2 - wpc: the same launch on the row-tile layout
+        g_gemv_stream = -2 - wpc;
+        g_gemv_stream_tm = -1;
+    }
     return old;
 }
 
@@ -2536,19 +2577,35 @@ int eif_hip_qweight_create(eif_hip_qweight **out, int fmt, int rows, int cols, i
             repack_int8_kernel<<<(unsigned)((n + threads - 1) / threads), threads, 0, st>>>(
                 (const int8_t *)src, rows, cols, (int8_t *)q.w, q.rows_pad, q.kpad);
         }
-        if (hipGetLastError() != hipSuccess || hipStreamSynchronize(st) != hipSuccess) rc = EIF_HIP_E_DEVICE;
+        if (hipGetLastError() != hipSuccess) rc = EIF_HIP_E_DEVICE;
     }
+    // the streaming GEMV's tile-major copy (same bytes, another order)
+    size_t tmbytes = 0;
+    if (rc == EIF_HIP_OK && fmt != kTern && q.rows_pad / 16 >= kBigTiles && (q.nsteps == 8 || q.nsteps == 16)) {
+        tmbytes = wbytes;
+        if (hipMalloc(&q.tm, tmbytes) != hipSuccess) {
+            rc = EIF_HIP_E_NOMEM;
+        } else {
+            const size_t n = tmbytes / 16;
+            tile_major_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>((const uint4 *)q.w, q.wld, q.nsteps,
+                                                                          fmt == kI4 ? 16 : 32, (uint4 *)q.tm, n);
+            if (hipGetLastError() != hipSuccess) rc = EIF_HIP_E_DEVICE;
+        }
+    }
+    if (rc == EIF_HIP_OK && hipStreamSynchronize(st) != hipSuccess) rc = EIF_HIP_E_DEVICE;
     if (src_dev) (void)hipFree(src_dev);
     if (rc != EIF_HIP_OK) {
         if (q.w) (void)hipFree(q.w);
         if (q.scales) (void)hipFree(q.scales);
+        if (q.tm) (void)hipFree(q.tm);
         return rc;
     }
-    q.bytes = wbytes + (scales ? sizeof(float) * sc_count : 0);
+    q.bytes = wbytes + tmbytes + (scales ? sizeof(float) * sc_count : 0);
     eif_hip_qweight *h = new (std::nothrow) eif_hip_qweight(q);
     if (!h) {
         (void)hipFree(q.w);
         if (q.scales) (void)hipFree(q.scales);
+        if (q.tm) (void)hipFree(q.tm);
         return EIF_HIP_E_NOMEM;
     }
     *out = h;
@@ -2560,6 +2617,7 @@ void eif_hip_qweight_destroy(eif_hip_qweight *w)
     if (!w) return;
     if (w->w) (void)hipFree(w->w);
     if (w->scales) (void)hipFree(w->scales);
+    if (w->tm) (void)hipFree(w->tm);
     delete w;
 }
 

@@ -232,8 +232,10 @@ int eif_hip_set_gemv_token_chunk(int m);
 
 /* The streaming GEMV of vocabulary-sized row-scaled INT4 / INT8 matrices (65,536 rows or more, prepped
  * activations, 4 to 32 token rows, 8 or 16 steps of K): waves per CU of its launch (1..32, which also takes 1
- * to 3 token rows; 0 = the default, 8; -1 = off, such matrices then take the GEMV above). Returns the previous
- * setting. A tuning knob: results do not depend on it.                                                  */
+ * to 3 token rows; 0 = the default, 8; -1 = off, such matrices then take the GEMV above). Such matrices keep a
+ * tile-major copy of their codes, which the stream reads (a load instruction covers 1 KB of whole lines);
+ * -2 - wpc (-2 .. -34) asks for the same launch on the row-tile layout instead. Returns the previous setting.
+ * A tuning knob: results do not depend on it.                                                             */
 int eif_hip_set_gemv_stream(int wpc);
 
 /* The row-pair GEMV of row-scaled INT4 / INT8 matrices at one token row, rows of whole 512-byte runs (INT4 K a

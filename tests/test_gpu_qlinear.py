@@ -541,7 +541,8 @@ def test_gguf_ternary_weight(gpu, oracle, kind):
 def test_stream_gemv(gpu, oracle, fmt, N, K):
     """The streaming GEMV of vocabulary-sized row-scaled matrices (65,536 rows or more, 8 or 16 steps along K)
     at M = 1, 5, 16, 17 and 32, with and without a bias: y and the integer sums bit for bit against the oracle,
-    and the same bits with the stream off (the tiled GEMV) and at other launch sizes."""
+    and the same bits with the stream off (the tiled GEMV), at other launch sizes and on the row-tile layout
+    instead of the tile-major copy."""
     lib = gpu.load()
     if fmt == "int8":
         w, s = synth.int8_weight((67, N, K), N, K)
@@ -559,7 +560,7 @@ def test_stream_gemv(gpu, oracle, fmt, N, K):
             bias = synth.rng(70, M).standard_normal(N).astype(np.float32) if M % 2 else None
             oy = np.zeros((M, N), np.float32)
             fn(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
-            for wpc in (0, 3, -1):
+            for wpc in (0, 3, -2, -1):   # -2: the row-tile layout instead of the tile-major copy
                 lib.eif_hip_set_gemv_stream(wpc)
                 y = run_linear(gpu, qw, xq_d, xs_d, M, GEMV, bias)
                 assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), (M, wpc)
