@@ -153,6 +153,8 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
     ("tern", 70, 640, 64, 33),
     ("int8", 896, 4864, 0, 70),
     ("int4", 512, 1024, 0, 48),
+    ("int8", 300, 128, 0, 20),       # one step of K
+    ("tern", 70, 64, 32, 18),        # g32, one step
 ])
 def test_gemm_forms(gpu, oracle, fmt, N, K, g, M):
     """The GEMM's tiled form with each prefetch ring (2, 4, 8 steps of loads in flight) and its panel form
