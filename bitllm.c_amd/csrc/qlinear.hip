@@ -1851,6 +1851,11 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     // fewer waves measured faster there (gate+up 13824x2560 at one token 6.70 us with 12 waves, 6.96 with 16)
     int ks = g_gemv_ksplit > 0 ? g_gemv_ksplit
                                : (p.x && rt == 4 ? eif_ceil_div(a.nsteps, 4) : pick_ks_gemv(rows_pad / 16, a.nsteps));
+    // row-scaled INT8 / INT4 at one token row, under 24 steps: 4 (INT8) or 8 (INT4) steps per wave, the waves'
+    // combine costing more than the steps it takes off (INT8 9728x896 4.07 us against 4.29 with 2 steps a wave,
+    // 896x896 2.53 against 2.72; INT4 7168x1024 3.10 against 3.25)
+    if (FMT != kTern && !p.x && a.M == 1 && a.nsteps < 24 && g_gemv_ksplit <= 0)
+        ks = eif_ceil_div(a.nsteps, FMT == kI8 ? 4 : 8);
     if (!GROUPED && !p.x && rows_pad / 16 >= kBigTiles && g_gemv_ksplit <= 0) {
         // row-scaled, many tiles, prepped activations: about 10 KiB of weights per wave
         const int row_bytes = a.nsteps * 4 * Geo<FMT, UD>::SB;
