@@ -1856,6 +1856,11 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     // 896x896 2.53 against 2.72; INT4 7168x1024 3.10 against 3.25)
     if (FMT != kTern && !p.x && a.M == 1 && a.nsteps < 24 && g_gemv_ksplit <= 0)
         ks = eif_ceil_div(a.nsteps, FMT == kI8 ? 4 : 8);
+    // grouped ternary on prepped activations: 10 waves for 24 steps or more (down 2560x6912 g96 at one row 5.4 us
+    // against 5.6 with 9, at 8 rows 7.1 against 7.4); with 8 or more token rows a step per wave under 24 steps
+    // (each step combines 8-16 rows' groups; at 8 rows QKV 3840x2560 4.1 us against 4.5 with 2 steps a wave,
+    // O 3.9 against 4.2)
+    if (GROUPED && !p.x && g_gemv_ksplit <= 0 && (a.nsteps >= 24 || a.M >= 8)) ks = a.nsteps < 24 ? a.nsteps : 10;
     if (!GROUPED && !p.x && rows_pad / 16 >= kBigTiles && g_gemv_ksplit <= 0) {
         // row-scaled, many tiles, prepped activations: about 10 KiB of weights per wave
         const int row_bytes = a.nsteps * 4 * Geo<FMT, UD>::SB;
@@ -1914,8 +1919,9 @@ int launch_gemv_m(const QArgs &a, PrepArgs p, int rows_pad, hipStream_t st)
             const int tiles = rows_pad / 16;
             const bool chunked = a.M > kFusedMaxM && !p.x;
             // more than kFusedMaxM tokens: four tiles once the workgroups (row tiles x token chunks) reach 768
+            // one token row of prepped activations: one tile (ternary 13824x2560 5.0 us against 6.3 with four)
             const bool four = chunked ? tiles * eif_ceil_div(a.M, gemv_wg_m(a)) >= 768
-                                      : tiles >= 768 && (GROUPED || p.x || tiles < kBigTiles);
+                                      : tiles >= 768 && (GROUPED || p.x || tiles < kBigTiles) && (p.x || a.M > 1);
             rt = g_gemv_rt > 0 ? g_gemv_rt : (four ? 4 : 1);
         }
     if (rt > 1) {
