@@ -2164,15 +2164,18 @@ bool gemv_fits_tile(const eif_hip_qweight *w)
 
 // Auto path (measured on MI355X, weights rotated past the Infinity Cache; us, GEMV / GEMM):
 // * up to kFusedMaxM tokens: the GEMV;
-// * 9 .. 16 tokens: the GEMV where a 16-row token tile fits one workgroup (every BitNet, INT8 and INT4 layer
-//   shape: ternary 3840x2560 5.5 / 6.2, 6912x2560 7.0 / 7.5, g96 2560x6912 9.0 / 8.6, INT8 896x4864 7.0 / 7.8);
-// * 17 .. 63 tokens, row-scaled matrices (INT8, INT4): the GEMV up to 32 tokens, and above that for matrices of
-//   fewer than 32 tiles of 64 rows (INT8 896x4864 at 48 / 63 tokens 7.8 / 7.6 against 8.2 / 9.4; INT4 1024x3584
-//   6.1 / 6.0 against 6.3 / 6.7; INT4 3584x1024 at 48 tokens 6.3 against 4.7);
-// * 17 .. 63 tokens, group-scaled ternary: the GEMM. The GEMV streams the weights once per 16- or 32-row token
-//   chunk and stages every chunk's int8 rows and group sums in LDS, and at these batches it lost on every layer
-//   shape (32 tokens: 3840x2560 7.5 / 6.3, 6912x2560 8.0 / 7.6, g96 2560x6912 17.3 / 9.6; 48 tokens:
-//   10.6 / 6.4, 13.5 / 8.4, 17.6 / 10.7), so the dense contraction takes them below the 64-token line.
+// * group-scaled ternary, 9 .. 16 tokens: the GEMV for matrices of under 256 tiles of 16 rows and under 24 steps
+//   of K, where a 16-row token tile fits one workgroup (GEMV / GEMM at 16 tokens, µs: 3840x2560 4.9 / 5.6,
+//   2560x2560 4.7 / 5.5); the GEMM for the others (6912x2560 6.8 / 6.4, g96 2560x6912 9.1 / 8.2);
+// * group-scaled ternary, 17 .. 63 tokens: the GEMM. The GEMV streams the weights once per 16- or 32-row token
+//   chunk and stages every chunk's int8 rows and group sums in LDS, and at these batches it loses on every layer
+//   shape (32 tokens: 3840x2560 7.3 / 5.7, 6912x2560 8.0 / 6.4, g96 2560x6912 17.2 / 9.0; 48 tokens:
+//   9.7 / 5.7, 13.7 / 7.5, 17.6 / 8.7), so the dense contraction takes them below the 64-token line;
+// * row-scaled matrices (INT8, INT4), 9 .. 63 tokens: the GEMV up to 16 tokens (INT8 4864x896 4.3 / 5.0, INT4
+//   3584x1024 3.6 / 4.3), up to 32 for vocabulary-sized matrices (the streaming GEMV: INT4 151936x1024 at 32
+//   tokens 19.2 / 27.1), and at any batch for matrices of fewer than 32 tiles of 64 rows (INT8 896x4864 at 48 /
+//   63 tokens 7.6 / 7.6 against 8.1 / 9.3); the GEMM otherwise (INT8 4864x896 at 32 tokens 5.1 against 5.7,
+//   INT4 3584x1024 4.3 against 4.6).
 constexpr int kGemvFewRows = 32 * 64;
 
 int resolve_path(const eif_hip_qweight *w, int path, int M)
@@ -2181,9 +2184,12 @@ int resolve_path(const eif_hip_qweight *w, int path, int M)
     if (M >= g_gemm_min_tokens) return EIF_HIP_PATH_GEMM;
     if (M <= kFusedMaxM) return EIF_HIP_PATH_GEMV;
     if (!gemv_fits_tile(w)) return EIF_HIP_PATH_GEMM;
-    if (M <= kGemvTileM) return EIF_HIP_PATH_GEMV;
     const bool grouped = w->fmt == kTern && w->group > 0;
-    return !grouped && (M <= 2 * kGemvTileM || w->rows_pad < kGemvFewRows) ? EIF_HIP_PATH_GEMV : EIF_HIP_PATH_GEMM;
+    const int tiles = w->rows_pad / 16;
+    if (grouped) return M <= kGemvTileM && tiles < 256 && w->nsteps < 24 ? EIF_HIP_PATH_GEMV : EIF_HIP_PATH_GEMM;
+    return M <= kGemvTileM || w->rows_pad < kGemvFewRows || (M <= 2 * kGemvTileM && tiles >= kBigTiles)
+               ? EIF_HIP_PATH_GEMV
+               : EIF_HIP_PATH_GEMM;
 }
 
 QArgs make_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)
