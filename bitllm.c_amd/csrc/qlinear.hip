@@ -1470,18 +1470,24 @@ int g_gemm_tt = 0;   // token tiles of a GEMM workgroup (1, 2, 4), 0 = chosen fr
 
 // Token tiles of the GEMM (16 x TT tokens per workgroup) for M tokens on rt64 tiles of 64 rows and nsteps steps
 // of K. The largest tile that holds the batch (64 tokens above 32), made smaller while the workgroups do not
-// fill the CUs once (a 64-token tile: twice, when the K loop is short), since a workgroup's time is a chain of
-// dependent steps and more, shorter chains finish sooner; each extra token tile re-reads the weight tile, mostly
-// from L2. Measured: INT8 896x896 at 128 tokens 7.7 us with 64-token tiles, 5.4 with 16; ternary 13824x2560 at 64
+// fill the CUs once, since a workgroup's time is a chain of dependent steps and more, shorter chains finish
+// sooner; each extra token tile re-reads the weight tile, mostly from L2, so a long K loop stops at four token
+// tiles. Measured: INT8 896x896 at 128 tokens 7.7 us with 64-token tiles, 5.4 with 16; ternary 13824x2560 at 64
 // tokens 13.7 / 10.5 (32-token tiles) / 13.9 (16); ternary 2560x2560 at 512 tokens 16.0 / 12.2 (32).
-int gemm_tt(int M, int rt64, int nsteps)
+int gemm_tt(int M, int rt64, int nsteps, bool grouped)
 {
     if (g_gemm_tt > 0) return g_gemm_tt;
     int tt = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
     const int C = device_cus();
     auto wgs = [&](int t) { return rt64 * eif_ceil_div(M, 16 * t); };
-    if (tt == 4 && nsteps < 24 && wgs(4) < 2 * C) tt = 2;
-    while (tt > 1 && wgs(tt) < C) tt /= 2;
+    // a short K loop takes 32-token tiles below 1.5 workgroups per CU at 64 (ternary 2560x2560 at 512 tokens, 320
+    // workgroups: 12.1 us with 32-token tiles, 13.9 with 64; 3840x2560, 480: 15.5 against 14.8; 13824x2560 at 128
+    // tokens, 432: 16.6 against 14.9)
+    if (tt == 4 && nsteps < 24 && 2 * wgs(4) < 3 * C) tt = 2;
+    // grouped ternary with a long K loop keeps the weight tile's re-reads to four token tiles (g96 2560x6912 at
+    // 128 tokens: 12.0 us with 32-token tiles, 18.7 with 16 and two splits)
+    const int min_tt = grouped && nsteps >= 24 ? std::max(1, std::min(4, M / 64)) : 1;
+    while (tt > min_tt && wgs(tt) < C) tt /= 2;
     return tt;
 }
 
@@ -1610,7 +1616,7 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_gemm(const QArgs &a, int rows_pad, hipStream_t st)
 {
-    switch (gemm_tt(a.M, rows_pad / 64, a.nsteps)) {
+    switch (gemm_tt(a.M, rows_pad / 64, a.nsteps, GROUPED)) {
     case 1: return launch_gemm_t<FMT, UD, GROUPED, ACC, 1>(a, rows_pad, st);
     case 2: return launch_gemm_t<FMT, UD, GROUPED, ACC, 2>(a, rows_pad, st);
     default: return launch_gemm_t<FMT, UD, GROUPED, ACC, 4>(a, rows_pad, st);
