@@ -1433,20 +1433,22 @@ int g_gemm_split = 0;   // splits along K of the GEMM, 0 = chosen from the shape
 
 // Splits along K (at most 16, at least three steps per split). Fewer tiles than CUs: none for a short K loop
 // (under 24 steps, where a split's coherent round trip costs more than the steps it takes off), else about two
-// workgroups per CU, floor(2 CUs / tiles), keeping six steps or more per split. One round or more: 2 when a long
-// K (24 steps or more) leaves the last round under 70% full (e.g. 320 tiles on 256 CUs). 1 for the parity
-// outputs and when no workspace can be had (first use of a stream inside a graph capture). Measured per shape
-// (INT8 896x4864 at 128 tokens: 15.4 us unsplit, 10.2 at 4 splits, 12.9 at 16; ternary 2560x2560 at 64 tokens:
-// 6.0 unsplit, 6.4 at 3).
-int choose_split(int nsteps, int tiles)
+// workgroups per CU for grouped ternary, floor(2 CUs / tiles), and one for the row-scaled formats, floor(CUs /
+// tiles), keeping six steps or more per split. One round or more: 3 (grouped) or 2 when a long K (24 steps or
+// more) leaves the last round under 70% full (e.g. 320 tiles on 256 CUs). 1 for the parity outputs and when no
+// workspace can be had (first use of a stream inside a graph capture). Measured per shape (µs): g96 2560x6912 at
+// 64 and 128 tokens 9.1 and 12.0 at 3 splits, 11.1 and 19.9 unsplit, at 512 tokens 31.6 at 3, 33.6 at 2; INT8
+// 896x4864 at 64, 128 and 256 tokens 8.0 at 4, 9.6 at 2, 12.7 unsplit, against 9.1, 10.2 and 14.3 at 6, 4, 2;
+// INT4 1024x3584 at 128 tokens 6.7 at 2, 7.1 at 4.
+int choose_split(int nsteps, int tiles, bool grouped)
 {
     int ks = g_gemm_split;
     if (ks == 0) {
         const int C = device_cus();
         if (tiles < C)
-            ks = nsteps < 24 ? 1 : std::max(1, std::min(2 * C / std::max(1, tiles), nsteps / 6));
+            ks = nsteps < 24 ? 1 : std::max(1, std::min((grouped ? 2 : 1) * C / std::max(1, tiles), nsteps / 6));
         else
-            ks = nsteps >= 24 && (double)tiles < 0.7 * eif_ceil_div(tiles, C) * C ? 2 : 1;
+            ks = nsteps >= 24 && (double)tiles < 0.7 * eif_ceil_div(tiles, C) * C ? (grouped ? 3 : 2) : 1;
     }
     return std::min(ks, std::min(16, std::max(1, nsteps / 3)));
 }
@@ -1503,10 +1505,10 @@ thread_local FixedWs tl_fixed_ws;
 // Splits along K for `tiles` output tiles of nv values per thread, with the partials' space (ks x tiles x 256
 // threads x nv floats) and the tiles' counters; 1 when the launch is not split.
 template <bool ACC>
-int pick_split(QArgs &a, int tiles, int nv, hipStream_t st)
+int pick_split(QArgs &a, int tiles, int nv, bool grouped, hipStream_t st)
 {
     if (ACC) return 1;
-    const int ks = choose_split(a.nsteps, tiles);
+    const int ks = choose_split(a.nsteps, tiles, grouped);
     if (ks <= 1 || tiles > kMaxSplitTiles) return 1;
     const size_t bytes = (size_t)ks * tiles * kGemmThreads * nv * sizeof(float);
     if (tl_fixed_ws.ptr) {   // a fixed workspace too small for this split: -1, nothing is launched
@@ -1571,7 +1573,7 @@ int launch_gemm_t(QArgs a, int rows_pad, hipStream_t st)
     if ((size_t)a.M * a.ldq >= ((size_t)1 << 32) || (size_t)rows_pad * a.wld >= ((size_t)1 << 32)) return EIF_HIP_E_LIMIT;
     const int tm = eif_ceil_div(a.M, 16 * TT), tiles = rows_pad / 64 * tm;
     static_assert(TT == 1 || TT == 2 || TT == 4, "token tiles of gemm_tt");
-    const int ks = pick_split<ACC>(a, tiles, 4 * TT, st);
+    const int ks = pick_split<ACC>(a, tiles, 4 * TT, GROUPED, st);
     if (ks == -2) return EIF_HIP_E_DEVICE;
     if (ks < 0) return EIF_HIP_E_LIMIT;
     dim3 grid(rows_pad / 64, tm, ks);
