@@ -81,8 +81,8 @@ void eif_hip_qweight_destroy(eif_hip_qweight *w);
 int eif_hip_qweight_info(const eif_hip_qweight *w, int *rows, int *cols, int *kpad, int *group, size_t *bytes);
 
 /* y[m, r] for m < M, r < rows (row stride ldy), activations xq [M, ldq] (ldq >= kpad, multiple of 16) with
- * per-row scales xs [M]; bias [rows] or NULL. Auto path: GEMV for M < eif_hip_gemm_min_tokens(), else the
- * int8-MFMA GEMM.                                                                                      */
+ * per-row scales xs [M]; bias [rows] or NULL. Auto path: the GEMV or the int8-MFMA GEMM by token count and
+ * shape (see eif_hip_set_gemm_min_tokens); the GEMM from eif_hip_gemm_min_tokens() tokens on.            */
 int eif_hip_qlinear(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, const float *bias,
                     float *y, int ldy, int M, void *stream);
 int eif_hip_qlinear_ex(const eif_hip_qweight *w, const int8_t *xq, int ldq, const float *xs, const float *bias,
@@ -209,10 +209,11 @@ int eif_hip_set_host_error_mode(int mode);
  * msg (may be NULL) receives its description, at most len bytes with the terminating NUL.              */
 int eif_hip_host_last_error(char *msg, size_t len);
 
-/* Token count from which the auto path uses the MFMA GEMM (default 64); returns the previous value. Below it
- * the auto path takes the streaming GEMV for up to 8 tokens, and for more where one workgroup stages 16
- * token rows of the weight's columns and the batch is at most 32 tokens or the weights at most 4 MiB
- * (the GEMM otherwise: it reads the weights once per 64 tokens).                                       */
+/* Token count from which the auto path always uses the MFMA GEMM (default 64); returns the previous value.
+ * Below it the auto path takes the GEMV for up to 8 tokens and, from 9 tokens on, where one workgroup stages
+ * 16 token rows of the weight's columns and the shape favours it: group-scaled ternary of fewer than 256
+ * 16-row tiles and 24 steps of K up to 16 tokens; row-scaled INT8 / INT4 up to 16 tokens, vocabulary-sized
+ * ones (the streaming GEMV) up to 32, and matrices of fewer than 2048 rows at any batch. The GEMM otherwise. */
 int eif_hip_set_gemm_min_tokens(int m);
 int eif_hip_gemm_min_tokens(void);
 
