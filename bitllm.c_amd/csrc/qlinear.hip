@@ -1981,8 +1981,13 @@ int launch_stream(const QArgs &a, const PrepArgs &p, int rows_pad, const uint8_t
 }
 
 // The row-pair GEMV: row-scaled INT4 / INT8 matrices at one prepped token row whose rows are whole 512-byte runs
-// (at most rowpair_max_p of them); by default only vocabulary-sized ones (kBigTiles tiles or more), where
-// bandwidth decides. Returns 1 for other shapes.
+// (at most rowpair_max_p of them); by default those of 1024 tiles (16,384 rows) or 20 MB of codes or more, where
+// bandwidth decides. Returns 1 for other shapes. Measured at one token row (µs, tiled GEMV / row-pair, weights
+// rotated past the Infinity Cache): INT8 9728x2560 6.86 / 6.61, 13824x2048 7.01 / 6.42, 27648x2560 14.1 / 12.2;
+// INT4 16384x2048 5.51 / 4.99, 32768x2048 8.37 / 7.33, 32768x1024 4.96 / 4.74; below, the tiled GEMV: INT8
+// 6912x2560 5.53 / 6.32, 4096x2560 4.34 / 6.01; INT4 8192x4096 5.59 / 5.98, 7168x1024 2.87 / 3.19.
+constexpr int kRowPairTiles = 1024;
+constexpr size_t kRowPairBytes = 20000000;
 
 template <int FMT, int UD, bool GROUPED, bool ACC>
 int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t st)
@@ -1992,7 +1997,7 @@ int launch_rowpair(const QArgs &a, const PrepArgs &p, int rows_pad, hipStream_t 
     } else {
         if (g_gemv_rowpair < 0 || p.x || p.sh_ml || a.M != 1 || a.wld % 512 != 0) return 1;
         const int ntiles = rows_pad / 16;
-        if (g_gemv_rowpair == 0 && ntiles < kBigTiles) return 1;
+        if (g_gemv_rowpair == 0 && ntiles < kRowPairTiles && (size_t)rows_pad * a.wld < kRowPairBytes) return 1;
         const int grid = eif_ceil_div(ntiles, kRowPairThreads / 64);
         constexpr int PM = rowpair_max_p<FMT>();
         static_assert(PM <= 5, "one case per pass count");

@@ -241,8 +241,8 @@ int eif_hip_set_gemv_stream(int wpc);
 
 /* The row-pair GEMV of row-scaled INT4 / INT8 matrices at one token row, rows of whole 512-byte runs (INT4 K a
  * multiple of 1024 up to 4096, INT8 of 512 up to 2560): each half-wave reads 512 contiguous bytes of a row and
- * the products are v_dot4_i32_i8 on the resident layout. 0 = used for 65,536 rows or more (the default), 1 = for
- * every such shape, -1 = off. Returns the previous setting. A tuning knob: results do not depend on it.     */
+ * the products are v_dot4_i32_i8 on the resident layout. 0 = used for 16,384 rows or 20 MB of codes or more (the
+ * default), 1 = for every such shape, -1 = off. Returns the previous setting. A tuning knob: results do not depend on it.     */
 int eif_hip_set_gemv_rowpair(int mode);
 
 /* Row tiles (of 4 rows) a wave takes at a time in the FP32-activation GEMVs of the host-pointer ABI (1 or 2;

@@ -579,11 +579,13 @@ def test_stream_gemv(gpu, oracle, fmt, N, K):
 
 
 @pytest.mark.parametrize("fmt,N,K,mode", [("int4", 151936, 1024, 0), ("int8", 128256, 2560, 0),
-                                          ("int8", 65600, 512, 0), ("int4", 1000, 2048, 1), ("int4", 77, 4096, 1),
+                                          ("int8", 65600, 512, 0), ("int4", 16390, 2048, 0), ("int8", 9730, 2560, 0),
+                                          ("int4", 1000, 2048, 1), ("int4", 77, 4096, 1),
                                           ("int8", 130, 1536, 1), ("int8", 64, 2048, 1)])
 def test_rowpair_gemv(gpu, oracle, fmt, N, K, mode):
     """The row-pair GEMV (one token row; rows of whole 512-byte runs read half a wave at a time, v_dot4 products
-    on the resident layout) on vocabulary-sized matrices (its default) and, forced on, on small and ragged ones:
+    on the resident layout) on its default shapes (16,384 rows or 20 MB of codes and more: vocabulary heads, ragged
+    mid-size matrices on either side of the rule) and, forced on, on small and ragged ones:
     y with and without a bias and the int32 sums bit for bit against the oracle, and the same bits with it off
     (the tiled GEMV)."""
     lib = gpu.load()
