@@ -1548,7 +1548,9 @@ size_t gemm_max_lds()
 // panel form with ring -pf). Measured per linear (µs, a launch in a graph of launches, weights rotated past the
 // Infinity Cache):
 // - row-scaled INT8 / INT4, an unsplit launch of one to four workgroups per CU that all fit at once: panel,
-//   ring 8 (INT8 9728x896 at 128 tokens 10.4 against 11.8 tiled);
+//   ring 8, when the split's steps all fit the first ring (INT8 9728x896, 7 steps, at 128 tokens 10.2 against 11.6
+//   tiled with ring 4); with more steps the tiled form with ring 2 (INT8 at 128 tokens: 9728x1024, 8 steps, 13.8
+//   against 17.7 as a panel; 9728x1152 14.1 against 18.4; 4864x1024 at 64 tokens 7.6 against 11.7);
 // - more than two workgroups per CU otherwise: tiled, ring 2 (four waves per SIMD hide each other's latency);
 // - grouped ternary, every panel workgroup resident at once, and split along K, or a K loop of 20 steps or
 //   more, or more workgroups than CUs: panel, ring 4 (down 2560x6912 g96 at 64 tokens, three splits: 8.5
@@ -1560,7 +1562,7 @@ int gemm_form(bool grouped, int wgs, int ks, int ns, int wpc)
 {
     const int C = device_cus();
     const bool resident = wgs <= C * wpc;
-    if (!grouped && ks == 1 && wgs > C && wgs <= 4 * C && resident) return -8;
+    if (!grouped && ks == 1 && wgs > C && wgs <= 4 * C && resident && ns < 8) return -8;
     if (wgs > 2 * C) return 2;
     if (grouped && resident && (ks > 1 || ns >= 20 || wgs > C)) return -4;
     return wgs <= C ? 4 : 2;
@@ -2187,9 +2189,15 @@ bool gemv_fits_tile(const eif_hip_qweight *w)
 // * row-scaled matrices (INT8, INT4), 9 .. 63 tokens: the GEMV up to 16 tokens (INT8 4864x896 4.3 / 5.0, INT4
 //   3584x1024 3.6 / 4.3), up to 32 for vocabulary-sized matrices (the streaming GEMV: INT4 151936x1024 at 32
 //   tokens 19.2 / 27.1), and at any batch for matrices of fewer than 32 tiles of 64 rows (INT8 896x4864 at 48 /
-//   63 tokens 7.6 / 7.6 against 8.1 / 9.3); the GEMM otherwise (INT8 4864x896 at 32 tokens 5.1 against 5.7,
-//   INT4 3584x1024 4.3 against 4.6).
+//   63 tokens 7.6 / 7.6 against 8.1 / 9.3), and up to 32 tokens for INT8 matrices of 8192 rows or 16 steps of K
+//   and more (17 / 32 tokens: 9728x896 5.5 / 6.8 against 6.8 / 7.0, 9728x1024 5.7 / 7.1 against 7.8 / 8.1,
+//   4096x2048 5.3 / 6.3 against 7.8 / 7.9, 2560x2560 5.5 / 7.2 against 8.7 / 8.8) and INT4 ones of 2048 tiles
+//   and more (32768x1024 7.0 / 7.8 against 7.1 / 7.8); the GEMM otherwise (INT8 4864x896 at 32 tokens 5.6
+//   against 5.0, INT4 3584x1024 4.3 against 4.6, 7168x1024 5.8 against 4.3, 16384x2048 9.0 against 7.6).
 constexpr int kGemvFewRows = 32 * 64;
+constexpr int kGemvI8Rows = 8192;    // INT8 rows from which the GEMV takes up to 32 tokens
+constexpr int kGemvI8Steps = 16;     // INT8 steps of K from which it does so too
+constexpr int kGemvI4Tiles = 2048;   // INT4 tiles of 16 rows from which it does so
 
 int resolve_path(const eif_hip_qweight *w, int path, int M)
 {
@@ -2200,9 +2208,11 @@ int resolve_path(const eif_hip_qweight *w, int path, int M)
     const bool grouped = w->fmt == kTern && w->group > 0;
     const int tiles = w->rows_pad / 16;
     if (grouped) return M <= kGemvTileM && tiles < 256 && w->nsteps < 24 ? EIF_HIP_PATH_GEMV : EIF_HIP_PATH_GEMM;
-    return M <= kGemvTileM || w->rows_pad < kGemvFewRows || (M <= 2 * kGemvTileM && tiles >= kBigTiles)
-               ? EIF_HIP_PATH_GEMV
-               : EIF_HIP_PATH_GEMM;
+    if (M <= kGemvTileM || w->rows_pad < kGemvFewRows) return EIF_HIP_PATH_GEMV;
+    if (M > 2 * kGemvTileM) return EIF_HIP_PATH_GEMM;
+    const bool big = tiles >= kBigTiles ||
+                     (w->fmt == kI8 ? w->rows_pad >= kGemvI8Rows || w->nsteps >= kGemvI8Steps : tiles >= kGemvI4Tiles);
+    return big ? EIF_HIP_PATH_GEMV : EIF_HIP_PATH_GEMM;
 }
 
 QArgs make_args(const eif_hip_qweight *w, const int8_t *xq, int ldq, int M)

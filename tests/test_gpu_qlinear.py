@@ -309,6 +309,7 @@ def test_ternary_rowscale_bit_exact(gpu, oracle, N, K, M, path, with_bias):
     ("int8", 4864, 896, 1, GEMV), ("int8", 896, 4864, 1, GEMV), ("int8", 128, 896, 3, GEMV),
     ("int8", 4864, 896, 128, GEMM), ("int8", 77, 100, 20, GEMM),
     ("int8", 4864, 896, 32, GEMV), ("int8", 896, 4864, 63, GEMV), ("int8", 77, 100, 20, GEMV),
+    ("int8", 9730, 1024, 24, 0), ("int8", 2600, 2560, 32, 0),   # the auto path's GEMV for large INT8 matrices
     ("int8", 896, 4864, 16, GEMV), ("int8", 896, 4864, 32, GEMV),   # 16 staged rows of 4864 columns: 8 pieces a thread
     ("int4", 3584, 1024, 1, GEMV), ("int4", 1024, 3584, 1, GEMV), ("int4", 3584, 1024, 32, GEMM),
     ("int4", 3584, 1024, 32, GEMV), ("int4", 1024, 3584, 16, GEMV),
