@@ -212,8 +212,9 @@ int eif_hip_host_last_error(char *msg, size_t len);
 /* Token count from which the auto path always uses the MFMA GEMM (default 64); returns the previous value.
  * Below it the auto path takes the GEMV for up to 8 tokens and, from 9 tokens on, where one workgroup stages
  * 16 token rows of the weight's columns and the shape favours it: group-scaled ternary of fewer than 256
- * 16-row tiles and 24 steps of K up to 16 tokens; row-scaled INT8 / INT4 up to 16 tokens, vocabulary-sized
- * ones (the streaming GEMV) up to 32, and matrices of fewer than 2048 rows at any batch. The GEMM otherwise. */
+ * 16-row tiles and 24 steps of K up to 16 tokens; row-scaled INT8 / INT4 up to 16 tokens; up to 32 tokens
+ * vocabulary-sized ones (the streaming GEMV), INT8 ones of 8192 rows or 16 steps of 128 columns and more, and
+ * INT4 ones of 32,768 rows and more; matrices of fewer than 2048 rows at any batch. The GEMM otherwise.     */
 int eif_hip_set_gemm_min_tokens(int m);
 int eif_hip_gemm_min_tokens(void);
 
