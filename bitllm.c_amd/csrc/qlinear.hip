@@ -1685,10 +1685,11 @@ size_t gemv_max_lds()
     return bytes - 256;   // the kernel's static LDS (xs_l, red_max)
 }
 
-// Launch shapes compiled for every step count and tile count: the BitNet group layouts (g96, g128), INT4 and
-// INT8. The other ternary layouts get one shape (one tile per workgroup, SMAX steps per wave, block at run time).
+// Launch shapes compiled for every step count and tile count: the BitNet group layouts (g96, g128), ternary with
+// one scale per row (the TTML / TLLM files), INT4 and INT8. The other ternary layouts get one shape (one tile per
+// workgroup, SMAX steps per wave, block at run time).
 template <int FMT, int UD, bool GROUPED>
-constexpr bool gemv_tuned() { return FMT != kTern || (GROUPED && (UD == 3 || UD == 4)); }
+constexpr bool gemv_tuned() { return FMT != kTern || UD == 4 || (GROUPED && UD == 3); }
 
 // The preloaded leading arguments of qgemv_kernel (its header comment gives their meaning per form).
 struct GemvHot {

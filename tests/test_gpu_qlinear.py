@@ -145,6 +145,56 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
         qw.close()
 
 
+@pytest.mark.parametrize("N,K", [(13824, 2560), (2560, 6912), (200, 2560), (70, 640)])
+def test_ternary_rowscale_shapes(gpu, oracle, N, K):
+    """Ternary with one scale per row through every GEMV launch shape (row tiles 1 / 4, waves per tile, token
+    tiles and chunks up to 40 rows) and the fused prep (WHT-128, E columns per thread): y bit-exact against the
+    oracle's row-scaled GEMV of the oracle's prep, int32 sums exact."""
+    import torch
+    dev = torch.device("cuda:0")
+    lib = gpu.load()
+    w, s = synth.ternary_weight((146, N, K), N, K, 0)
+    qw = gpu.QWeight(gpu.W_TERNARY, N, K, 0, w, s)
+    codes = synth.unpack_ternary(w, K).astype(np.int64)
+    bias = synth.rng(147, N).standard_normal(N).astype(np.float32)
+    norm = gpu.wht_norm(128)
+    try:
+        for M in (1, 3, 8, 20, 40):
+            x = synth.activations((148, M, K), M, K)
+            xq, xs, xq_d, xs_d = dev_inputs(gpu, oracle, x, qw.kpad)
+            oacc = (xq[:, :K].astype(np.int64) @ codes.T).astype(np.int32)
+            oy = np.zeros((M, N), np.float32)
+            oracle.orc_ternary_gemv_rowscale(P(w), P(s), P(xq), qw.kpad, P(xs), P(bias), P(oy), N, M, N, K)
+            # the fused prep's reference: the oracle's WHT-128 prep, then its row-scaled GEMV
+            rq = np.zeros((M, qw.kpad), np.int8)
+            rs = np.zeros(M, np.float32)
+            assert oracle.orc_prep_rows(P(x), K, None, M, K, 128, norm, P(rq), qw.kpad, P(rs), None, 0) == 0
+            fy = np.zeros((M, N), np.float32)
+            oracle.orc_ternary_gemv_rowscale(P(w), P(s), P(rq), qw.kpad, P(rs), None, P(fy), N, M, N, K)
+            xd = torch.from_numpy(x).to(dev)
+            for rt, ks in [(0, 0), (1, 0), (4, 0), (1, 2), (4, 2), (1, 16), (4, 4), (1, 1)]:
+                lib.eif_hip_set_gemv_row_tiles(rt)
+                lib.eif_hip_set_gemv_ksplit(ks)
+                case = (M, rt, ks)
+                y = run_linear(gpu, qw, xq_d, xs_d, M, GEMV, bias)
+                assert np.array_equal(y.view(np.uint32), oy.view(np.uint32)), case
+                acc = run_acc(gpu, qw, xq_d, M, (M, N), GEMV)
+                assert np.array_equal(acc, oacc), case
+                if M <= 8:
+                    for e in (0, 8, 16):
+                        lib.eif_hip_set_gemv_prep_cols(e)
+                        yf = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+                        qw.linear_f32(xd, yf, 128, norm)
+                        yf = yf.cpu().numpy()
+                        assert np.array_equal(yf.view(np.uint32), fy.view(np.uint32)), case + (e,)
+                    lib.eif_hip_set_gemv_prep_cols(0)
+    finally:
+        lib.eif_hip_set_gemv_row_tiles(0)
+        lib.eif_hip_set_gemv_ksplit(0)
+        lib.eif_hip_set_gemv_prep_cols(0)
+        qw.close()
+
+
 @pytest.mark.parametrize("fmt,N,K,g,M", [
     ("tern", 200, 2560, 128, 40),    # 20 steps: rounds of 8 with 4 left, of 4 with none
     ("tern", 96, 2688, 128, 17),     # 21 steps: 5, 1 and 1 left for rings of 8, 4, 2
