@@ -1895,7 +1895,17 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
         // shortest chains win: E = 16 on 3 waves measured slower than E = 4 on 10 for K = 2560 (QKV 4.8 against
         // 4.1 us), E = 16 slower than E = 8 for K = 6912 (down 7.2 against 6.6 us). The standalone prep kernel
         // and the persistent decode step take the same E, so a pre-op's sum of squares has the same order there.
-        for (int e = 4; e <= 16; e *= 2) {
+        // The one-shape group layouts at one token row with no pre-op (E does not change the prep's bits then):
+        // 8 columns a thread on the fewest waves that cover the row (K = 2560: g64 8.4 us against 10.0 with 4
+        // columns on 10 waves, g32 9.7 against 10.3, g256 7.6 against 9.4; K = 6912 takes 8 columns anyway).
+        int e0 = 4;
+        if constexpr (GROUPED && !gemv_tuned<FMT, UD, GROUPED>()) {
+            if (a.M == 1 && p.pre == EIF_HIP_PRE_NONE && !p.sh_ml && g_gemv_prep_cols <= 0 && g_gemv_ksplit <= 0) {
+                e0 = 8;
+                ks = 1;
+            }
+        }
+        for (int e = e0; e <= 16; e *= 2) {
             if (64 * e < p.block || e < g_gemv_prep_cols) continue;
             if (p.sh_ml && (e > 8 || p.sh_hd % e != 0)) continue;
             int k = ks;

@@ -104,10 +104,11 @@ def test_ternary_grouped(gpu, oracle, N, K, g, M, path):
     qw.close()
 
 
-@pytest.mark.parametrize("N,K,g", [(3072, 2560, 128), (1024, 6912, 96), (200, 2560, 128)])
+@pytest.mark.parametrize("N,K,g", [(3072, 2560, 128), (1024, 6912, 96), (200, 2560, 128),
+                                   (1000, 2560, 64), (300, 2560, 32), (500, 2560, 256), (260, 6912, 64)])
 def test_gemv_shape_knobs(gpu, oracle, N, K, g):
     """Row tiles per workgroup, waves per tile and prep columns per thread change the launch, never the result
-    (y, acc, fused y)."""
+    (y, acc, fused y); the fused y is the oracle's prep and grouped GEMV bit for bit."""
     import torch
     dev = torch.device("cuda:0")
     lib = gpu.load()
@@ -125,6 +126,12 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
             oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(xq), qw.kpad, P(xs), None, P(oy), N, M, N, K)
             oacc = np.zeros((M, N, ng), np.int32)
             oracle.orc_ternary_acc_i32(P(w), P(xq), qw.kpad, M, N, K, g, P(oacc))
+            # the fused prep's reference: the oracle's WHT-128 prep, then its grouped GEMV
+            rq = np.zeros((M, qw.kpad), np.int8)
+            rs = np.zeros(M, np.float32)
+            assert oracle.orc_prep_rows(P(x), K, None, M, K, 128, norm, P(rq), qw.kpad, P(rs), None, 0) == 0
+            fy = np.zeros((M, N), np.float32)
+            oracle.orc_ternary_gemv_grouped(P(w), P(s), g, P(rq), qw.kpad, P(rs), None, P(fy), N, M, N, K)
             ref = None
             for rt, ks, e in [(0, 0, 0), (1, 0, 0), (4, 0, 0), (1, 2, 0), (4, 2, 0), (1, 16, 0), (4, 4, 0), (1, 1, 0),
                               (0, 0, 8), (1, 0, 16), (4, 0, 8), (1, 4, 16)]:
@@ -140,6 +147,7 @@ def test_gemv_shape_knobs(gpu, oracle, N, K, g):
                 yf = yf.cpu().numpy()
                 if ref is None:
                     ref = yf
+                    assert np.array_equal(yf.view(np.uint32), fy.view(np.uint32)), M
                 assert np.array_equal(yf.view(np.uint32), ref.view(np.uint32)), (M, rt, ks, e)
     finally:
         lib.eif_hip_set_gemv_row_tiles(0)
