@@ -1872,13 +1872,14 @@ int launch_gemv_tiles(const QArgs &a, const PrepArgs &p, int rows_pad, int rt, h
     // (each step combines 8-16 rows' groups; at 8 rows QKV 3840x2560 4.1 us against 4.5 with 2 steps a wave,
     // O 3.9 against 4.2)
     if (GROUPED && !p.x && g_gemv_ksplit <= 0 && (a.nsteps >= 24 || a.M >= 8)) ks = a.nsteps < 24 ? a.nsteps : 10;
-    // the one-shape group layouts (g32, g64, g256) at one prepped token row: SMAX - 2 steps a wave. Their single
-    // launch shape holds SMAX steps in registers and loads all of them, a wave's last step again past its own, so
-    // fewer waves with fuller registers load less (6912x2560 g64 5.7 us against 9.3 at 2 steps a wave, g32 8.0
-    // against 8.9; 2560x6912 g32 9.9 against 10.5, g64 6.6 either way; g256 keeps 2 steps a wave, its best)
+    // the one-shape group layouts (g32, g64, g256) on prepped rows, one token tile: SMAX - 2 steps a wave. Their
+    // single launch shape holds SMAX steps in registers and loads all of them, a wave's last step again past its
+    // own, so fewer waves with fuller registers load less (6912x2560 g64 at 1 / 8 rows 5.7 / 7.0 us against 9.3 /
+    // 12.3, g32 8.0 / 9.7 against 8.9 / 10.5; 2560x6912 g32 at 16 rows 21.7 against 23.9, g256 at 8 rows 6.9
+    // against 7.8; g64 there and g256 at 6912x2560 within 0.1 us either way)
     if constexpr (GROUPED && !gemv_tuned<FMT, UD, GROUPED>()) {
         constexpr int SMAX = Geo<FMT, UD>::SB >= 32 ? 4 : 8;   // launch_gemv_e's steps per wave
-        if (!p.x && a.M == 1 && g_gemv_ksplit <= 0) ks = eif_ceil_div(a.nsteps, std::max(2, SMAX - 2));
+        if (!p.x && a.M <= kGemvTileM && g_gemv_ksplit <= 0) ks = eif_ceil_div(a.nsteps, std::max(2, SMAX - 2));
     }
     if (!GROUPED && !p.x && rows_pad / 16 >= kBigTiles && g_gemv_ksplit <= 0) {
         // row-scaled, many tiles, prepped activations: about 10 KiB of weights per wave

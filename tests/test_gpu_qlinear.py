@@ -52,9 +52,12 @@ TERN_GROUPED = [
     (130, 200, 32, 3, GEMV),        # ragged rows and columns
     (70, 640, 64, 5, GEMV),
     (64, 512, 256, 2, GEMV),
-    (6912, 2560, 64, 1, GEMV),      # the one-shape layouts at one row: SMAX - 2 steps a wave
+    (6912, 2560, 64, 1, GEMV),      # the one-shape layouts up to 16 rows: SMAX - 2 steps a wave
     (1000, 6912, 32, 1, GEMV),
     (300, 2560, 256, 1, GEMV),
+    (700, 2560, 64, 8, GEMV),
+    (500, 6912, 32, 16, GEMV),
+    (300, 6912, 256, 5, GEMV),
     (6912, 2560, 128, 16, GEMV),    # 9 .. 63 tokens: the GEMV in token chunks
     (3840, 2560, 128, 32, GEMV),
     (2560, 6912, 96, 16, GEMV),     # g96 down: one 16-row token tile per workgroup (int16 group sums in LDS)
