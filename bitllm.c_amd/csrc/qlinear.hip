@@ -2231,7 +2231,8 @@ int resolve_path(const eif_hip_qweight *w, int path, int M)
     if (M <= kGemvTileM || w->rows_pad < kGemvFewRows) return EIF_HIP_PATH_GEMV;
     if (M > 2 * kGemvTileM) return EIF_HIP_PATH_GEMM;
     const bool big = tiles >= kBigTiles ||
-                     (w->fmt == kI8 ? w->rows_pad >= kGemvI8Rows || w->nsteps >= kGemvI8Steps : tiles >= kGemvI4Tiles);
+                     (w->fmt == kI8 && (w->rows_pad >= kGemvI8Rows || w->nsteps >= kGemvI8Steps)) ||
+                     (w->fmt == kI4 && tiles >= kGemvI4Tiles);
     return big ? EIF_HIP_PATH_GEMV : EIF_HIP_PATH_GEMM;
 }
 
